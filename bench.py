@@ -1,0 +1,306 @@
+#!/usr/bin/env python3
+"""bench.py — decode KV-attention + KV append on one MI355X.
+
+Workload (BASELINE.json config 1 at ctx 4096): the Qwen3-0.6B layer shape
+(16 query heads, 8 KV heads, head_dim 128, F32). One step is one decode token
+through all 28 layers: per layer, one fused launch that appends the new K/V
+row at position ctx and attends over ctx+1 cached keys. The 28 layer caches
+(28 x 32 MiB = 897 MiB) are distinct, so the working set is more than twice
+the 256 MB Infinity Cache and the figure is HBM bandwidth, not MALL bandwidth.
+The 28 launches of a step are captured once in a HIP graph and replayed.
+
+Algorithmic bytes per launch (Qwen3-0.6B):  8192*L + 32768
+    K and V history 2*4096*L, new k,v read 8192, new rows written 8192,
+    q read 8192, output written 8192.
+value = total algorithmic bytes / timed wall time (GB/s); roofline.achieved =
+the same bytes / mean launch duration; peak = 8 TB/s.
+
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
+Prints ONE JSON line on stdout; progress goes to stderr.
+"""
+import argparse
+import json
+import os
+import pathlib
+import statistics
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path[:0] = [str(ROOT / "infer-llm_amd"), str(ROOT / "oracle")]
+
+METRIC = "decode KV-attn GB/s (% HBM peak) @ctx 4096; TPOT ms Qwen3-0.6B F32"
+HBM_PEAK_GBS = 8000.0
+FP32_MFMA_PEAK_TFLOPS = 157.3
+N_HEAD, N_HEAD_KV, D, N_LAYER = 16, 8, 128, 28
+TRAFFIC_FILE = ROOT / "profiles" / "decode_append_ctx4096_traffic.json"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def decode_bytes(ctx, n_head=N_HEAD, n_head_kv=N_HEAD_KV, d=D):
+    row = n_head_kv * d * 4
+    return 2 * row * ctx + 2 * row + 2 * row + 2 * n_head * d * 4
+
+
+def prefill_flops(p, n_head=N_HEAD, d=D):
+    # unmasked (query, key) pairs x (QK^T + PV) = n_head * P(P+1)/2 * 4d
+    return n_head * (p * (p + 1) // 2) * 4 * d
+
+
+class DecodeRig:
+    """28 layers of KV cache at one context length, launched through the C-ABI."""
+
+    def __init__(self, torch, ikv, ctx, n_layer=N_LAYER, seed=0x1F0000 + 1000 + 2):
+        self.torch, self.ikv, self.ctx, self.n_layer = torch, ikv, ctx, n_layer
+        dev = torch.device("cuda:0")
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+        self.layers = []
+        for _ in range(n_layer):
+            kc = torch.empty((ctx + 1, N_HEAD_KV, D), device=dev)
+            vc = torch.empty((ctx + 1, N_HEAD_KV, D), device=dev)
+            kc.normal_(generator=g)
+            vc.normal_(generator=g)
+            self.layers.append(dict(
+                kc=kc, vc=vc,
+                q=torch.randn((N_HEAD, D), generator=g, device=dev),
+                kn=torch.randn((N_HEAD_KV, D), generator=g, device=dev),
+                vn=torch.randn((N_HEAD_KV, D), generator=g, device=dev),
+                out=torch.empty((N_HEAD, D), device=dev)))
+        self.ws = ikv.decode_workspace(N_HEAD, N_HEAD_KV, D, ctx + 1, device=dev)
+        self.ws_bytes = self.ws.numel() * 4
+        self.lib = ikv.load()
+        self.graph = None
+
+    def step(self):
+        s = self.torch.cuda.current_stream().cuda_stream
+        f = self.lib.ikv_attn_decode_f32
+        n_kv = self.ctx + 1
+        for L in self.layers:
+            rc = f(L["q"].data_ptr(), L["kc"].data_ptr(), L["vc"].data_ptr(), L["kn"].data_ptr(),
+                   L["vn"].data_ptr(), L["out"].data_ptr(), N_HEAD, N_HEAD_KV, D, n_kv, 0.0,
+                   self.ws.data_ptr(), self.ws_bytes, s)
+            if rc != 0:
+                raise RuntimeError(f"ikv_attn_decode_f32 returned {rc}")
+
+    def capture(self):
+        torch = self.torch
+        self.step()  # eager reference for the graph check
+        torch.cuda.synchronize()
+        ref = [L["out"].clone() for L in self.layers]
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            self.step()  # warm the capture stream
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.step()
+        self.graph = g
+        for _ in range(3):  # every replay must match the eager step bit for bit
+            for L in self.layers:
+                L["out"].zero_()
+            g.replay()
+            torch.cuda.synchronize()
+            for L, r in zip(self.layers, ref):
+                if not torch.equal(L["out"], r):
+                    raise RuntimeError("graph replay differs from the eager step")
+
+    def run(self, n):
+        for _ in range(n):
+            if self.graph is not None:
+                self.graph.replay()
+            else:
+                self.step()
+
+    def time(self, steps, warmup):
+        torch = self.torch
+        self.run(warmup)
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        self.run(steps)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / 1e3  # seconds
+
+
+def time_prefill(torch, ikv, p, reps):
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(0x1F0000 + 2000 + p)
+    q = torch.randn((p, N_HEAD, D), generator=g, device=dev)
+    k = torch.randn((p, N_HEAD_KV, D), generator=g, device=dev)
+    v = torch.randn((p, N_HEAD_KV, D), generator=g, device=dev)
+    out = torch.empty_like(q)
+    for _ in range(3):
+        ikv.attn_prefill(q, k, v, 0, out=out)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        ikv.attn_prefill(q, k, v, 0, out=out)
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / 1e3 / reps
+
+
+def cpu_baseline(ctx, seconds):
+    """The oracle (restated reference CPU backend) on this host: the same
+    decode step (append + attention) of one layer, rotated over 8 layers."""
+    import numpy as np
+
+    import oracle
+    from ikv import synth
+
+    workers = min(oracle.default_workers(), 15)
+    threads = oracle.set_workers(workers)
+    layers = []
+    for i in range(8):
+        kc = synth.normal(synth.config_seed(1, 100 + i), ((ctx + 1), N_HEAD_KV, D))
+        vc = synth.normal(synth.config_seed(1, 200 + i), ((ctx + 1), N_HEAD_KV, D))
+        layers.append((kc, vc))
+    q = synth.normal(synth.config_seed(1, 300), (N_HEAD, D))
+    kn = synth.normal(synth.config_seed(1, 301), (N_HEAD_KV, D))
+    vn = synth.normal(synth.config_seed(1, 302), (N_HEAD_KV, D))
+    oracle.decode_append_attn(q, kn, vn, *layers[0], ctx)  # warm
+    n, t0 = 0, time.perf_counter()
+    while True:
+        kc, vc = layers[n % len(layers)]
+        oracle.decode_append_attn(q, kn, vn, kc, vc, ctx)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return {
+        "value": round(decode_bytes(ctx) * n / el / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{n} decode steps (append + GQA attention, 1 layer, ctx {ctx}) rotated over "
+                  f"8 layer caches, {el:.1f} s; {workers} pool workers + calling thread "
+                  f"(reference ThreadPool convention), host nproc {os.cpu_count()}",
+        "ms_per_layer": round(el / n * 1e3, 3),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--ctx", type=int, default=4096)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the ctx sweep and prefill")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the hot path has no "
+              "multi-GPU leg in this build", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import ikv
+
+    torch.cuda.set_device(0)
+    ikv.load()
+    log(f"[bench] {ikv.version()} on {torch.cuda.get_device_name(0)}")
+
+    rig = DecodeRig(torch, ikv, args.ctx)
+    rig.capture()
+    log(f"[bench] graph captured ({N_LAYER} launches per step), replays match eager")
+    secs = rig.time(args.steps, args.warmup)
+    launches = args.steps * N_LAYER
+    per_launch = secs / launches
+    bpl = decode_bytes(args.ctx)
+    value = bpl * launches / secs / 1e9
+    achieved = bpl / per_launch / 1e9
+    log(f"[bench] ctx {args.ctx}: {secs / args.steps * 1e3:.3f} ms/step, "
+        f"{per_launch * 1e6:.2f} us/launch, {value:.1f} GB/s")
+
+    traffic = None
+    if TRAFFIC_FILE.exists():
+        t = json.loads(TRAFFIC_FILE.read_text())
+        if t.get("ctx") == args.ctx:
+            traffic = t.get("hbm_bytes_per_launch")
+
+    extra = {"eager_gbs": None, "ctx_sweep_gbs": {}, "mall_hot_gbs": None, "prefill": {}}
+    if not args.no_extra:
+        rig.graph = None
+        es = rig.time(max(args.steps // 2, 5), 2)
+        extra["eager_gbs"] = round(bpl * max(args.steps // 2, 5) * N_LAYER / es / 1e9, 1)
+        del rig
+        torch.cuda.empty_cache()
+        for ctx in (256, 1024, 4096, 16384, 32768):
+            r = DecodeRig(torch, ikv, ctx)
+            r.capture()
+            n = max(5, min(50, int(2e4 // max(ctx // 64, 1))))
+            s = r.time(n, 3)
+            extra["ctx_sweep_gbs"][str(ctx)] = round(decode_bytes(ctx) * n * N_LAYER / s / 1e9, 1)
+            log(f"[bench] sweep ctx {ctx}: {extra['ctx_sweep_gbs'][str(ctx)]} GB/s")
+            del r
+            torch.cuda.empty_cache()
+        hot = DecodeRig(torch, ikv, args.ctx, n_layer=1)
+        hot.layers = hot.layers * N_LAYER  # the same cache 28 times: MALL-resident
+        hot.capture()
+        s = hot.time(20, 3)
+        extra["mall_hot_gbs"] = round(bpl * 20 * N_LAYER / s / 1e9, 1)
+        del hot
+        for p in (32, 64, 128, 256, 2048):
+            t = time_prefill(torch, ikv, p, 20 if p < 2048 else 10)
+            tf = prefill_flops(p) / t / 1e12
+            extra["prefill"][str(p)] = {"us": round(t * 1e6, 2), "tflops": round(tf, 2),
+                                        "mfma_frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)}
+            log(f"[bench] prefill P={p}: {t * 1e6:.1f} us, {tf:.2f} TFLOP/s")
+
+    cpu = None
+    if not args.no_cpu:
+        log(f"[bench] cpu baseline ({args.cpu_seconds:.0f} s)...")
+        cpu = cpu_baseline(args.ctx, args.cpu_seconds)
+        log(f"[bench] cpu baseline {cpu['value']} GB/s on {cpu['cores']} threads")
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(secs / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: K,V,q,k_new,v_new ~ N(0,1) F32 (torch.randn, fixed seed)",
+        "config": {
+            "workload": "decode attention + fused KV append, Qwen3-0.6B layer shape "
+                        f"(16 q heads, 8 KV heads, head_dim 128), n_past {args.ctx}, one step = "
+                        f"{N_LAYER} layers with distinct caches ({N_LAYER} x "
+                        f"{2 * (args.ctx + 1) * 4096 / 2**20:.0f} MiB), HIP-graph replay",
+            "ctx": args.ctx, "layers": N_LAYER, "n_head": N_HEAD, "n_head_kv": N_HEAD_KV,
+            "head_dim": D, "bytes_per_launch": bpl,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "launch_us": round(per_launch * 1e6, 3),
+        },
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,136 @@
+/*
+ * ikv.h — C-ABI of the MI355X (gfx950) KV-cache hot path.
+ *
+ * This is the layer the HIP backend's dispatch calls, in the place where the
+ * reference's CUDA backend calls CUDA_F32::compute_* (reference
+ * include/kernels/cuda/kernel_f32.hpp:5-29, dispatched from
+ * src/backends/cuda_backend.cpp:208-241). Arguments are plain pointers and
+ * sizes; no C++ or torch types cross it.
+ *
+ * Layouts are the reference Tensor layouts (include/tensor.hpp:12-29,
+ * dims[0] innermost), all contiguous F32:
+ *   q, out      [n_q][n_head][head_dim]
+ *   k, v caches [n_kv][n_head_kv][head_dim]   (token stride n_head_kv*head_dim)
+ *   theta/sin/cos tables [n_ctx][head_dim/2]
+ *
+ * Conventions:
+ *   - Device pointers unless a name ends in _host.
+ *   - stream is a hipStream_t passed as void*; NULL means the null stream.
+ *   - No entry point allocates, frees or synchronises. Work is enqueued on
+ *     `stream` and errors inside kernels never fault the device.
+ *   - Return value: 0 on success; a negative errno (-EINVAL, -ENOTSUP,
+ *     -EOVERFLOW) when arguments are rejected before any launch; a positive
+ *     hipError_t when a launch fails. The HIP backend maps negative codes to
+ *     std::errc and positive ones to std::errc::io_error, as check_cuda does
+ *     (reference include/cuda_util.hpp:7-16).
+ */
+#ifndef IKV_H
+#define IKV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Version string of the library, e.g. "ikv 0.1 gfx950". */
+const char *ikv_version(void);
+
+/* ---------------------------------------------------------------------
+ * KV append.
+ * Replaces CUDA_F32::compute_cpy (src/kernels/cuda/kernel_f32.cu:305-319) and
+ * CPUBackend::compute_cpy (src/backends/cpu_backend.cpp:705-742): copies
+ * n_rows * row_bytes contiguous bytes from src_rows to dst_rows (the writable
+ * cache view [n_past, n_past+n_new)). Byte-exact; nothing else is written.
+ * ------------------------------------------------------------------- */
+int ikv_append_f32(void *dst_rows, const void *src_rows, size_t n_rows, size_t row_bytes,
+                   void *stream);
+
+/* ---------------------------------------------------------------------
+ * Decode attention, one query token, GQA, split-K over the context, with an
+ * optional fused KV append.
+ * Replaces compute_flash_attn for n_q == 1 (src/kernels/cuda/kernel_f32.cu:
+ * 452-511; CPU semantics src/backends/cpu_backend.cpp:525-634).
+ *
+ *   q        [n_head][head_dim]
+ *   k_cache, v_cache  readable cache views, [n_kv][n_head_kv][head_dim]
+ *   k_new, v_new      NULL, or the new token's rows [n_head_kv][head_dim].
+ *            When given, row n_kv-1 of the caches is read from them and is
+ *            also written to the caches (the append of ModelBase::append_kv,
+ *            src/model.cpp:602-625, fused into the attention launch).
+ *   out      [n_head][head_dim]
+ *   scale    softmax scale; <= 0 selects 1/sqrtf(head_dim)
+ *   workspace  device memory of ikv_attn_decode_workspace_bytes() bytes,
+ *            zero-filled before its first use; every completed launch
+ *            leaves it ready for the next. Launches that share one
+ *            workspace must be ordered (same stream); concurrent ones race.
+ * head_dim must be 128; n_head/n_head_kv must be 1, 2, 4 or 8.
+ * ------------------------------------------------------------------- */
+size_t ikv_attn_decode_workspace_bytes(int n_head, int n_head_kv, int head_dim, int64_t n_kv);
+
+int ikv_attn_decode_f32(const float *q, float *k_cache, float *v_cache, const float *k_new,
+                        const float *v_new, float *out, int n_head, int n_head_kv, int head_dim,
+                        int64_t n_kv, float scale, void *workspace, size_t workspace_bytes,
+                        void *stream);
+
+/* ---------------------------------------------------------------------
+ * Prefill / general attention, n_q >= 1 query tokens, causal: key j is
+ * visible to query t iff j <= n_past + t (src/backends/cpu_backend.cpp:578,
+ * src/kernels/cuda/kernel_f32.cu:346). F32 MFMA tiles; K/V tiles staged in
+ * LDS and shared by the n_head/n_head_kv query heads of a KV head.
+ * Replaces compute_flash_attn for n_q > 1. Needs no workspace.
+ * head_dim must be 128; n_head/n_head_kv must be 1, 2, 4 or 8.
+ * ------------------------------------------------------------------- */
+int ikv_attn_prefill_f32(const float *q, const float *k, const float *v, float *out, int n_head,
+                         int n_head_kv, int head_dim, int64_t n_q, int64_t n_kv, int64_t n_past,
+                         float scale, void *stream);
+
+/* ---------------------------------------------------------------------
+ * RMS norm over rows of `dim` floats: out = (x * s) * w with
+ * s = float(1 / sqrt(sum_d double(x_d*x_d) / dim + eps)), the sum taken in
+ * double in index order — the arithmetic of CPUBackend::compute_rms_norm
+ * (src/backends/cpu_backend.cpp:335-382), so results are bit-identical to it.
+ * Replaces CUDA_F32::compute_rms_norm (src/kernels/cuda/kernel_f32.cu:16-90).
+ * ------------------------------------------------------------------- */
+int ikv_rms_norm_f32(const float *x, const float *w, float *out, int64_t rows, int64_t dim,
+                     float eps, void *stream);
+
+/* ---------------------------------------------------------------------
+ * Host helper: sin/cos tables from a RoPE angle table (host memory).
+ * sin_host[i] = sinf(theta_host[i]), cos_host[i] = cosf(theta_host[i]) —
+ * the per-step computation of src/backends/cpu_backend.cpp:472-487, done
+ * once so that the device tables can stay resident in HBM.
+ * ------------------------------------------------------------------- */
+int ikv_rope_sincos_table_f32(const float *theta_host, size_t count, float *sin_host,
+                              float *cos_host);
+
+/* ---------------------------------------------------------------------
+ * RoPE, NeoX half split: for pair (j, j+head_dim/2) of every head of token t
+ * at position p = pos[t]:  o_j = x0*c - x1*s,  o_{j+h} = x0*s + x1*c  with
+ * c = cos_tab[p][j], s = sin_tab[p][j]  (src/backends/cpu_backend.cpp:
+ * 443-523). Replaces CUDA_F32::compute_rope (src/kernels/cuda/kernel_f32.cu:
+ * 242-301). A position outside [0, n_ctx) does not fault: its rows are
+ * written as zeros and *status (if non-NULL, device int) is set to 1.
+ * x may equal out.
+ * ------------------------------------------------------------------- */
+int ikv_rope_neox_f32(const float *x, float *out, const int32_t *pos, int64_t n_tokens,
+                      int n_heads, int head_dim, const float *sin_tab, const float *cos_tab,
+                      int64_t n_ctx, int *status, void *stream);
+
+/* ---------------------------------------------------------------------
+ * Fused qk-RMSNorm + RoPE: ikv_rms_norm_f32 over each head row with weight
+ * w[head_dim], then ikv_rope_neox_f32, in one launch. Bit-identical to the
+ * two ops in sequence (the RMSNorm -> RoPE order of Qwen3Model::build_graph,
+ * src/models/Qwen3.cpp:66-71).
+ * ------------------------------------------------------------------- */
+int ikv_qk_norm_rope_f32(const float *x, const float *w, float *out, const int32_t *pos,
+                         int64_t n_tokens, int n_heads, int head_dim, float eps,
+                         const float *sin_tab, const float *cos_tab, int64_t n_ctx, int *status,
+                         void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* IKV_H */

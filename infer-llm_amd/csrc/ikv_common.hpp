@@ -1,0 +1,65 @@
+// ikv_common.hpp — helpers shared by the gfx950 kernels and their C-ABI
+// wrappers. Written for CDNA4 only: 64-lane wavefronts, 32-lane half-wave
+// reductions, float4 (16-byte) global accesses.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cerrno>
+#include <cmath>
+#include <cstddef>
+#include <cstdint>
+
+namespace ikv {
+
+constexpr int kWave = 64;
+
+// Return code of an entry point after its launches: 0, or the hipError_t of
+// the failed launch (positive, as documented in ikv.h).
+inline int launch_status() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? 0 : static_cast<int>(e);
+}
+
+inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Sum over the 32 lanes of a half-wave; every lane of the half gets the sum.
+__device__ __forceinline__ float half_wave_sum(float v) {
+  v += __shfl_xor(v, 16, 32);
+  v += __shfl_xor(v, 8, 32);
+  v += __shfl_xor(v, 4, 32);
+  v += __shfl_xor(v, 2, 32);
+  v += __shfl_xor(v, 1, 32);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// 2^x on the hardware exp unit. Inputs below the float range give +0, and
+// -inf gives 0, which is what masked softmax terms need.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float dot4(const float4 a, const float4 b) {
+  return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
+}
+
+__device__ __forceinline__ float4 fma4(float s, const float4 v, const float4 acc) {
+  return make_float4(fmaf(s, v.x, acc.x), fmaf(s, v.y, acc.y), fmaf(s, v.z, acc.z),
+                     fmaf(s, v.w, acc.w));
+}
+
+__device__ __forceinline__ float4 scale4(float s, const float4 v) {
+  return make_float4(s * v.x, s * v.y, s * v.z, s * v.w);
+}
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+}  // namespace ikv

@@ -1,0 +1,270 @@
+"""ikv — Python bindings for the MI355X KV-cache hot path.
+
+Thin ctypes layer over the C-ABI declared in ``include/ikv.h`` and built into
+``infer-llm_amd/lib/libikv.so``. PyTorch is used only as plumbing: device
+buffers and the current HIP stream. Every call goes to the HIP kernels; there
+is no CPU fallback, and loading fails loudly when the library is missing.
+
+Return codes follow ikv.h: 0 ok, negative errno for rejected arguments,
+positive hipError_t for a failed launch. Non-zero codes raise ``IkvError``.
+"""
+from __future__ import annotations
+
+import ctypes
+import errno
+import os
+import pathlib
+import re
+from typing import Optional
+
+PKG_ROOT = pathlib.Path(__file__).resolve().parents[1]  # infer-llm_amd/
+REPO_ROOT = PKG_ROOT.parent
+LIB_PATH = PKG_ROOT / "lib" / "libikv.so"
+HEADER_PATH = REPO_ROOT / "include" / "ikv.h"
+
+_c_void_p = ctypes.c_void_p
+_c_size_t = ctypes.c_size_t
+_c_int = ctypes.c_int
+_c_int64 = ctypes.c_int64
+_c_float = ctypes.c_float
+
+# name -> (restype, argtypes); kept in the order of include/ikv.h
+SIGNATURES = {
+    "ikv_version": (ctypes.c_char_p, []),
+    "ikv_append_f32": (_c_int, [_c_void_p, _c_void_p, _c_size_t, _c_size_t, _c_void_p]),
+    "ikv_attn_decode_workspace_bytes": (_c_size_t, [_c_int, _c_int, _c_int, _c_int64]),
+    "ikv_attn_decode_f32": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+         _c_int, _c_int, _c_int, _c_int64, _c_float, _c_void_p, _c_size_t, _c_void_p],
+    ),
+    "ikv_attn_prefill_f32": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int,
+         _c_int64, _c_int64, _c_int64, _c_float, _c_void_p],
+    ),
+    "ikv_rms_norm_f32": (
+        _c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int64, _c_int64, _c_float, _c_void_p]),
+    "ikv_rope_sincos_table_f32": (_c_int, [_c_void_p, _c_size_t, _c_void_p, _c_void_p]),
+    "ikv_rope_neox_f32": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_int64, _c_int, _c_int, _c_void_p, _c_void_p,
+         _c_int64, _c_void_p, _c_void_p],
+    ),
+    "ikv_qk_norm_rope_f32": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int64, _c_int, _c_int, _c_float,
+         _c_void_p, _c_void_p, _c_int64, _c_void_p, _c_void_p],
+    ),
+}
+
+
+class IkvError(RuntimeError):
+    """A C-ABI entry point returned a non-zero code."""
+
+    def __init__(self, fn: str, rc: int):
+        self.fn, self.rc = fn, rc
+        if rc < 0:
+            what = errno.errorcode.get(-rc, str(-rc))
+            super().__init__(f"{fn} rejected its arguments: -{what}")
+        else:
+            super().__init__(f"{fn} launch failed: hipError_t {rc}")
+
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def header_functions() -> list[str]:
+    """Names of the entry points declared in include/ikv.h."""
+    text = HEADER_PATH.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ikv_[a-z0-9_]+)\s*\(", text)))
+
+
+def load() -> ctypes.CDLL:
+    """Load libikv.so (once). Raises if the library has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise FileNotFoundError(
+            f"{LIB_PATH} is not built; run `python -c 'import __graft_entry__ as g; g.build()'`")
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def _check(fn: str, rc: int) -> None:
+    if rc != 0:
+        raise IkvError(fn, rc)
+
+
+# ----------------------------------------------------------------------------
+# torch plumbing
+# ----------------------------------------------------------------------------
+
+def _torch():
+    import torch  # imported lazily so CPU-only users of the ABI need no torch
+    return torch
+
+
+def _ptr(t) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(stream=None) -> int:
+    torch = _torch()
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return stream.cuda_stream
+
+
+def _need_f32_dev(name: str, t) -> None:
+    torch = _torch()
+    if t.dtype != torch.float32:
+        raise TypeError(f"{name} must be float32, got {t.dtype}")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+# ----------------------------------------------------------------------------
+# entry points
+# ----------------------------------------------------------------------------
+
+def version() -> str:
+    return load().ikv_version().decode()
+
+
+def append(dst_rows, src_rows, stream=None) -> None:
+    """KV append: copy src_rows into dst_rows (both contiguous device tensors of
+    equal byte size; dst_rows is the writable cache view)."""
+    _need_f32_dev("dst_rows", dst_rows)
+    _need_f32_dev("src_rows", src_rows)
+    if dst_rows.numel() != src_rows.numel():
+        raise ValueError("append: size mismatch")
+    n_rows = src_rows.shape[0] if src_rows.dim() > 0 else 1
+    row_bytes = src_rows.numel() * 4 // max(n_rows, 1)
+    _check("ikv_append_f32",
+           load().ikv_append_f32(_ptr(dst_rows), _ptr(src_rows), n_rows, row_bytes, _stream(stream)))
+
+
+def decode_workspace_bytes(n_head: int, n_head_kv: int, head_dim: int, n_kv: int) -> int:
+    return int(load().ikv_attn_decode_workspace_bytes(n_head, n_head_kv, head_dim, n_kv))
+
+
+def decode_workspace(n_head: int, n_head_kv: int, head_dim: int, n_kv: int, device="cuda"):
+    """Zero-filled workspace for attn_decode (reusable across ordered launches)."""
+    torch = _torch()
+    nbytes = max(decode_workspace_bytes(n_head, n_head_kv, head_dim, n_kv), 256)
+    return torch.zeros((nbytes + 3) // 4, dtype=torch.float32, device=device)
+
+
+def attn_decode(q, k_cache, v_cache, n_kv: int, *, k_new=None, v_new=None, out=None,
+                scale: float = 0.0, workspace=None, stream=None):
+    """Decode attention for one query token over cache rows [0, n_kv).
+
+    q: [n_head, D]; k_cache/v_cache: [capacity, n_head_kv, D]; when k_new/v_new
+    ([n_head_kv, D]) are given, row n_kv-1 is taken from them and appended."""
+    torch = _torch()
+    for name, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache)):
+        _need_f32_dev(name, t)
+    n_head, D = q.shape[-2], q.shape[-1]
+    n_head_kv = k_cache.shape[-2]
+    if k_cache.shape[0] < n_kv or v_cache.shape[0] < n_kv:
+        raise ValueError("cache shorter than n_kv")
+    if (k_new is None) != (v_new is None):
+        raise ValueError("k_new and v_new go together")
+    if k_new is not None:
+        _need_f32_dev("k_new", k_new)
+        _need_f32_dev("v_new", v_new)
+        if k_new.numel() != n_head_kv * D or v_new.numel() != n_head_kv * D:
+            raise ValueError("k_new/v_new must hold one token row")
+    if out is None:
+        out = torch.empty((n_head, D), dtype=torch.float32, device=q.device)
+    _need_f32_dev("out", out)
+    if workspace is None:
+        workspace = decode_workspace(n_head, n_head_kv, D, n_kv, device=q.device)
+    rc = load().ikv_attn_decode_f32(
+        _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(k_new), _ptr(v_new), _ptr(out),
+        n_head, n_head_kv, D, n_kv, scale, _ptr(workspace), workspace.numel() * 4, _stream(stream))
+    _check("ikv_attn_decode_f32", rc)
+    return out
+
+
+def attn_prefill(q, k, v, n_past: int = 0, *, n_kv: Optional[int] = None, out=None,
+                 scale: float = 0.0, stream=None):
+    """Causal attention for q [n_q, n_head, D] over k, v [>= n_kv, n_head_kv, D]."""
+    torch = _torch()
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        _need_f32_dev(name, t)
+    n_q, n_head, D = q.shape
+    n_head_kv = k.shape[1]
+    if n_kv is None:
+        n_kv = n_past + n_q
+    if out is None:
+        out = torch.empty_like(q)
+    _need_f32_dev("out", out)
+    rc = load().ikv_attn_prefill_f32(_ptr(q), _ptr(k), _ptr(v), _ptr(out), n_head, n_head_kv, D,
+                                     n_q, n_kv, n_past, scale, _stream(stream))
+    _check("ikv_attn_prefill_f32", rc)
+    return out
+
+
+def rms_norm(x, w, eps: float, out=None, stream=None):
+    torch = _torch()
+    _need_f32_dev("x", x)
+    _need_f32_dev("w", w)
+    dim = x.shape[-1]
+    if w.numel() != dim:
+        raise ValueError("weight length must equal the last dim")
+    if out is None:
+        out = torch.empty_like(x)
+    rows = x.numel() // dim
+    _check("ikv_rms_norm_f32",
+           load().ikv_rms_norm_f32(_ptr(x), _ptr(w), _ptr(out), rows, dim, eps, _stream(stream)))
+    return out
+
+
+def rope_sincos_table(theta):
+    """Host sin/cos tables (numpy float32) from a host angle table."""
+    import numpy as np
+    theta = np.ascontiguousarray(theta, dtype=np.float32)
+    s = np.empty_like(theta)
+    c = np.empty_like(theta)
+    _check("ikv_rope_sincos_table_f32",
+           load().ikv_rope_sincos_table_f32(theta.ctypes.data, theta.size, s.ctypes.data,
+                                            c.ctypes.data))
+    return s, c
+
+
+def rope_neox(x, pos, sin_tab, cos_tab, out=None, status=None, stream=None):
+    """x: [n_tokens, n_heads, D]; pos: int32 [n_tokens]; tables [n_ctx, D/2]."""
+    torch = _torch()
+    _need_f32_dev("x", x)
+    n_tokens, n_heads, D = x.shape
+    if out is None:
+        out = torch.empty_like(x)
+    rc = load().ikv_rope_neox_f32(_ptr(x), _ptr(out), _ptr(pos), n_tokens, n_heads, D,
+                                  _ptr(sin_tab), _ptr(cos_tab), sin_tab.shape[0], _ptr(status),
+                                  _stream(stream))
+    _check("ikv_rope_neox_f32", rc)
+    return out
+
+
+def qk_norm_rope(x, w, pos, eps: float, sin_tab, cos_tab, out=None, status=None, stream=None):
+    torch = _torch()
+    _need_f32_dev("x", x)
+    n_tokens, n_heads, D = x.shape
+    if out is None:
+        out = torch.empty_like(x)
+    rc = load().ikv_qk_norm_rope_f32(_ptr(x), _ptr(w), _ptr(out), _ptr(pos), n_tokens, n_heads, D,
+                                     eps, _ptr(sin_tab), _ptr(cos_tab), sin_tab.shape[0],
+                                     _ptr(status), _stream(stream))
+    _check("ikv_qk_norm_rope_f32", rc)
+    return out

@@ -1,0 +1,99 @@
+"""The C-ABI library on the CPU: it loads, exports every entry point that
+include/ikv.h declares, and rejects bad arguments before touching a device.
+No kernel is launched here."""
+import ctypes
+import errno
+import subprocess
+
+import numpy as np
+import pytest
+
+import ikv
+import oracle
+
+
+def test_library_loads_and_reports_version():
+    assert ikv.version().startswith("ikv ")
+
+
+def test_every_declared_entry_point_is_exported():
+    declared = ikv.header_functions()
+    assert declared, "no declarations parsed from include/ikv.h"
+    lib = ikv.load()
+    for name in declared:
+        assert hasattr(lib, name), name
+    exported = subprocess.run(["nm", "-D", "--defined-only", str(ikv.LIB_PATH)],
+                              capture_output=True, text=True, check=True).stdout
+    names = {line.split()[-1] for line in exported.splitlines() if line.strip()}
+    assert set(declared) <= names
+    assert set(ikv.SIGNATURES) == set(declared)
+
+
+def test_library_does_not_link_the_oracle():
+    deps = subprocess.run(["ldd", str(ikv.LIB_PATH)], capture_output=True, text=True).stdout
+    assert "oracle" not in deps
+    syms = subprocess.run(["nm", "-D", str(ikv.LIB_PATH)], capture_output=True, text=True).stdout
+    assert "oracle_" not in syms
+
+
+def _rc(name, *args):
+    return getattr(ikv.load(), name)(*args)
+
+
+def test_decode_rejects_bad_arguments_without_launching():
+    P = 64  # fake 16-byte aligned non-null "device" address; never dereferenced
+    ok = dict(n_head=16, n_head_kv=8, head_dim=128, n_kv=100)
+
+    def call(q=P, k=P, v=P, kn=None, vn=None, out=P, n_head=16, n_head_kv=8, head_dim=128,
+             n_kv=100, ws=None, wsb=0):
+        return _rc("ikv_attn_decode_f32", q, k, v, kn, vn, out, n_head, n_head_kv, head_dim, n_kv,
+                   0.0, ws, wsb, None)
+
+    assert call(q=None) == -errno.EINVAL
+    assert call(kn=P) == -errno.EINVAL                 # k_new without v_new
+    assert call(n_head=12) == -errno.EINVAL            # not a multiple of n_head_kv
+    assert call(n_kv=0) == -errno.EINVAL
+    assert call(head_dim=64) == -errno.ENOTSUP
+    assert call(n_head=24) == -errno.ENOTSUP           # group of 3
+    assert call(q=P + 4) == -errno.EINVAL              # misaligned
+    assert call(n_kv=4097) == -errno.EINVAL            # split-K needs a workspace
+    need = ikv.decode_workspace_bytes(ok["n_head"], ok["n_head_kv"], 128, 4097)
+    assert call(n_kv=4097, ws=P, wsb=need - 4) == -errno.EINVAL
+
+
+def test_prefill_and_rows_reject_bad_arguments():
+    P = 64
+    assert _rc("ikv_attn_prefill_f32", P, P, P, P, 16, 8, 128, 0, 10, 0, 0.0, None) == 0  # n_q=0
+    assert _rc("ikv_attn_prefill_f32", None, P, P, P, 16, 8, 128, 4, 10, 0, 0.0, None) == -errno.EINVAL
+    assert _rc("ikv_attn_prefill_f32", P, P, P, P, 16, 8, 96, 4, 10, 0, 0.0, None) == -errno.ENOTSUP
+    assert _rc("ikv_rms_norm_f32", None, P, P, 4, 128, 1e-6, None) == -errno.EINVAL
+    assert _rc("ikv_rms_norm_f32", P, P, P, 0, 128, 1e-6, None) == 0
+    assert _rc("ikv_rope_neox_f32", P, P, P, 2, 8, 127, P, P, 10, None, None) == -errno.EINVAL
+    assert _rc("ikv_qk_norm_rope_f32", P, None, P, P, 2, 8, 128, 1e-6, P, P, 10, None, None) == -errno.EINVAL
+    assert _rc("ikv_append_f32", None, P, 1, 4096, None) == -errno.EINVAL
+    assert _rc("ikv_append_f32", P, P, 0, 4096, None) == 0
+    assert _rc("ikv_append_f32", P, P, 2**62, 2**8, None) == -errno.EOVERFLOW
+
+
+def test_workspace_bytes_grow_with_context_and_are_bounded():
+    sizes = [ikv.decode_workspace_bytes(16, 8, 128, n) for n in (1, 256, 4097, 32769, 10**6)]
+    assert all(s > 0 for s in sizes)
+    assert sizes == sorted(sizes)
+    assert sizes[-1] <= 16 * 512 * (128 + 2) * 4 + 4096  # at most 512 splits per head
+    assert ikv.decode_workspace_bytes(16, 8, 64, 100) == 0
+
+
+def test_sincos_table_is_bitwise_glibc():
+    """The host table must hold exactly the cosf/sinf values the reference CPU
+    rope uses. The oracle's rope of unit vectors exposes them bitwise:
+    e_j -> (cos, sin) at (j, j+64), since 1*c - 0*s == c exactly."""
+    th = oracle.rope_theta_table(1e6, 128, 40960)
+    pos = np.array([0, 1, 2, 1000, 4096, 32768, 40959], np.int32)
+    s, c = ikv.rope_sincos_table(th[pos])
+    x = np.zeros((len(pos), 64, 128), np.float32)
+    x[:, np.arange(64), np.arange(64)] = 1.0
+    r = oracle.rope_neox(x, pos, th)
+    cos_ref = r[:, np.arange(64), np.arange(64)]
+    sin_ref = r[:, np.arange(64), np.arange(64) + 64]
+    assert np.array_equal(c.view(np.uint32), cos_ref.view(np.uint32))
+    assert np.array_equal(s.view(np.uint32), sin_ref.view(np.uint32))

@@ -1,0 +1,299 @@
+"""Parity of the gfx950 kernels (through the C-ABI) with the CPU oracle.
+
+Bars (from the path's contract):
+  * KV append and cache contents: bit-exact; bytes outside the appended rows
+    untouched (checked against sentinel-filled caches).
+  * RMSNorm, RoPE, fused qk-norm+RoPE: bit-exact with the oracle.
+  * Attention outputs: |hip - oracle| <= 1e-5 + 1e-4 * |oracle| elementwise.
+"""
+import ctypes
+import pathlib
+
+import numpy as np
+import pytest
+import torch
+
+import ikv
+import oracle
+from ikv import synth
+
+pytestmark = pytest.mark.gpu
+
+D = 128
+RTOL, ATOL = 1e-4, 1e-5
+GOLDEN = pathlib.Path(__file__).resolve().parent / "golden" / "hotpath_small.npz"
+SENT_K = np.float32(-1234.5)
+SENT_V = np.float32(4321.25)
+
+
+def assert_attn_close(got, want, what=""):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    err = np.abs(got - want)
+    bound = ATOL + RTOL * np.abs(want)
+    worst = float(np.max(err - bound))
+    assert np.all(err <= bound), f"{what}: max excess {worst:.3e}, max abs err {err.max():.3e}"
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def rand(gen, shape, std=1.0):
+    return torch.randn(shape, generator=gen, device="cuda", dtype=torch.float32) * std
+
+
+def gen(seed):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    return g
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _setup(dev, oracle_pool):
+    ikv.load()
+    yield
+
+
+# ---------------------------------------------------------------------------
+# KV append
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("n_rows,n_past", [(1, 0), (1, 4096), (32, 7), (2048, 0), (5, 100)])
+def test_append_is_bit_exact_and_touches_nothing_else(dev, n_rows, n_past):
+    cap = n_past + n_rows + 3
+    cache = torch.full((cap, 8, D), float(SENT_K), device=dev)
+    src = rand(gen(1 + n_rows), (n_rows, 8, D))
+    ikv.append(cache[n_past:n_past + n_rows], src)
+    torch.cuda.synchronize()
+    c = cache.cpu().numpy()
+    assert np.array_equal(bits(c[n_past:n_past + n_rows]), bits(src.cpu().numpy()))
+    assert np.all(c[:n_past] == SENT_K) and np.all(c[n_past + n_rows:] == SENT_K)
+
+
+def test_append_unaligned_bytes(dev):
+    buf = torch.zeros(4 * 1024, dtype=torch.uint8, device=dev)
+    src = torch.arange(3 * 1001, dtype=torch.int32, device=dev).to(torch.uint8)
+    lib = ikv.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    rc = lib.ikv_append_f32(buf.data_ptr() + 3, src.data_ptr(), 3, 1001, stream)
+    assert rc == 0
+    torch.cuda.synchronize()
+    b = buf.cpu().numpy()
+    assert np.array_equal(b[3:3 + 3003], src.cpu().numpy())
+    assert not b[:3].any() and not b[3 + 3003:].any()
+
+
+# ---------------------------------------------------------------------------
+# decode attention with fused append
+# ---------------------------------------------------------------------------
+
+def run_decode_case(dev, ctx, Hq=16, Hkv=8, seed=0, fused=True):
+    cap = ctx + 4
+    g = gen(1000 + seed * 7 + ctx)
+    k_cache = torch.full((cap, Hkv, D), float(SENT_K), device=dev)
+    v_cache = torch.full((cap, Hkv, D), float(SENT_V), device=dev)
+    k_cache[:ctx] = rand(g, (ctx, Hkv, D))
+    v_cache[:ctx] = rand(g, (ctx, Hkv, D))
+    q = rand(g, (Hq, D))
+    kn = rand(g, (Hkv, D))
+    vn = rand(g, (Hkv, D))
+    k_host = k_cache.cpu().numpy()
+    v_host = v_cache.cpu().numpy()
+    want = oracle.decode_append_attn(q.cpu().numpy(), kn.cpu().numpy(), vn.cpu().numpy(),
+                                     k_host, v_host, ctx)
+    if fused:
+        out = ikv.attn_decode(q, k_cache, v_cache, ctx + 1, k_new=kn, v_new=vn)
+    else:
+        ikv.append(k_cache[ctx:ctx + 1], kn[None])
+        ikv.append(v_cache[ctx:ctx + 1], vn[None])
+        out = ikv.attn_decode(q, k_cache, v_cache, ctx + 1)
+    torch.cuda.synchronize()
+    return out.cpu().numpy(), want, k_cache.cpu().numpy(), v_cache.cpu().numpy(), k_host, v_host
+
+
+@pytest.mark.parametrize("ctx", [0, 1, 2, 31, 32, 33, 255, 256, 1024, 4096, 16384, 32768])
+def test_decode_fused_append_qwen3_06b(dev, ctx):
+    out, want, kc, vc, k_ref, v_ref = run_decode_case(dev, ctx)
+    assert_attn_close(out, want, f"ctx={ctx}")
+    # cache bit-exact: history + appended row, sentinels beyond
+    assert np.array_equal(bits(kc), bits(k_ref)) and np.array_equal(bits(vc), bits(v_ref))
+    assert np.all(kc[ctx + 1:] == SENT_K) and np.all(vc[ctx + 1:] == SENT_V)
+
+
+@pytest.mark.parametrize("Hq,Hkv,ctx", [(8, 8, 1000), (16, 8, 5000), (32, 8, 4096), (32, 8, 777),
+                                        (64, 8, 3000), (16, 4, 2049), (8, 1, 600)])
+def test_decode_group_sizes(dev, Hq, Hkv, ctx):
+    out, want, kc, vc, k_ref, v_ref = run_decode_case(dev, ctx, Hq, Hkv, seed=3)
+    assert_attn_close(out, want, f"Hq={Hq} Hkv={Hkv} ctx={ctx}")
+    assert np.array_equal(bits(kc), bits(k_ref)) and np.array_equal(bits(vc), bits(v_ref))
+
+
+def test_decode_unfused_equals_fused(dev):
+    a = run_decode_case(dev, 3000, seed=5, fused=True)
+    b = run_decode_case(dev, 3000, seed=5, fused=False)
+    assert np.array_equal(bits(a[0]), bits(b[0]))
+    assert np.array_equal(bits(a[2]), bits(b[2])) and np.array_equal(bits(a[3]), bits(b[3]))
+
+
+def test_decode_workspace_reuse_is_deterministic(dev):
+    g = gen(77)
+    k = rand(g, (8200, 8, D))
+    v = rand(g, (8200, 8, D))
+    q = rand(g, (16, D))
+    ws = ikv.decode_workspace(16, 8, D, 8200)
+    a = ikv.attn_decode(q, k, v, 8200, workspace=ws).clone()
+    small = ikv.attn_decode(q, k, v, 1500, workspace=ws).clone()
+    b = ikv.attn_decode(q, k, v, 8200, workspace=ws).clone()
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(a.cpu().numpy()), bits(b.cpu().numpy()))
+    kh, vh = k.cpu().numpy(), v.cpu().numpy()
+    want = oracle.flash_attn(q.cpu().numpy()[None], kh[:1500], vh[:1500], 1499)[0]
+    assert_attn_close(small.cpu().numpy(), want, "ctx 1500 after 8200")
+
+
+# ---------------------------------------------------------------------------
+# prefill attention (MFMA)
+# ---------------------------------------------------------------------------
+
+def run_prefill_case(dev, n_q, n_past, Hq=16, Hkv=8, seed=0):
+    n_kv = n_past + n_q
+    g = gen(5000 + seed * 13 + n_q * 3 + n_past)
+    q = rand(g, (n_q, Hq, D))
+    k = rand(g, (n_kv, Hkv, D))
+    v = rand(g, (n_kv, Hkv, D))
+    out = ikv.attn_prefill(q, k, v, n_past)
+    torch.cuda.synchronize()
+    want = oracle.flash_attn(q.cpu().numpy(), k.cpu().numpy(), v.cpu().numpy(), n_past)
+    return out.cpu().numpy(), want
+
+
+@pytest.mark.parametrize("P", [1, 2, 31, 32, 33, 64, 65, 128, 256, 2048])
+def test_prefill_causal_qwen3_06b(dev, P):
+    out, want = run_prefill_case(dev, P, 0)
+    assert_attn_close(out, want, f"P={P}")
+
+
+@pytest.mark.parametrize("n_q,n_past", [(17, 100), (64, 1000), (3, 4093), (128, 128)])
+def test_prefill_with_history(dev, n_q, n_past):
+    out, want = run_prefill_case(dev, n_q, n_past, seed=2)
+    assert_attn_close(out, want, f"n_q={n_q} n_past={n_past}")
+
+
+@pytest.mark.parametrize("Hq,Hkv,P", [(8, 8, 200), (32, 8, 300), (64, 8, 100), (8, 1, 150)])
+def test_prefill_group_sizes(dev, Hq, Hkv, P):
+    out, want = run_prefill_case(dev, P, 0, Hq, Hkv, seed=4)
+    assert_attn_close(out, want, f"Hq={Hq} Hkv={Hkv} P={P}")
+
+
+def test_prefill_first_row_is_first_value(dev):
+    g = gen(9)
+    q = rand(g, (40, 16, D))
+    k = rand(g, (40, 8, D))
+    v = rand(g, (40, 8, D))
+    out = ikv.attn_prefill(q, k, v, 0)
+    torch.cuda.synchronize()
+    want = np.repeat(v[0].cpu().numpy(), 2, axis=0)
+    assert_attn_close(out[0].cpu().numpy(), want, "row 0")
+
+
+def test_decode_steps_equal_prefill_rows_on_gpu(dev):
+    """Cached decode == recompute on the device: append + decode token by
+    token reproduces the causal prefill rows."""
+    P = 300
+    g = gen(11)
+    q = rand(g, (P, 16, D))
+    k = rand(g, (P, 8, D))
+    v = rand(g, (P, 8, D))
+    full = ikv.attn_prefill(q, k, v, 0).cpu().numpy()
+    kc = torch.zeros((P, 8, D), device=dev)
+    vc = torch.zeros((P, 8, D), device=dev)
+    ws = ikv.decode_workspace(16, 8, D, P)
+    rows = []
+    for t in range(P):
+        rows.append(ikv.attn_decode(q[t], kc, vc, t + 1, k_new=k[t], v_new=v[t], workspace=ws).clone())
+    torch.cuda.synchronize()
+    dec = torch.stack(rows).cpu().numpy()
+    assert np.array_equal(bits(kc.cpu().numpy()), bits(k.cpu().numpy()))
+    want = oracle.flash_attn(q.cpu().numpy(), k.cpu().numpy(), v.cpu().numpy(), 0)
+    assert_attn_close(dec, want, "decode steps")
+    assert_attn_close(full, want, "prefill")
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm / RoPE (bit-exact)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("rows,dim", [(1, 128), (24, 128), (65, 128), (49152, 128), (3, 1024), (7, 100)])
+def test_rms_norm_bit_exact(dev, rows, dim):
+    x = synth.normal(100 + rows, (rows, dim), std=3.0)
+    w = synth.normal(200 + dim, (dim,))
+    got = ikv.rms_norm(torch.from_numpy(x).to(dev), torch.from_numpy(w).to(dev), 1e-6)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(got.cpu().numpy()), bits(oracle.rms_norm(x, w, 1e-6)))
+
+
+def sincos_dev(dev, n_ctx=40960):
+    th = oracle.rope_theta_table(1e6, D, n_ctx)
+    s, c = ikv.rope_sincos_table(th)
+    return th, torch.from_numpy(s).to(dev), torch.from_numpy(c).to(dev)
+
+
+@pytest.mark.parametrize("n_tokens,n_heads", [(1, 16), (1, 8), (7, 16), (2048, 8)])
+def test_rope_bit_exact(dev, n_tokens, n_heads):
+    th, s, c = sincos_dev(dev)
+    x = synth.normal(300 + n_tokens, (n_tokens, n_heads, D))
+    pos = synth.uniform_ints(301 + n_tokens, n_tokens, 40960)
+    pos[0] = 0
+    got = ikv.rope_neox(torch.from_numpy(x).to(dev), torch.from_numpy(pos).to(dev), s, c)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(got.cpu().numpy()), bits(oracle.rope_neox(x, pos, th)))
+
+
+@pytest.mark.parametrize("n_tokens,n_heads", [(1, 16), (1, 8), (32, 16), (2048, 16)])
+def test_qk_norm_rope_bit_exact(dev, n_tokens, n_heads):
+    th, s, c = sincos_dev(dev)
+    x = synth.normal(400 + n_tokens, (n_tokens, n_heads, D), std=2.0)
+    w = synth.normal(401, (D,))
+    pos = (np.arange(n_tokens) + 4000).astype(np.int32)
+    xd = torch.from_numpy(x).to(dev)
+    got = ikv.qk_norm_rope(xd, torch.from_numpy(w).to(dev), torch.from_numpy(pos).to(dev), 1e-6, s, c)
+    inplace = xd.clone()
+    ikv.qk_norm_rope(inplace, torch.from_numpy(w).to(dev), torch.from_numpy(pos).to(dev), 1e-6, s, c,
+                     out=inplace)
+    torch.cuda.synchronize()
+    want = oracle.rope_neox(oracle.rms_norm(x, w, 1e-6), pos, th)
+    assert np.array_equal(bits(got.cpu().numpy()), bits(want))
+    assert np.array_equal(bits(inplace.cpu().numpy()), bits(want))
+
+
+def test_rope_bad_position_sets_status_without_fault(dev):
+    th, s, c = sincos_dev(dev, 64)
+    x = torch.ones((3, 8, D), device=dev)
+    pos = torch.tensor([1, 64, 2], dtype=torch.int32, device=dev)
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = ikv.rope_neox(x, pos, s, c, status=status)
+    torch.cuda.synchronize()
+    assert int(status.item()) == 1
+    o = out.cpu().numpy()
+    assert np.all(o[1] == 0) and np.all(o[0] != 0)
+
+
+# ---------------------------------------------------------------------------
+# committed fixtures
+# ---------------------------------------------------------------------------
+
+def test_golden_fixtures(dev):
+    with np.load(GOLDEN, allow_pickle=False) as f:
+        g = {k: f[k] for k in f.files}
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    got = ikv.rms_norm(t(g["rms_x"]), t(g["rms_w"]), 1e-6).cpu().numpy()
+    assert np.array_equal(bits(got), bits(g["rms_out"]))
+    _, s, c = sincos_dev(dev, 4096)
+    got = ikv.rope_neox(t(g["rms_out"]), t(g["rope_pos"]), s, c).cpu().numpy()
+    assert np.array_equal(bits(got), bits(g["rope_out"]))
+    kc, vc = t(g["dec_k"]).clone(), t(g["dec_v"]).clone()
+    got = ikv.attn_decode(t(g["dec_q"][0]), kc, vc, 17).cpu().numpy()
+    assert_attn_close(got, g["dec_out"][0], "golden decode")
+    got = ikv.attn_prefill(t(g["pre_q"]), t(g["pre_k"]), t(g["pre_v"]), 0).cpu().numpy()
+    assert_attn_close(got, g["pre_out"], "golden prefill")
