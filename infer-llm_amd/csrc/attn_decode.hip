@@ -8,23 +8,33 @@
 // CPUBackend::compute_flash_attn (src/backends/cpu_backend.cpp:525-634):
 // q head h reads KV head h / (n_head / n_head_kv); softmax(q.k * scale) . v.
 //
-// Work decomposition (gfx950, 256 CUs in 8 XCDs):
-//   * One workgroup = 4 wavefronts = one (KV head g, context split s).
-//     blockIdx = s * n_head_kv + g, so with 8 KV heads every split of head g
-//     is dispatched to XCD g and shares that XCD's L2.
-//   * Within a workgroup each half-wave (32 lanes x float4) owns one 512-byte
-//     K or V row at a time: loads are fully coalesced 16-byte accesses along
-//     the token-major cache ([token][kv head][128] F32, 4096 B per token at
-//     Qwen3 shapes). Each K/V row is read from HBM exactly once and serves all
-//     G query heads of the group.
-//   * Online softmax (base-2, running max / sum) per half-wave, merged across
-//     half-waves by a lane exchange and across the 4 waves through LDS.
-//   * Split partials (max, sum, unnormalised output) go to the workspace; the
-//     last workgroup of each KV head to finish (device-scope counter) merges
-//     them and writes the output, then resets its counter for the next launch.
-//   * Fused append: the row of the new token (n_kv-1) is read from k_new/v_new
-//     instead of the cache, and the workgroup that owns it stores it into the
-//     cache unchanged (a 16-byte copy, bit-exact).
+// Two launches, no device-scope fences or atomics:
+//   split kernel  one workgroup (4 wavefronts) per (KV head g, context split).
+//                 blockIdx = split * n_head_kv + g, so with 8 KV heads every
+//                 split of head g lands on XCD g. Each half-wave (32 lanes x
+//                 float4) owns one 512-byte K or V row at a time: coalesced
+//                 16-byte non-temporal loads along the token-major cache
+//                 ([token][kv head][128] F32, 4096 B per token at Qwen3
+//                 shapes), every row read from HBM once and used by all G
+//                 query heads of the group. The next R rows per lane are
+//                 prefetched into registers while the current ones are
+//                 scored. Online softmax in base 2 per half-wave, merged
+//                 across half-waves by lane exchange and across waves through
+//                 LDS. With one split the output is written directly;
+//                 otherwise (max, sum, unnormalised output) per split goes to
+//                 the workspace.
+//   merge kernel  four workgroups per query head rescale and sum the split
+//                 partials in one memory round trip.
+// Why a second launch: the kernel boundary makes the partials of all 8 XCDs
+// visible. Merging inside the split kernel ("last workgroup to arrive merges")
+// was measured on MI355X and is slower than the extra launch at every context
+// length: agent-scope release/acquire fences write back / invalidate the
+// XCD's L2 (buffer_wbl2 / buffer_inv), and device-scope atomics on one
+// counter serialise at about 0.14 us per arriving workgroup, while a kernel
+// boundary in a HIP graph costs about 1.6 us.
+// Fused append: the row of the new token (n_kv-1) is read from k_new/v_new
+// instead of the cache, and the workgroup that owns it stores it into the
+// cache unchanged (a 16-byte copy, bit-exact).
 #include "ikv_common.hpp"
 #include "../../include/ikv.h"
 
@@ -35,13 +45,19 @@ namespace {
 constexpr int D = 128;         // head_dim supported by this kernel
 constexpr int NWAVE = 4;       // wavefronts per workgroup
 constexpr int WG = NWAVE * 64;
-constexpr int R = 4;           // K and V rows held per lane per iteration
+#ifndef IKV_DECODE_R
+#define IKV_DECODE_R 4
+#endif
+constexpr int R = IKV_DECODE_R;      // K and V rows per lane per iteration
 constexpr int TILE = NWAVE * 2 * R;  // tokens per workgroup iteration
-constexpr int kMaxSplits = 512;
+constexpr int kMaxSplits = 1024;
 
 #ifndef IKV_DECODE_TARGET_WGS
-// About two workgroups per CU on MI355X (256 CUs).
-#define IKV_DECODE_TARGET_WGS 512
+// Split-kernel workgroups aimed for: four per CU on MI355X (256 CUs).
+#define IKV_DECODE_TARGET_WGS 1024
+#endif
+#ifndef IKV_DECODE_NT
+#define IKV_DECODE_NT 1  // 1: K/V history read with non-temporal (streaming) loads
 #endif
 
 struct Plan {
@@ -50,11 +66,14 @@ struct Plan {
 };
 
 Plan plan_for(int n_head_kv, int64_t n_kv) {
+  // Whole tiles per split, as few per split as the target allows: at ctx 4096
+  // (129 tiles per head) every split is one tile and all workgroups are
+  // resident at once. Splits stay below 2*target <= kMaxSplits.
   int64_t target = (IKV_DECODE_TARGET_WGS + n_head_kv - 1) / n_head_kv;
   if (target < 1) target = 1;
-  if (target > kMaxSplits) target = kMaxSplits;
+  if (target > kMaxSplits / 2) target = kMaxSplits / 2;
   const int64_t n_tiles = (n_kv + TILE - 1) / TILE;
-  int64_t tiles_per_split = (n_tiles + target - 1) / target;
+  int64_t tiles_per_split = n_tiles / target;
   if (tiles_per_split < 1) tiles_per_split = 1;
   const int64_t tokens = tiles_per_split * TILE;
   const int64_t splits = (n_kv + tokens - 1) / tokens;
@@ -64,30 +83,76 @@ Plan plan_for(int n_head_kv, int64_t n_kv) {
 size_t align256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
 
 struct WsLayout {
-  size_t counters, part_ml, part_o, total;
+  size_t part_ml, part_o, total;
 };
 
-WsLayout ws_layout(int n_head, int n_head_kv, int n_splits) {
+// [n_head x n_splits x (max, sum)][n_head x n_splits x D]
+WsLayout ws_layout(int n_head, int n_splits) {
   WsLayout w;
-  w.counters = 0;
-  w.part_ml = align256(sizeof(unsigned) * static_cast<size_t>(n_head_kv));
-  w.part_o = w.part_ml + align256(sizeof(float) * 2 * static_cast<size_t>(n_head) * n_splits);
+  w.part_ml = 0;
+  w.part_o = align256(sizeof(float) * 2 * static_cast<size_t>(n_head) * n_splits);
   w.total = w.part_o + sizeof(float) * static_cast<size_t>(n_head) * n_splits * D;
   return w;
 }
 
 template <int G>
-__global__ __launch_bounds__(WG) void decode_kernel(
+__device__ __forceinline__ void load_rows(float4 (&kr)[R], float4 (&vr)[R], int base, int t_end,
+                                          int wave, int half, int new_row, const float *kc,
+                                          const float *vc, const float *k_new, const float *v_new,
+                                          size_t tok_stride, size_t head_off) {
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int t = base + r * (NWAVE * 2) + wave * 2 + half;
+    if (t < t_end) {
+      const bool fresh = (t == new_row);
+      const float *kp = fresh ? k_new + head_off : kc + static_cast<size_t>(t) * tok_stride + head_off;
+      const float *vp = fresh ? v_new + head_off : vc + static_cast<size_t>(t) * tok_stride + head_off;
+#if IKV_DECODE_NT
+      typedef float f4v __attribute__((ext_vector_type(4)));
+      const f4v a = __builtin_nontemporal_load(reinterpret_cast<const f4v *>(kp));
+      const f4v b = __builtin_nontemporal_load(reinterpret_cast<const f4v *>(vp));
+      kr[r] = make_float4(a.x, a.y, a.z, a.w);
+      vr[r] = make_float4(b.x, b.y, b.z, b.w);
+#else
+      kr[r] = *reinterpret_cast<const float4 *>(kp);
+      vr[r] = *reinterpret_cast<const float4 *>(vp);
+#endif
+    } else {
+      kr[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+      vr[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+}
+
+// Combines the online-softmax states of the 4 waves (in LDS) for query head
+// h of the group, dim d: unnormalised output O, sum L, max M.
+template <int G>
+__device__ __forceinline__ void merge_waves(const float (&s_acc)[NWAVE][G][D],
+                                            const float (&s_m)[NWAVE][G],
+                                            const float (&s_l)[NWAVE][G], int h, int d, float &O,
+                                            float &L, float &M) {
+  M = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < NWAVE; ++w) M = fmaxf(M, s_m[w][h]);
+  O = 0.f;
+  L = 0.f;
+#pragma unroll
+  for (int w = 0; w < NWAVE; ++w) {
+    const float mw = s_m[w][h];
+    const float e = (mw == -INFINITY) ? 0.f : ikv::fast_exp2(mw - M);
+    O += s_acc[w][h][d] * e;
+    L += s_l[w][h] * e;
+  }
+}
+
+template <int G>
+__global__ __launch_bounds__(WG) void decode_split_kernel(
     const float *__restrict__ q, float *kc, float *vc, const float *k_new, const float *v_new,
-    float *__restrict__ out, unsigned *__restrict__ counters, float *__restrict__ part_ml,
-    float *__restrict__ part_o, int n_head_kv, int n_kv, int tokens_per_split, int n_splits,
-    float scale_log2) {
+    float *__restrict__ out, float *__restrict__ part_ml, float *__restrict__ part_o,
+    int n_head_kv, int n_kv, int tokens_per_split, int n_splits, float scale_log2) {
   __shared__ float s_acc[NWAVE][G][D];
   __shared__ float s_m[NWAVE][G];
   __shared__ float s_l[NWAVE][G];
-  __shared__ float s_w[G][kMaxSplits];
-  __shared__ float s_inv[G];
-  __shared__ unsigned s_last;
 
   const int g = blockIdx.x % n_head_kv;
   const int split = blockIdx.x / n_head_kv;
@@ -101,6 +166,10 @@ __global__ __launch_bounds__(WG) void decode_kernel(
   const int new_row = k_new ? n_kv - 1 : -1;
   const size_t tok_stride = static_cast<size_t>(n_head_kv) * D;
   const size_t head_off = static_cast<size_t>(g) * D + 4 * sub;
+
+  float4 kr[R], vr[R];
+  load_rows<G>(kr, vr, t_begin, t_end, wave, half, new_row, kc, vc, k_new, v_new, tok_stride,
+               head_off);
 
   float4 qv[G];
 #pragma unroll
@@ -117,28 +186,17 @@ __global__ __launch_bounds__(WG) void decode_kernel(
   }
 
   for (int base = t_begin; base < t_end; base += TILE) {
-    float4 kr[R], vr[R];
-    int tok[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) tok[r] = base + r * (NWAVE * 2) + wave * 2 + half;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int t = tok[r];
-      if (t < t_end) {
-        const bool fresh = (t == new_row);
-        const float *kp = fresh ? k_new + head_off : kc + static_cast<size_t>(t) * tok_stride + head_off;
-        const float *vp = fresh ? v_new + head_off : vc + static_cast<size_t>(t) * tok_stride + head_off;
-        kr[r] = *reinterpret_cast<const float4 *>(kp);
-        vr[r] = *reinterpret_cast<const float4 *>(vp);
-      } else {
-        kr[r] = make_float4(0.f, 0.f, 0.f, 0.f);
-        vr[r] = make_float4(0.f, 0.f, 0.f, 0.f);
-      }
-    }
+    float4 kn[R], vn[R];
+    const bool more = base + TILE < t_end;
+    if (more)
+      load_rows<G>(kn, vn, base + TILE, t_end, wave, half, new_row, kc, vc, k_new, v_new,
+                   tok_stride, head_off);
+
     if (new_row >= base && new_row < base + TILE) {
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        if (tok[r] == new_row && tok[r] < t_end) {
+        const int t = base + r * (NWAVE * 2) + wave * 2 + half;
+        if (t == new_row) {
           const size_t off = static_cast<size_t>(new_row) * tok_stride + head_off;
           *reinterpret_cast<float4 *>(kc + off) = kr[r];
           *reinterpret_cast<float4 *>(vc + off) = vr[r];
@@ -150,8 +208,9 @@ __global__ __launch_bounds__(WG) void decode_kernel(
       float sc[R];
 #pragma unroll
       for (int r = 0; r < R; ++r) {
+        const int t = base + r * (NWAVE * 2) + wave * 2 + half;
         const float d = ikv::half_wave_sum(ikv::dot4(qv[h], kr[r]));
-        sc[r] = (tok[r] < t_end) ? d * scale_log2 : -INFINITY;
+        sc[r] = (t < t_end) ? d * scale_log2 : -INFINITY;
       }
       float mx = m[h];
 #pragma unroll
@@ -167,6 +226,13 @@ __global__ __launch_bounds__(WG) void decode_kernel(
           acc[h] = ikv::fma4(p, vr[r], acc[h]);
         }
         m[h] = mx;
+      }
+    }
+    if (more) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        kr[r] = kn[r];
+        vr[r] = vn[r];
       }
     }
   }
@@ -201,89 +267,135 @@ __global__ __launch_bounds__(WG) void decode_kernel(
   }
   __syncthreads();
 
-  // Merge the 4 waves: thread (h, d).
+  // Merge the 4 waves. With one split the result is final.
+  if (n_splits == 1) {
+    for (int idx = tid; idx < G * D; idx += WG) {
+      const int h = idx / D;
+      const int d = idx - h * D;
+      float O, L, M;
+      merge_waves<G>(s_acc, s_m, s_l, h, d, O, L, M);
+      out[static_cast<size_t>(g * G + h) * D + d] = O / L;
+    }
+    return;
+  }
   for (int idx = tid; idx < G * D; idx += WG) {
     const int h = idx / D;
     const int d = idx - h * D;
-    float M = -INFINITY;
+    float O, L, M;
+    merge_waves<G>(s_acc, s_m, s_l, h, d, O, L, M);
+    const size_t slot = static_cast<size_t>(g * G + h) * n_splits + split;
+    part_o[slot * D + d] = O;
+    if (d == 0) {
+      part_ml[2 * slot] = M;
+      part_ml[2 * slot + 1] = L;
+    }
+  }
+}
+
+// Merge of the split partials: 4 workgroups per query head, each owning 32
+// dims. Thread (grp, dd) of 8 x 32 sums splits grp, grp+8, ... for dim dd.
+// All partial loads of a chunk of 256 splits are issued before any is used,
+// so a chunk costs one memory round trip.
+constexpr int kMergeThreads = 256;
+constexpr int kMergeDims = 32;
+constexpr int kMergeGroups = kMergeThreads / kMergeDims;  // 8
+constexpr int kMergeChunk = 256;                          // splits per round trip
+constexpr int kMergeJ = kMergeChunk / kMergeGroups;       // 32 loads per thread
+
+__global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
+    const float *__restrict__ part_ml, const float *__restrict__ part_o, float *__restrict__ out,
+    int n_splits) {
+  __shared__ float s_w[kMaxSplits];
+  __shared__ float s_red[kMergeGroups][kMergeDims];
+  __shared__ float s_stat[4];
+  const int qh = blockIdx.x / (D / kMergeDims);
+  const int d0 = (blockIdx.x % (D / kMergeDims)) * kMergeDims;
+  const int tid = threadIdx.x;
+  const int grp = tid / kMergeDims;
+  const int dd = tid % kMergeDims;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const float *ml = part_ml + static_cast<size_t>(qh) * n_splits * 2;
+  const float *po = part_o + static_cast<size_t>(qh) * n_splits * D + d0 + dd;
+
+  float v[kMergeJ];
 #pragma unroll
-    for (int w = 0; w < NWAVE; ++w) M = fmaxf(M, s_m[w][h]);
-    float O = 0.f, L = 0.f;
+  for (int j = 0; j < kMergeJ; ++j) {
+    const int s = grp + kMergeGroups * j;
+    v[j] = (s < n_splits) ? po[static_cast<size_t>(s) * D] : 0.f;
+  }
+  // Split statistics, one (max, sum) pair per split, loaded together with the
+  // partials above: weights 2^(m - M) and the weighted sum of l.
+  float2 st[kMergeChunk / kMergeThreads];
 #pragma unroll
-    for (int w = 0; w < NWAVE; ++w) {
-      const float mw = s_m[w][h];
-      const float e = (mw == -INFINITY) ? 0.f : ikv::fast_exp2(mw - M);
-      O += s_acc[w][h][d] * e;
-      L += s_l[w][h] * e;
-    }
-    const int qh = g * G + h;
-    if (n_splits == 1) {
-      out[static_cast<size_t>(qh) * D + d] = O / L;
-    } else {
-      const size_t slot = static_cast<size_t>(qh) * n_splits + split;
-      part_o[slot * D + d] = O;
-      if (d == 0) {
-        part_ml[2 * slot] = M;
-        part_ml[2 * slot + 1] = L;
-      }
-    }
+  for (int k = 0; k < kMergeChunk / kMergeThreads; ++k) {
+    const int i = tid + k * kMergeThreads;
+    st[k] = (i < n_splits) ? reinterpret_cast<const float2 *>(ml)[i] : make_float2(-INFINITY, 0.f);
   }
-  if (n_splits == 1) return;
-
-  // Last workgroup of this KV head merges the split partials.
-  __threadfence();
+  float mloc = -INFINITY;
+  for (int i = tid + kMergeChunk; i < n_splits; i += kMergeThreads) mloc = fmaxf(mloc, ml[2 * i]);
+#pragma unroll
+  for (int k = 0; k < kMergeChunk / kMergeThreads; ++k) mloc = fmaxf(mloc, st[k].x);
+  mloc = ikv::wave_max(mloc);
+  if (lane == 0) s_stat[wave] = mloc;
   __syncthreads();
-  if (tid == 0) {
-    const unsigned prev = atomicAdd(&counters[g], 1u);
-    s_last = (prev == static_cast<unsigned>(n_splits) - 1u) ? 1u : 0u;
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-
-  for (int h = wave; h < G; h += NWAVE) {
-    const float *ml = part_ml + static_cast<size_t>(g * G + h) * n_splits * 2;
-    float mx = -INFINITY;
-    for (int i = lane; i < n_splits; i += 64) mx = fmaxf(mx, ml[2 * i]);
-    mx = ikv::wave_max(mx);
-    float sum = 0.f;
-    for (int i = lane; i < n_splits; i += 64) {
-      const float w = ikv::fast_exp2(ml[2 * i] - mx);
-      s_w[h][i] = w;
-      sum += ml[2 * i + 1] * w;
+  const float M = fmaxf(fmaxf(s_stat[0], s_stat[1]), fmaxf(s_stat[2], s_stat[3]));
+  float lsum = 0.f;
+#pragma unroll
+  for (int k = 0; k < kMergeChunk / kMergeThreads; ++k) {
+    const int i = tid + k * kMergeThreads;
+    if (i < n_splits) {
+      const float w = ikv::fast_exp2(st[k].x - M);
+      s_w[i] = w;
+      lsum += st[k].y * w;
     }
-    sum = ikv::wave_sum(sum);
-    if (lane == 0) s_inv[h] = 1.0f / sum;
   }
+  for (int i = tid + kMergeChunk; i < n_splits; i += kMergeThreads) {
+    const float w = ikv::fast_exp2(ml[2 * i] - M);
+    s_w[i] = w;
+    lsum += ml[2 * i + 1] * w;
+  }
+  lsum = ikv::wave_sum(lsum);
   __syncthreads();
+  if (lane == 0) s_stat[wave] = lsum;
+  __syncthreads();
+  const float inv = 1.0f / ((s_stat[0] + s_stat[1]) + (s_stat[2] + s_stat[3]));
 
-  for (int idx = tid; idx < G * D; idx += WG) {
-    const int h = idx / D;
-    const int d = idx - h * D;
-    const int qh = g * G + h;
-    const float *po = part_o + static_cast<size_t>(qh) * n_splits * D + d;
-    float O0 = 0.f, O1 = 0.f, O2 = 0.f, O3 = 0.f;
-    int i = 0;
-    for (; i + 4 <= n_splits; i += 4) {
-      O0 += po[static_cast<size_t>(i) * D] * s_w[h][i];
-      O1 += po[static_cast<size_t>(i + 1) * D] * s_w[h][i + 1];
-      O2 += po[static_cast<size_t>(i + 2) * D] * s_w[h][i + 2];
-      O3 += po[static_cast<size_t>(i + 3) * D] * s_w[h][i + 3];
-    }
-    for (; i < n_splits; ++i) O0 += po[static_cast<size_t>(i) * D] * s_w[h][i];
-    out[static_cast<size_t>(qh) * D + d] = ((O0 + O1) + (O2 + O3)) * s_inv[h];
+  float acc = 0.f;
+#pragma unroll
+  for (int j = 0; j < kMergeJ; ++j) {
+    const int s = grp + kMergeGroups * j;
+    if (s < n_splits) acc += v[j] * s_w[s];
   }
-  if (tid == 0) atomicExch(&counters[g], 0u);
+  for (int base = kMergeChunk; base < n_splits; base += kMergeChunk) {
+#pragma unroll
+    for (int j = 0; j < kMergeJ; ++j) {
+      const int s = base + grp + kMergeGroups * j;
+      v[j] = (s < n_splits) ? po[static_cast<size_t>(s) * D] : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < kMergeJ; ++j) {
+      const int s = base + grp + kMergeGroups * j;
+      if (s < n_splits) acc += v[j] * s_w[s];
+    }
+  }
+  s_red[grp][dd] = acc;
+  __syncthreads();
+  if (grp == 0) {
+    float o = 0.f;
+#pragma unroll
+    for (int k = 0; k < kMergeGroups; ++k) o += s_red[k][dd];
+    out[static_cast<size_t>(qh) * D + d0 + dd] = o * inv;
+  }
 }
 
 template <int G>
-void launch(const float *q, float *kc, float *vc, const float *kn, const float *vn, float *out,
-            char *ws, const WsLayout &L, int n_head_kv, int n_kv, const Plan &p, float scale_log2,
-            hipStream_t s) {
-  decode_kernel<G><<<n_head_kv * p.n_splits, WG, 0, s>>>(
-      q, kc, vc, kn, vn, out, reinterpret_cast<unsigned *>(ws + L.counters),
-      reinterpret_cast<float *>(ws + L.part_ml), reinterpret_cast<float *>(ws + L.part_o),
-      n_head_kv, n_kv, p.tokens_per_split, p.n_splits, scale_log2);
+void launch_split(const float *q, float *kc, float *vc, const float *kn, const float *vn,
+                  float *out, float *part_ml, float *part_o, int n_head_kv, int n_kv,
+                  const Plan &p, float scale_log2, hipStream_t s) {
+  decode_split_kernel<G><<<n_head_kv * p.n_splits, WG, 0, s>>>(
+      q, kc, vc, kn, vn, out, part_ml, part_o, n_head_kv, n_kv, p.tokens_per_split, p.n_splits,
+      scale_log2);
 }
 
 }  // namespace
@@ -292,7 +404,7 @@ extern "C" size_t ikv_attn_decode_workspace_bytes(int n_head, int n_head_kv, int
                                                   int64_t n_kv) {
   if (n_head <= 0 || n_head_kv <= 0 || head_dim != D || n_kv <= 0) return 0;
   const Plan p = plan_for(n_head_kv, n_kv);
-  return ws_layout(n_head, n_head_kv, p.n_splits).total;
+  return ws_layout(n_head, p.n_splits).total;
 }
 
 extern "C" int ikv_attn_decode_f32(const float *q, float *k_cache, float *v_cache,
@@ -306,24 +418,30 @@ extern "C" int ikv_attn_decode_f32(const float *q, float *k_cache, float *v_cach
   if (head_dim != D) return -ENOTSUP;
   const int G = n_head / n_head_kv;
   if (G != 1 && G != 2 && G != 4 && G != 8) return -ENOTSUP;
-  if (n_kv > INT_MAX - TILE) return -EOVERFLOW;
+  if (n_kv > INT_MAX - 2 * TILE) return -EOVERFLOW;
   if (!ikv::aligned16(q) || !ikv::aligned16(k_cache) || !ikv::aligned16(v_cache) ||
       !ikv::aligned16(out) || (k_new && (!ikv::aligned16(k_new) || !ikv::aligned16(v_new))))
     return -EINVAL;
   const Plan p = plan_for(n_head_kv, n_kv);
-  const WsLayout L = ws_layout(n_head, n_head_kv, p.n_splits);
-  if (p.n_splits > 1 && (!workspace || workspace_bytes < L.total || !ikv::aligned16(workspace)))
-    return -EINVAL;
+  const WsLayout L = ws_layout(n_head, p.n_splits);
+  float *part_ml = nullptr, *part_o = nullptr;
+  if (p.n_splits > 1) {
+    if (!workspace || workspace_bytes < L.total || !ikv::aligned16(workspace)) return -EINVAL;
+    part_ml = reinterpret_cast<float *>(static_cast<char *>(workspace) + L.part_ml);
+    part_o = reinterpret_cast<float *>(static_cast<char *>(workspace) + L.part_o);
+  }
   if (!(scale > 0.0f)) scale = 1.0f / sqrtf(static_cast<float>(head_dim));
-  const float scale_log2 = scale * ikv::kLog2e;
-  char *ws = static_cast<char *>(workspace);
+  const float sl2 = scale * ikv::kLog2e;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int nk = static_cast<int>(n_kv);
   switch (G) {
-    case 1: launch<1>(q, k_cache, v_cache, k_new, v_new, out, ws, L, n_head_kv, nk, p, scale_log2, s); break;
-    case 2: launch<2>(q, k_cache, v_cache, k_new, v_new, out, ws, L, n_head_kv, nk, p, scale_log2, s); break;
-    case 4: launch<4>(q, k_cache, v_cache, k_new, v_new, out, ws, L, n_head_kv, nk, p, scale_log2, s); break;
-    default: launch<8>(q, k_cache, v_cache, k_new, v_new, out, ws, L, n_head_kv, nk, p, scale_log2, s); break;
+    case 1: launch_split<1>(q, k_cache, v_cache, k_new, v_new, out, part_ml, part_o, n_head_kv, nk, p, sl2, s); break;
+    case 2: launch_split<2>(q, k_cache, v_cache, k_new, v_new, out, part_ml, part_o, n_head_kv, nk, p, sl2, s); break;
+    case 4: launch_split<4>(q, k_cache, v_cache, k_new, v_new, out, part_ml, part_o, n_head_kv, nk, p, sl2, s); break;
+    default: launch_split<8>(q, k_cache, v_cache, k_new, v_new, out, part_ml, part_o, n_head_kv, nk, p, sl2, s); break;
   }
+  if (p.n_splits > 1)
+    decode_merge_kernel<<<n_head * (D / kMergeDims), kMergeThreads, 0, s>>>(part_ml, part_o, out,
+                                                                          p.n_splits);
   return ikv::launch_status();
 }

@@ -23,13 +23,26 @@ inline int launch_status() {
 
 inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Cross-lane moves on the DPP network (no LDS round trip).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // lane i <-> 7-i within 8 lanes
+constexpr int kDppMirror = 0x140;     // lane i <-> 15-i within 16 lanes
+
 // Sum over the 32 lanes of a half-wave; every lane of the half gets the sum.
+// Four DPP steps build sums over 4, 8 and 16 lanes; one ds_swizzle (xor 16
+// inside each 32-lane group, bitmask mode) finishes.
 __device__ __forceinline__ float half_wave_sum(float v) {
-  v += __shfl_xor(v, 16, 32);
-  v += __shfl_xor(v, 8, 32);
-  v += __shfl_xor(v, 4, 32);
-  v += __shfl_xor(v, 2, 32);
-  v += __shfl_xor(v, 1, 32);
+  v += dpp<kDppXor1>(v);
+  v += dpp<kDppXor2>(v);
+  v += dpp<kDppHalfMirror>(v);
+  v += dpp<kDppMirror>(v);
+  v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
   return v;
 }
 

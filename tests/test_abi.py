@@ -79,7 +79,7 @@ def test_workspace_bytes_grow_with_context_and_are_bounded():
     sizes = [ikv.decode_workspace_bytes(16, 8, 128, n) for n in (1, 256, 4097, 32769, 10**6)]
     assert all(s > 0 for s in sizes)
     assert sizes == sorted(sizes)
-    assert sizes[-1] <= 16 * 512 * (128 + 2) * 4 + 4096  # at most 512 splits per head
+    assert sizes[-1] <= 16 * 1024 * (128 + 2) * 4 + 4096  # at most 1024 splits per head
     assert ikv.decode_workspace_bytes(16, 8, 64, 100) == 0
 
 
