@@ -151,6 +151,64 @@ def time_prefill(torch, ikv, p, reps):
     return e0.elapsed_time(e1) / 1e3 / reps
 
 
+def hbm_probes(torch, ikv):
+    """What this box sustains, measured in the same run: a long streaming read
+    (897 MiB per kernel), a streaming read of one decode layer's size (33.6 MB
+    per kernel, 28 rotating buffers, HIP graph), and an empty kernel."""
+    import ctypes
+
+    lib = ikv.load()
+    dev = torch.device("cuda:0")
+    sink = torch.empty(16384, device=dev)
+    res = {}
+
+    def timed_graph(fn, reps):
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            fn()
+        g.replay()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / 1e3 / reps
+
+    def read(buf, grid):
+        rc = lib.ikv_probe_read(buf.data_ptr(), buf.numel() * 4, sink.data_ptr(), grid,
+                                torch.cuda.current_stream().cuda_stream)
+        if rc:
+            raise RuntimeError(f"ikv_probe_read {rc}")
+
+    big = torch.ones(N_LAYER * decode_bytes(4096) // 4 // 16 * 16, device=dev)
+    t = timed_graph(lambda: read(big, 2048), 5)
+    res["read_long_gbs"] = round(big.numel() * 4 / t / 1e9, 1)
+    del big
+    bufs = [torch.ones(decode_bytes(4096) // 4 // 16 * 16, device=dev) for _ in range(N_LAYER)]
+    for grid in (1024, 2048):
+        t = timed_graph(lambda: [read(b, grid) for b in bufs], 10) / N_LAYER
+        res[f"read_33MB_grid{grid}_us"] = round(t * 1e6, 2)
+        res[f"read_33MB_grid{grid}_gbs"] = round(bufs[0].numel() * 4 / t / 1e9, 1)
+    del bufs
+
+    def empties():
+        for _ in range(200):
+            lib.ikv_probe_empty(1024, torch.cuda.current_stream().cuda_stream)
+
+    res["empty_kernel_us"] = round(timed_graph(empties, 5) / 200 * 1e6, 2)
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(ctx, seconds):
     """The oracle (restated reference CPU backend) on this host: the same
     decode step (append + attention) of one layer, rotated over 8 layers."""
@@ -199,6 +257,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the ctx sweep and prefill")
+    ap.add_argument("--eager", action="store_true", help="launch without HIP-graph capture")
+    ap.add_argument("--pmc-calibrate", action="store_true",
+                    help="only run 3 copies of 256 MiB through ikv_append_f32 (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the hot path has no "
@@ -211,11 +272,23 @@ def main():
 
     torch.cuda.set_device(0)
     ikv.load()
+    if args.pmc_calibrate:
+        n = 256 * 2**20
+        a = torch.ones(n // 4, device="cuda:0")
+        b = torch.empty_like(a)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            ikv.append(b, a)
+        torch.cuda.synchronize()
+        print(json.dumps({"pmc_calibration": "ikv_append_f32 copy", "bytes_read": n,
+                          "bytes_written": n, "dispatches": 3}), flush=True)
+        return
     log(f"[bench] {ikv.version()} on {torch.cuda.get_device_name(0)}")
 
     rig = DecodeRig(torch, ikv, args.ctx)
-    rig.capture()
-    log(f"[bench] graph captured ({N_LAYER} launches per step), replays match eager")
+    if not args.eager:
+        rig.capture()
+        log(f"[bench] graph captured ({N_LAYER} launches per step), replays match eager")
     secs = rig.time(args.steps, args.warmup)
     launches = args.steps * N_LAYER
     per_launch = secs / launches
@@ -231,7 +304,8 @@ def main():
         if t.get("ctx") == args.ctx:
             traffic = t.get("hbm_bytes_per_launch")
 
-    extra = {"eager_gbs": None, "ctx_sweep_gbs": {}, "mall_hot_gbs": None, "prefill": {}}
+    extra = {"eager_gbs": None, "ctx_sweep_gbs": {}, "mall_hot_gbs": None, "prefill": {},
+             "hbm_probes": None}
     if not args.no_extra:
         rig.graph = None
         es = rig.time(max(args.steps // 2, 5), 2)
@@ -253,6 +327,8 @@ def main():
         s = hot.time(20, 3)
         extra["mall_hot_gbs"] = round(bpl * 20 * N_LAYER / s / 1e9, 1)
         del hot
+        extra["hbm_probes"] = hbm_probes(torch, ikv)
+        log(f"[bench] hbm probes: {extra['hbm_probes']}")
         for p in (32, 64, 128, 256, 2048):
             t = time_prefill(torch, ikv, p, 20 if p < 2048 else 10)
             tf = prefill_flops(p) / t / 1e12

@@ -1,0 +1,472 @@
+#include "hip_backend.hpp"
+
+#include <cstdio>
+#include <cstring>
+#include <vector>
+
+#include "../../include/ikv.h"
+#include "op_params.hpp"
+
+namespace {
+
+// C-ABI return code -> error_code: negative errno as std::errc, positive
+// hipError_t as io_error (the mapping of check_cuda, reference
+// include/cuda_util.hpp:7-16).
+infer::expected<void, std::error_code> check_ikv(int rc, const char *what) {
+  if (rc == 0) return {};
+  if (rc < 0) return infer::unexpected(std::make_error_code(static_cast<std::errc>(-rc)));
+  std::fprintf(stderr, "[hip] %s: %s\n", what, hipGetErrorString(static_cast<hipError_t>(rc)));
+  return infer::fail(std::errc::io_error);
+}
+
+infer::expected<void, std::error_code> check_hip(hipError_t e, const char *what) {
+  if (e == hipSuccess) return {};
+  std::fprintf(stderr, "[hip] %s: %s\n", what, hipGetErrorString(e));
+  return infer::fail(std::errc::io_error);
+}
+
+bool contiguous_f32(const Tensor *t) {
+  return t && t->data && t->dataType == GGML_TYPE_F32 && t->is_contiguous();
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// HBM allocator
+
+infer::expected<void *, std::error_code> HIPPhysicalAllocator::raw_alloc(size_t bytes) {
+  if (bytes == 0) return static_cast<void *>(nullptr);
+  void *p = nullptr;
+  if (hipMalloc(&p, bytes) != hipSuccess || !p) {
+    (void)hipGetLastError();
+    return infer::fail(std::errc::not_enough_memory);
+  }
+  return p;
+}
+
+void HIPPhysicalAllocator::raw_free(void *ptr) {
+  if (ptr) (void)hipFree(ptr);
+}
+
+// ---------------------------------------------------------------------------
+// registration
+
+std::vector<DeviceInfo> probe_hip_devices() {
+  std::vector<DeviceInfo> devices;
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess) {
+    (void)hipGetLastError();
+    return devices;
+  }
+  int prev = 0;
+  const bool restore = hipGetDevice(&prev) == hipSuccess;
+  for (int i = 0; i < count; ++i) {
+    if (hipSetDevice(i) != hipSuccess) continue;
+    size_t free_b = 0, total_b = 0;
+    if (hipMemGetInfo(&free_b, &total_b) != hipSuccess) continue;
+    devices.push_back({"hip:" + std::to_string(i), DeviceType::HIP, free_b});
+  }
+  if (restore) (void)hipSetDevice(prev);
+  return devices;
+}
+
+void register_hip_backend() {
+  BackendRegistry::instance().register_backend(
+      "hip", [] { return probe_hip_devices(); },
+      [](int device_id, DeviceInfo info, const PoolConfig &cfg) -> std::unique_ptr<Backend> {
+        return std::make_unique<HIPBackend>(device_id, std::move(info), cfg);
+      });
+}
+
+// ---------------------------------------------------------------------------
+
+HIPBackend::HIPBackend(int device_id, DeviceInfo info, const PoolConfig &cfg)
+    : Backend(device_id, std::move(info), cfg) {
+  init_pools(std::make_unique<HIPPhysicalAllocator>());
+  (void)hipSetDevice(_device_id);
+  (void)hipStreamCreate(&_stream);
+  if (hipMalloc(reinterpret_cast<void **>(&_status), sizeof(int)) == hipSuccess)
+    (void)hipMemset(_status, 0, sizeof(int));
+}
+
+HIPBackend::~HIPBackend() {
+  (void)hipSetDevice(_device_id);
+  if (_stream) (void)hipStreamSynchronize(_stream);
+  for (auto &t : _tables) {
+    (void)hipFree(t.sin);
+    (void)hipFree(t.cos);
+  }
+  if (_workspace) (void)hipFree(_workspace);
+  if (_status) (void)hipFree(_status);
+  if (_stream) (void)hipStreamDestroy(_stream);
+}
+
+infer::expected<void, std::error_code> HIPBackend::set_device() const {
+  return check_hip(hipSetDevice(_device_id), "hipSetDevice");
+}
+
+bool HIPBackend::supports_op(OperationType op, const Tensor &t) const {
+  (void)t;
+  switch (op) {
+    case OperationType::GGML_OP_NONE:
+    case OperationType::GGML_OP_CPY:
+    case OperationType::GGML_OP_VIEW:
+    case OperationType::GGML_OP_RESHAPE:
+    case OperationType::GGML_OP_RMS_NORM:
+    case OperationType::GGML_OP_ROPE:
+    case OperationType::GGML_OP_FLASH_ATTN_EXT:
+      return true;
+    default:
+      return false;
+  }
+}
+
+bool HIPBackend::accepts_host_src(const Tensor &node, int src_index) const {
+  return node.op == OperationType::GGML_OP_ROPE && src_index == 2;
+}
+
+infer::expected<void *, std::error_code> HIPBackend::alloc(BufferKind kind, size_t bytes) {
+  if (auto r = set_device(); !r) return infer::unexpected(r.error());
+  return Backend::alloc(kind, bytes);
+}
+
+void HIPBackend::free(BufferKind kind, void *ptr) {
+  (void)hipSetDevice(_device_id);
+  Backend::free(kind, ptr);
+}
+
+infer::expected<void, std::error_code> HIPBackend::copy_tensor_set(Tensor *tensor, const void *data,
+                                                                   size_t offset, size_t size) {
+  if (!tensor || !tensor->data || !data) return infer::fail(std::errc::invalid_argument);
+  if (offset + size > tensor->byte_size()) return infer::fail(std::errc::invalid_argument);
+  if (auto r = set_device(); !r) return r;
+  auto r = check_hip(hipMemcpyAsync(static_cast<char *>(tensor->data) + offset, data, size,
+                                    hipMemcpyHostToDevice, _stream),
+                     "copy_tensor_set");
+  if (!r) return r;
+  return check_hip(hipStreamSynchronize(_stream), "copy_tensor_set sync");
+}
+
+infer::expected<void, std::error_code> HIPBackend::copy_tensor_get(const Tensor *tensor, void *data,
+                                                                   size_t offset, size_t size) {
+  if (!tensor || !tensor->data || !data) return infer::fail(std::errc::invalid_argument);
+  if (offset + size > tensor->byte_size()) return infer::fail(std::errc::invalid_argument);
+  if (auto r = set_device(); !r) return r;
+  auto r = check_hip(hipMemcpyAsync(data, static_cast<const char *>(tensor->data) + offset, size,
+                                    hipMemcpyDeviceToHost, _stream),
+                     "copy_tensor_get");
+  if (!r) return r;
+  return check_hip(hipStreamSynchronize(_stream), "copy_tensor_get sync");
+}
+
+infer::expected<bool, std::error_code> HIPBackend::copy_tensor_high(const Tensor *src,
+                                                                    Tensor *dst) const {
+  if (!src || !dst || !src->backend || !dst->data || !src->data) return false;
+  if (src->device != DeviceType::HIP) return false;  // host sources go through copy_tensor_set
+  const auto *peer = dynamic_cast<const HIPBackend *>(src->backend);
+  if (!peer) return infer::fail(std::errc::invalid_argument);
+  if (src->byte_size() != dst->byte_size()) return infer::fail(std::errc::invalid_argument);
+  if (auto r = set_device(); !r) return infer::unexpected(r.error());
+  hipError_t e;
+  if (peer->_device_id == _device_id)
+    e = hipMemcpyAsync(dst->data, src->data, src->byte_size(), hipMemcpyDeviceToDevice, _stream);
+  else  // over xGMI when peer access is enabled, staged by the runtime otherwise
+    e = hipMemcpyPeerAsync(dst->data, _device_id, src->data, peer->_device_id, src->byte_size(),
+                           _stream);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  return true;
+}
+
+infer::expected<void, std::error_code> HIPBackend::synchronize() {
+  if (auto r = set_device(); !r) return r;
+  if (auto r = check_hip(hipStreamSynchronize(_stream), "synchronize"); !r) return r;
+  int status = 0;
+  if (_status) {
+    if (auto r = check_hip(hipMemcpy(&status, _status, sizeof(int), hipMemcpyDeviceToHost), "status");
+        !r)
+      return r;
+  }
+  if (status != 0) {
+    (void)hipMemset(_status, 0, sizeof(int));
+    std::fprintf(stderr, "[hip] RoPE position outside the angle table\n");
+    return infer::fail(std::errc::invalid_argument);
+  }
+  return {};
+}
+
+infer::expected<void, std::error_code> HIPBackend::ensure_workspace(size_t bytes) {
+  if (bytes <= _workspace_bytes) return {};
+  if (_workspace) {
+    (void)hipStreamSynchronize(_stream);
+    (void)hipFree(_workspace);
+    _workspace = nullptr;
+    _workspace_bytes = 0;
+  }
+  if (hipMalloc(&_workspace, bytes) != hipSuccess) {
+    (void)hipGetLastError();
+    _workspace = nullptr;
+    return infer::fail(std::errc::not_enough_memory);
+  }
+  _workspace_bytes = bytes;
+  return {};
+}
+
+infer::expected<void, std::error_code> HIPBackend::reserve_decode_workspace(int n_head,
+                                                                           int n_head_kv,
+                                                                           int head_dim,
+                                                                           int64_t max_kv) {
+  if (auto r = set_device(); !r) return r;
+  size_t need = 0;
+  for (int64_t n = 1; n <= max_kv; n = n < 64 ? n + 1 : n * 2)  // workspace grows with n_kv
+    need = std::max(need, ikv_attn_decode_workspace_bytes(n_head, n_head_kv, head_dim, n));
+  need = std::max(need, ikv_attn_decode_workspace_bytes(n_head, n_head_kv, head_dim, max_kv));
+  return ensure_workspace(need);
+}
+
+infer::expected<const HIPBackend::RopeTables *, std::error_code> HIPBackend::rope_tables(
+    const Tensor &theta) {
+  if (auto it = _rope.find(theta.data); it != _rope.end()) return &_tables[it->second];
+  if (theta.dataType != GGML_TYPE_F32 || !theta.data) return infer::fail(std::errc::invalid_argument);
+  const int64_t half = theta.dims[0];
+  const int64_t n_ctx = theta.dims[1];
+  if (half <= 0 || n_ctx <= 0) return infer::fail(std::errc::invalid_argument);
+  const size_t count = static_cast<size_t>(half * n_ctx);
+  const bool on_host = theta.device == DeviceType::CPU;
+
+  // Content key: the dims and row 1 (the frequencies, which fix theta_base
+  // and head_dim). A table staged to the device at a new address each step
+  // then maps to the sin/cos tables already built for it.
+  std::vector<float> row1(static_cast<size_t>(half), 0.f);
+  if (n_ctx > 1) {
+    const float *src = static_cast<const float *>(theta.data) + half;
+    if (on_host)
+      std::memcpy(row1.data(), src, row1.size() * sizeof(float));
+    else if (auto r = check_hip(hipMemcpy(row1.data(), src, row1.size() * sizeof(float),
+                                          hipMemcpyDeviceToHost),
+                                "rope table key");
+             !r)
+      return infer::unexpected(r.error());
+  }
+  std::string key(reinterpret_cast<const char *>(&half), sizeof(half));
+  key.append(reinterpret_cast<const char *>(&n_ctx), sizeof(n_ctx));
+  key.append(reinterpret_cast<const char *>(row1.data()), row1.size() * sizeof(float));
+  if (auto it = _rope_by_content.find(key); it != _rope_by_content.end()) {
+    _rope.emplace(theta.data, it->second);
+    return &_tables[it->second];
+  }
+
+  std::vector<float> host(count), s(count), c(count);
+  if (on_host) {
+    std::memcpy(host.data(), theta.data, count * sizeof(float));
+  } else if (auto r = check_hip(hipMemcpy(host.data(), theta.data, count * sizeof(float),
+                                          hipMemcpyDeviceToHost),
+                                "rope table");
+             !r) {
+    return infer::unexpected(r.error());
+  }
+  if (auto r = check_ikv(ikv_rope_sincos_table_f32(host.data(), count, s.data(), c.data()), "sincos");
+      !r)
+    return infer::unexpected(r.error());
+  RopeTables t;
+  t.half = half;
+  t.n_ctx = n_ctx;
+  if (hipMalloc(reinterpret_cast<void **>(&t.sin), count * sizeof(float)) != hipSuccess ||
+      hipMalloc(reinterpret_cast<void **>(&t.cos), count * sizeof(float)) != hipSuccess) {
+    (void)hipGetLastError();
+    (void)hipFree(t.sin);
+    return infer::fail(std::errc::not_enough_memory);
+  }
+  if (auto r = check_hip(hipMemcpy(t.sin, s.data(), count * sizeof(float), hipMemcpyHostToDevice),
+                         "sin upload");
+      !r)
+    return infer::unexpected(r.error());
+  if (auto r = check_hip(hipMemcpy(t.cos, c.data(), count * sizeof(float), hipMemcpyHostToDevice),
+                         "cos upload");
+      !r)
+    return infer::unexpected(r.error());
+  _tables.push_back(t);
+  const size_t idx = _tables.size() - 1;
+  _rope_by_content.emplace(std::move(key), idx);
+  _rope.emplace(theta.data, idx);
+  return &_tables[idx];
+}
+
+infer::expected<void, std::error_code> HIPBackend::compute(Graph &graph) {
+  if (auto r = set_device(); !r) return r;
+  _stats = Stats{};
+  _norm_into_rope.clear();
+  _append_into_attn.clear();
+  _skip.clear();
+
+  if (_fusion) {
+    std::unordered_map<const Tensor *, int> uses;
+    for (Tensor *n : graph.nodes())
+      for (Tensor *s : n->src)
+        if (s) ++uses[s];
+    for (Tensor *o : graph.outputs()) ++uses[o];
+    for (Tensor *n : graph.nodes()) {
+      if (n->op == OperationType::GGML_OP_ROPE) {
+        const Tensor *nm = n->src[0];
+        if (nm && nm->op == OperationType::GGML_OP_RMS_NORM && uses[nm] == 1 &&
+            nm->dims == n->dims && nm->src[1] && nm->src[1]->element_count() == size_t(n->dims[0])) {
+          _norm_into_rope[n] = nm;
+          _skip[nm] = true;
+        }
+      }
+      if (n->op == OperationType::GGML_OP_FLASH_ATTN_EXT && n->src[0] && n->src[0]->dims[2] == 1) {
+        const Tensor *kv = n->src[1], *vv = n->src[2];
+        if (!kv || !vv || kv->op != OperationType::GGML_OP_VIEW || vv->op != OperationType::GGML_OP_VIEW)
+          continue;
+        const Tensor *kc = kv->src[0], *vc = vv->src[0];
+        if (!kc || !vc || kc->op != OperationType::GGML_OP_CPY || vc->op != OperationType::GGML_OP_CPY)
+          continue;
+        if (uses[kv] != 1 || uses[vv] != 1 || uses[kc] != 1 || uses[vc] != 1) continue;
+        const int64_t n_kv = kv->dims[2];
+        AttnParams p;
+        std::memcpy(&p, n->op_params, sizeof(p));
+        const size_t row = static_cast<size_t>(kv->dims[0] * kv->dims[1]) * 4;
+        const bool last_row_k = kc->dims[2] == 1 && kc->dims[3] == 1 &&
+                                kc->data == static_cast<char *>(kv->data) + (n_kv - 1) * row;
+        const bool last_row_v = vc->dims[2] == 1 && vc->dims[3] == 1 &&
+                                vc->data == static_cast<char *>(vv->data) + (n_kv - 1) * row;
+        if (!last_row_k || !last_row_v || int64_t(p.n_ctx) + 1 != n_kv) continue;
+        if (!contiguous_f32(kc->src[0]) || !contiguous_f32(vc->src[0])) continue;
+        _append_into_attn[n] = {kc->src[0], vc->src[0]};
+        _skip[kc] = true;
+        _skip[vc] = true;
+      }
+    }
+  }
+
+  for (Tensor *node : graph.nodes()) {
+    if (node->op == OperationType::GGML_OP_NONE) continue;
+    if (_skip.count(node)) continue;
+    if (auto r = dispatch(node); !r) {
+      std::fprintf(stderr, "[hip] compute failed at node %s op=%u\n", node->name.c_str(),
+                   static_cast<unsigned>(node->op));
+      return r;
+    }
+  }
+  return {};
+}
+
+infer::expected<void, std::error_code> HIPBackend::dispatch(Tensor *node) {
+  void *s = _stream;
+  switch (node->op) {
+    case OperationType::GGML_OP_VIEW:
+      return {};
+
+    case OperationType::GGML_OP_CPY: {
+      const Tensor *src = node->src[0];
+      if (!src || !src->data || !node->data || src->dataType != node->dataType || src->dims != node->dims)
+        return infer::fail(std::errc::invalid_argument);
+      if (!src->is_contiguous() || !node->is_contiguous()) return infer::fail(std::errc::not_supported);
+      const size_t rows = static_cast<size_t>(node->dims[2] * node->dims[3]);
+      const size_t row_bytes = static_cast<size_t>(node->dims[0] * node->dims[1]) * dataType_size(node->dataType);
+      ++_stats.launches;
+      return check_ikv(ikv_append_f32(node->data, src->data, rows, row_bytes, s), "append");
+    }
+
+    case OperationType::GGML_OP_RESHAPE: {
+      const Tensor *src = node->src[0];
+      if (!src || !src->data || !node->data || src->byte_size() != node->byte_size())
+        return infer::fail(std::errc::invalid_argument);
+      if (node->data == src->data) return {};
+      ++_stats.launches;
+      return check_ikv(ikv_append_f32(node->data, src->data, 1, src->byte_size(), s), "reshape");
+    }
+
+    case OperationType::GGML_OP_RMS_NORM: {
+      const Tensor *x = node->src[0], *w = node->src[1];
+      if (!contiguous_f32(x) || !contiguous_f32(w) || !node->data || x->dims != node->dims ||
+          w->element_count() != static_cast<size_t>(x->dims[0]))
+        return infer::fail(std::errc::invalid_argument);
+      float eps;
+      std::memcpy(&eps, &node->op_params[0], sizeof(eps));
+      ++_stats.launches;
+      return check_ikv(ikv_rms_norm_f32(static_cast<const float *>(x->data),
+                                        static_cast<const float *>(w->data),
+                                        static_cast<float *>(node->data),
+                                        static_cast<int64_t>(x->element_count() / x->dims[0]),
+                                        x->dims[0], eps, s),
+                       "rms_norm");
+    }
+
+    case OperationType::GGML_OP_ROPE: {
+      const Tensor *pos = node->src[1], *theta = node->src[2];
+      const auto fused = _norm_into_rope.find(node);
+      const Tensor *x = fused != _norm_into_rope.end() ? fused->second->src[0] : node->src[0];
+      if (!contiguous_f32(x) || !pos || !pos->data || pos->dataType != GGML_TYPE_I32 || !theta ||
+          !node->data || x->dims != node->dims || pos->element_count() != static_cast<size_t>(x->dims[2]))
+        return infer::fail(std::errc::invalid_argument);
+      if (theta->dims[0] * 2 != x->dims[0]) return infer::fail(std::errc::invalid_argument);
+      auto tab = rope_tables(*theta);
+      if (!tab) return infer::unexpected(tab.error());
+      const RopeTables &t = **tab;
+      ++_stats.launches;
+      if (fused != _norm_into_rope.end()) {
+        const Tensor *w = fused->second->src[1];
+        float eps;
+        std::memcpy(&eps, &fused->second->op_params[0], sizeof(eps));
+        ++_stats.fused_norm_rope;
+        return check_ikv(ikv_qk_norm_rope_f32(static_cast<const float *>(x->data),
+                                              static_cast<const float *>(w->data),
+                                              static_cast<float *>(node->data),
+                                              static_cast<const int32_t *>(pos->data), x->dims[2],
+                                              static_cast<int>(x->dims[1]), static_cast<int>(x->dims[0]),
+                                              eps, t.sin, t.cos, t.n_ctx, _status, s),
+                         "qk_norm_rope");
+      }
+      return check_ikv(ikv_rope_neox_f32(static_cast<const float *>(x->data),
+                                         static_cast<float *>(node->data),
+                                         static_cast<const int32_t *>(pos->data), x->dims[2],
+                                         static_cast<int>(x->dims[1]), static_cast<int>(x->dims[0]),
+                                         t.sin, t.cos, t.n_ctx, _status, s),
+                       "rope");
+    }
+
+    case OperationType::GGML_OP_FLASH_ATTN_EXT: {
+      const Tensor *q = node->src[0], *k = node->src[1], *v = node->src[2];
+      if (!contiguous_f32(q) || !contiguous_f32(k) || !contiguous_f32(v) || !node->data)
+        return infer::fail(std::errc::invalid_argument);
+      AttnParams p;
+      std::memcpy(&p, node->op_params, sizeof(p));
+      const int64_t D = q->dims[0], Hq = q->dims[1], nq = q->dims[2];
+      const int64_t Hkv = k->dims[1], nkv = k->dims[2];
+      if (k->dims[0] != D || v->dims[0] != D || v->dims[1] != Hkv || v->dims[2] != nkv || Hkv <= 0 ||
+          Hq % Hkv != 0)
+        return infer::fail(std::errc::invalid_argument);
+      ++_stats.launches;
+      if (nq == 1 && nkv == static_cast<int64_t>(p.n_ctx) + 1) {
+        const auto fused = _append_into_attn.find(node);
+        const void *kn = nullptr, *vn = nullptr;
+        if (fused != _append_into_attn.end()) {
+          kn = fused->second.first->data;
+          vn = fused->second.second->data;
+          ++_stats.fused_append_decode;
+        }
+        const size_t need = ikv_attn_decode_workspace_bytes(int(Hq), int(Hkv), int(D), nkv);
+        if (auto r = ensure_workspace(need); !r) return r;
+        return check_ikv(ikv_attn_decode_f32(static_cast<const float *>(q->data),
+                                             static_cast<float *>(k->data), static_cast<float *>(v->data),
+                                             static_cast<const float *>(kn), static_cast<const float *>(vn),
+                                             static_cast<float *>(node->data), int(Hq), int(Hkv), int(D),
+                                             nkv, p.scale, _workspace, _workspace_bytes, s),
+                         "attn_decode");
+      }
+      return check_ikv(ikv_attn_prefill_f32(static_cast<const float *>(q->data),
+                                            static_cast<const float *>(k->data),
+                                            static_cast<const float *>(v->data),
+                                            static_cast<float *>(node->data), int(Hq), int(Hkv), int(D),
+                                            nq, nkv, p.n_ctx, p.scale, s),
+                       "attn_prefill");
+    }
+
+    default:
+      std::fprintf(stderr, "[hip] unsupported op %u\n", static_cast<unsigned>(node->op));
+      return infer::fail(std::errc::not_supported);
+  }
+}

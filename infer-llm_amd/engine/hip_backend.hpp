@@ -1,0 +1,93 @@
+// hip_backend.hpp — the MI355X backend behind the engine's Backend interface
+// (the slot of CUDABackend, reference include/backends/cuda_backend.hpp:15-97,
+// src/backends/cuda_backend.cpp:6-241).
+//
+// * Registered as "hip"; devices are probed with hipGetDeviceCount /
+//   hipMemGetInfo and named "hip:<id>".
+// * WEIGHTS / ACTIVATION / KVCACHE pools allocate with hipMalloc, so the KV
+//   cache of NaiveKVStorage lives in HBM.
+// * One stream per backend (default priority); every entry point selects the
+//   device first.
+// * compute() walks the subgraph in topological order and calls the C-ABI
+//   of include/ikv.h. Two fusions are applied when the graph has the shape
+//   the Qwen3 attention slice builds: RMS_NORM -> ROPE becomes one
+//   qk-norm+RoPE launch, and CPY (K), CPY (V) -> VIEW -> FLASH_ATTN_EXT for
+//   one query token becomes one decode launch with the append inside.
+// * RoPE reads device-resident sin/cos tables built once, with the host's
+//   sinf/cosf, from the angle table the graph supplies (host memory); the
+//   reference copied that 10.5 MB table to the device every step.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "backend.hpp"
+#include "graph.hpp"
+
+std::vector<DeviceInfo> probe_hip_devices();
+
+class HIPBackend : public Backend {
+ public:
+  HIPBackend(int device_id, DeviceInfo info, const PoolConfig &cfg);
+  ~HIPBackend() override;
+
+  DeviceType device_type() const override { return DeviceType::HIP; }
+  std::string device_name() const override { return "HIP:" + std::to_string(_device_id); }
+  bool supports_op(OperationType op, const Tensor &t) const override;
+  infer::expected<void *, std::error_code> alloc(BufferKind kind, size_t bytes) override;
+  void free(BufferKind kind, void *ptr) override;
+  bool is_host() const override { return false; }
+  infer::expected<void, std::error_code> copy_tensor_set(Tensor *tensor, const void *data,
+                                                         size_t offset, size_t size) override;
+  infer::expected<void, std::error_code> copy_tensor_get(const Tensor *tensor, void *data,
+                                                         size_t offset, size_t size) override;
+  infer::expected<bool, std::error_code> copy_tensor_high(const Tensor *src,
+                                                          Tensor *dst) const override;
+  infer::expected<void, std::error_code> compute(Graph &sub_graph) override;
+  // Waits for the stream, then reports RoPE position errors recorded by the
+  // kernels since the last call (invalid_argument).
+  infer::expected<void, std::error_code> synchronize() override;
+  bool accepts_host_src(const Tensor &node, int src_index) const override;
+
+  hipStream_t stream() const { return _stream; }
+  // Sizes the decode workspace for contexts up to max_kv keys, so that no
+  // allocation happens inside compute() (e.g. under graph capture).
+  infer::expected<void, std::error_code> reserve_decode_workspace(int n_head, int n_head_kv,
+                                                                  int head_dim, int64_t max_kv);
+  void set_fusion(bool on) { _fusion = on; }
+  struct Stats {
+    int launches = 0;
+    int fused_norm_rope = 0;
+    int fused_append_decode = 0;
+  };
+  const Stats &last_stats() const { return _stats; }
+
+ private:
+  struct RopeTables {
+    float *sin = nullptr;
+    float *cos = nullptr;
+    int64_t n_ctx = 0;
+    int64_t half = 0;
+  };
+  infer::expected<const RopeTables *, std::error_code> rope_tables(const Tensor &theta);
+  infer::expected<void, std::error_code> ensure_workspace(size_t bytes);
+  infer::expected<void, std::error_code> dispatch(Tensor *node);
+  infer::expected<void, std::error_code> set_device() const;
+
+  hipStream_t _stream = nullptr;
+  int *_status = nullptr;  // device flag raised by RoPE on a bad position
+  void *_workspace = nullptr;
+  size_t _workspace_bytes = 0;
+  std::vector<RopeTables> _tables;                            // device sin/cos tables
+  std::unordered_map<const void *, size_t> _rope;             // angle-table address -> table
+  std::unordered_map<std::string, size_t> _rope_by_content;   // dims + row 1 -> table
+  bool _fusion = true;
+  Stats _stats;
+  // per-compute() fusion plan
+  std::unordered_map<const Tensor *, const Tensor *> _norm_into_rope;  // rope -> its rms_norm
+  std::unordered_map<const Tensor *, std::pair<const Tensor *, const Tensor *>> _append_into_attn;
+  std::unordered_map<const Tensor *, bool> _skip;
+};

@@ -1,0 +1,86 @@
+// kvstrategy.hpp — token -> storage mapping and the guarded layer views
+// (reference include/kvcache/kvstrategy.hpp:29-77, src/kvcache/kvstrategy.cpp
+// and src/kvcache/KVStrategys/contiguousKVStrategy.cpp).
+//
+// Contract (as in the reference): sequence lengths and the pending append are
+// owned by KVCacheManager; strategy methods take explicit TokenRanges;
+// lookup() sees ranges reserved but not yet committed; one uncommitted
+// append per sequence at a time.
+#pragma once
+
+#include <memory>
+#include <span>
+#include <system_error>
+#include <unordered_map>
+#include <vector>
+
+#include "../expected.hpp"
+#include "kvstorage.hpp"
+#include "kvutil.hpp"
+
+class KVStrategy {
+ public:
+  explicit KVStrategy(std::unique_ptr<KVStorage> storage) noexcept : _storage(std::move(storage)) {}
+  virtual ~KVStrategy() = default;
+  KVStrategy(const KVStrategy &) = delete;
+  KVStrategy &operator=(const KVStrategy &) = delete;
+
+  virtual infer::expected<void, std::error_code> init(std::span<const KVLayerSpec> layers,
+                                                      std::span<Backend *const> backend_layer,
+                                                      const KVCacheConfig &config) = 0;
+  virtual infer::expected<void, std::error_code> create_sequence(SequenceId id) = 0;
+  virtual infer::expected<void, std::error_code> reserve_append(SequenceId id, TokenRange range) = 0;
+
+  // Readable view [0, pending.end()) and writable view `pending`, each
+  // storage object acquired once (reference src/kvcache/kvstrategy.cpp:7-55).
+  infer::expected<KVLayerAccess, std::error_code> acquire_layer(SequenceId id, std::size_t layer,
+                                                                TokenRange pending);
+  infer::expected<void, std::error_code> release_layer(KVLayerAccess &access) noexcept;
+
+  virtual infer::expected<void, std::error_code> commit_append(SequenceId id, TokenRange range) = 0;
+  virtual infer::expected<void, std::error_code> abort_append(SequenceId id, TokenRange range) = 0;
+  virtual infer::expected<void, std::error_code> release_sequence(SequenceId id) = 0;
+  virtual infer::expected<void, std::error_code> clear_sequence() = 0;
+
+  KVStorage *storage() const { return _storage.get(); }
+
+ protected:
+  virtual infer::expected<KVMapping, std::error_code> lookup(SequenceId id, std::size_t layer,
+                                                             TokenRange range) const = 0;
+  infer::expected<KVRangeAccess, std::error_code> make_KVRangeAccess(
+      const KVMapping &mapping, TokenRange range, std::size_t layer,
+      std::unordered_map<StorageId, KVStorageObject> &objects, KVLayerAccess &access);
+
+  std::unique_ptr<KVStorage> _storage;
+  std::vector<KVLayerSpec> _layers;
+  KVCacheConfig _cfg = {};
+};
+
+// One storage object per (sequence, layer) of max_tokens_per_sequence tokens;
+// a token's offset in it is its absolute position.
+class ContiguousKVStrategy : public KVStrategy {
+ public:
+  explicit ContiguousKVStrategy(std::unique_ptr<KVStorage> storage) noexcept
+      : KVStrategy(std::move(storage)) {}
+
+  infer::expected<void, std::error_code> init(std::span<const KVLayerSpec> layers,
+                                              std::span<Backend *const> backend_layer,
+                                              const KVCacheConfig &config) override;
+  infer::expected<void, std::error_code> create_sequence(SequenceId id) override;
+  infer::expected<void, std::error_code> reserve_append(SequenceId id, TokenRange range) override;
+  infer::expected<void, std::error_code> commit_append(SequenceId id, TokenRange range) override;
+  infer::expected<void, std::error_code> abort_append(SequenceId id, TokenRange range) override;
+  infer::expected<void, std::error_code> release_sequence(SequenceId id) override;
+  infer::expected<void, std::error_code> clear_sequence() override;
+
+ protected:
+  infer::expected<KVMapping, std::error_code> lookup(SequenceId id, std::size_t layer,
+                                                     TokenRange range) const override;
+
+ private:
+  bool fits(TokenRange r) const {
+    const auto cap = _cfg.max_tokens_per_sequence;
+    return r.begin <= cap && r.count <= cap - r.begin;
+  }
+  std::unordered_map<SequenceId, std::vector<StorageId>> _sequences;  // index = layer
+};

@@ -20,7 +20,7 @@ from typing import Optional
 PKG_ROOT = pathlib.Path(__file__).resolve().parents[1]  # infer-llm_amd/
 REPO_ROOT = PKG_ROOT.parent
 LIB_PATH = PKG_ROOT / "lib" / "libikv.so"
-HEADER_PATH = REPO_ROOT / "include" / "ikv.h"
+HEADER_DIR = REPO_ROOT / "include"
 
 _c_void_p = ctypes.c_void_p
 _c_size_t = ctypes.c_size_t
@@ -28,7 +28,7 @@ _c_int = ctypes.c_int
 _c_int64 = ctypes.c_int64
 _c_float = ctypes.c_float
 
-# name -> (restype, argtypes); kept in the order of include/ikv.h
+# name -> (restype, argtypes); include/ikv.h, then include/ikv_probe.h
 SIGNATURES = {
     "ikv_version": (ctypes.c_char_p, []),
     "ikv_append_f32": (_c_int, [_c_void_p, _c_void_p, _c_size_t, _c_size_t, _c_void_p]),
@@ -56,6 +56,8 @@ SIGNATURES = {
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int64, _c_int, _c_int, _c_float,
          _c_void_p, _c_void_p, _c_int64, _c_void_p, _c_void_p],
     ),
+    "ikv_probe_read": (_c_int, [_c_void_p, _c_size_t, _c_void_p, _c_int, _c_void_p]),
+    "ikv_probe_empty": (_c_int, [_c_int, _c_void_p]),
 }
 
 
@@ -75,10 +77,12 @@ _lib: Optional[ctypes.CDLL] = None
 
 
 def header_functions() -> list[str]:
-    """Names of the entry points declared in include/ikv.h."""
-    text = HEADER_PATH.read_text()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(ikv_[a-z0-9_]+)\s*\(", text)))
+    """Names of the entry points declared in include/*.h."""
+    names = set()
+    for h in sorted(HEADER_DIR.glob("*.h")):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names |= set(re.findall(r"\b(ikv_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
 
 
 def load() -> ctypes.CDLL:

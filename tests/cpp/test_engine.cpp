@@ -1,0 +1,420 @@
+// test_engine.cpp — tests of the C++ engine layer.
+//
+//   test_engine --cpu   host-only: expected, registry, the KV-cache
+//                       transaction state machine (reference preconditions of
+//                       src/kvcache/*.cpp), views, graph order, RoPE table.
+//   test_engine --gpu   the Qwen3 attention slice (qk-norm, RoPE, KV append,
+//                       attention; src/models/Qwen3.cpp:61-88) built with the
+//                       engine's OpFactory, scheduled on HIPBackend over a
+//                       KVCacheManager, for a prefill and several decode
+//                       steps, checked against the CPU oracle: cache bytes
+//                       bit-exact, attention within 1e-4 rel / 1e-5 abs.
+//
+// Prints one line per check; the exit status is the number of failures.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "../../infer-llm_amd/engine/backend.hpp"
+#include "../../infer-llm_amd/engine/graph.hpp"
+#include "../../infer-llm_amd/engine/hip_backend.hpp"
+#include "../../infer-llm_amd/engine/kvcache/kvcache_manager.hpp"
+#include "../../infer-llm_amd/engine/op_factory.hpp"
+#include "../../infer-llm_amd/engine/scheduler.hpp"
+#include "../../oracle/oracle.h"
+
+static int g_fail = 0;
+#define CHECK(cond, name)                                         \
+  do {                                                            \
+    if (cond) {                                                   \
+      std::printf("PASS %s\n", name);                             \
+    } else {                                                      \
+      std::printf("FAIL %s (%s:%d)\n", name, __FILE__, __LINE__); \
+      ++g_fail;                                                   \
+    }                                                             \
+    std::fflush(stdout);                                          \
+  } while (0)
+
+static bool is_err(const std::error_code &e, std::errc want) { return e == std::make_error_code(want); }
+
+// Host backend test double: malloc pools, counts frees, computes nothing.
+class HostBackend : public Backend {
+ public:
+  explicit HostBackend(int id = 0) : Backend(id, {"host:" + std::to_string(id), DeviceType::CPU, 0}, {}) {
+    init_pools(std::make_unique<HostPhysicalAllocator>());
+  }
+  DeviceType device_type() const override { return DeviceType::CPU; }
+  std::string device_name() const override { return "HOST"; }
+  bool supports_op(OperationType, const Tensor &) const override { return false; }
+  bool is_host() const override { return true; }
+  infer::expected<void *, std::error_code> alloc(BufferKind k, size_t b) override {
+    ++allocs;
+    return Backend::alloc(k, b);
+  }
+  void free(BufferKind k, void *p) override {
+    if (p) ++frees;
+    Backend::free(k, p);
+  }
+  infer::expected<void, std::error_code> copy_tensor_set(Tensor *t, const void *d, size_t o, size_t s) override {
+    std::memcpy(static_cast<char *>(t->data) + o, d, s);
+    return {};
+  }
+  infer::expected<void, std::error_code> copy_tensor_get(const Tensor *t, void *d, size_t o, size_t s) override {
+    std::memcpy(d, static_cast<const char *>(t->data) + o, s);
+    return {};
+  }
+  infer::expected<bool, std::error_code> copy_tensor_high(const Tensor *, Tensor *) const override { return false; }
+  infer::expected<void, std::error_code> compute(Graph &) override { return infer::fail(std::errc::not_supported); }
+  int allocs = 0, frees = 0;
+};
+
+// splitmix64 -> Box-Muller, the generator of the Python tests
+struct Rng {
+  uint64_t s;
+  explicit Rng(uint64_t seed) : s(seed) {}
+  uint64_t next() {
+    uint64_t z = (s += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+  }
+  std::vector<float> normal(size_t n, double std = 1.0) {
+    std::vector<float> v(n);
+    for (size_t i = 0; i < n; i += 2) {
+      const double u1 = (double((next() >> 11)) + 1.0) * 0x1.0p-53;
+      const double u2 = double(next() >> 11) * 0x1.0p-53;
+      const double r = std::sqrt(-2.0 * std::log(u1));
+      v[i] = float(r * std::cos(2.0 * M_PI * u2) * std);
+      if (i + 1 < n) v[i + 1] = float(r * std::sin(2.0 * M_PI * u2) * std);
+    }
+    return v;
+  }
+};
+
+// ---------------------------------------------------------------------------
+// CPU checks
+
+static void cpu_tests() {
+  {
+    infer::expected<int, std::error_code> a = 5;
+    infer::expected<int, std::error_code> b = infer::fail(std::errc::invalid_argument);
+    infer::expected<void, std::error_code> c;
+    CHECK(a && *a == 5 && !b && is_err(b.error(), std::errc::invalid_argument) && c, "expected polyfill");
+  }
+  {
+    auto &reg = BackendRegistry::instance();
+    reg.register_backend(
+        "host", [] { return std::vector<DeviceInfo>{{"host:0", DeviceType::CPU, 1}}; },
+        [](int id, DeviceInfo, const PoolConfig &) -> std::unique_ptr<Backend> {
+          return std::make_unique<HostBackend>(id);
+        });
+    reg.probe_all();
+    auto ok = reg.create("host:0", {});
+    auto missing = reg.create("host:7", {});
+    CHECK(ok && (*ok)->is_host() && !missing && is_err(missing.error(), std::errc::no_such_device),
+          "registry create by name");
+    CHECK(BackendRegistry::extract_type("hip:3") == "hip" && BackendRegistry::extract_device_id("hip:3") == 3 &&
+              BackendRegistry::extract_device_id("cpu") == 0,
+          "registry name parsing");
+  }
+
+  HostBackend be;
+  const size_t L = 3, cap = 16;
+  std::vector<KVLayerSpec> specs(L, KVLayerSpec{8, 128, 128, GGML_TYPE_F32, GGML_TYPE_F32});
+  std::vector<Backend *> place(L, &be);
+  KVCacheManager kv(std::make_unique<ContiguousKVStrategy>(std::make_unique<NaiveKVStorage>()));
+  CHECK(kv.init(specs, place, KVCacheConfig{.layers = L, .max_tokens_per_sequence = cap}), "kv init");
+  auto bad_init = KVCacheManager(std::make_unique<ContiguousKVStrategy>(std::make_unique<NaiveKVStorage>()))
+                      .init(specs, place, KVCacheConfig{.layers = 2, .max_tokens_per_sequence = cap});
+  CHECK(!bad_init && is_err(bad_init.error(), std::errc::invalid_argument), "kv init rejects layer mismatch");
+
+  auto sid = kv.create_sequence();
+  CHECK(sid && *sid == 1 && be.allocs == int(L), "create_sequence allocates one K+V block per layer");
+  const SequenceId id = *sid;
+  auto over = kv.reserve_append(id, cap + 1);
+  CHECK(!over && is_err(over.error(), std::errc::not_enough_memory), "reserve beyond capacity");
+  auto no_pending = kv.acquire_layer(id, 0);
+  CHECK(!no_pending && is_err(no_pending.error(), std::errc::invalid_argument), "acquire without reserve");
+  CHECK(kv.reserve_append(id, 4), "reserve 4");
+  auto busy = kv.reserve_append(id, 1);
+  CHECK(!busy && is_err(busy.error(), std::errc::device_or_resource_busy), "second reserve is busy");
+
+  auto a0 = kv.acquire_layer(id, 0);
+  CHECK(bool(a0), "acquire layer 0");
+  const KVStorage *st = kv.strategy()->storage();
+  const Tensor &rk = a0->readable.k.front().view, &wk = a0->writable.k.front().view;
+  const Tensor &rv = a0->readable.v.front().view;
+  const size_t row = 8 * 128 * 4;
+  CHECK(a0->n_past == 0 && a0->n_new == 4 && rk.dims[0] == 128 && rk.dims[1] == 8 && rk.dims[2] == 4 &&
+            rk.strides[2] == int64_t(row) && wk.data == rk.data &&
+            static_cast<char *>(rv.data) == static_cast<char *>(rk.data) + cap * row &&
+            rk.tensorRole == TensorRole::TENSOR_ROLE_KVCACHE,
+          "views: [128,8,n] token-major, V after K");
+  CHECK(st->state(1) && st->state(1)->active_users == 1, "storage acquired once per access");
+  CHECK(kv.release_layer(*a0) && a0->released() && st->state(1)->active_users == 0, "release_layer");
+  CHECK(kv.release_layer(*a0), "second release is a no-op");
+  CHECK(kv.commit_append(id) && *kv.length(id) == 4, "commit -> length 4");
+  auto no_commit = kv.commit_append(id);
+  CHECK(!no_commit && is_err(no_commit.error(), std::errc::invalid_argument), "commit without pending");
+
+  CHECK(kv.reserve_append(id, 1), "reserve 1 (decode)");
+  auto a1 = kv.acquire_layer(id, 2);
+  CHECK(a1 && a1->n_past == 4 && a1->readable.k.front().view.dims[2] == 5 &&
+            static_cast<char *>(a1->writable.k.front().view.data) ==
+                static_cast<char *>(a1->readable.k.front().view.data) + 4 * row,
+          "decode views: readable [0,5), writable row 4");
+  CHECK(kv.abort_append(id) && *kv.length(id) == 4, "abort keeps length");
+  CHECK(kv.release_layer(*a1) && st->state(3)->active_users == 0, "release after abort");
+
+  // deferred free while an access is outstanding
+  CHECK(kv.reserve_append(id, 1), "reserve after abort");
+  auto a2 = kv.acquire_layer(id, 1);
+  const int frees_before = be.frees;
+  CHECK(kv.release_sequence(id) && be.frees == frees_before + int(L) - 1, "release_sequence defers in-use layer");
+  CHECK(kv.strategy()->release_layer(*a2) && be.frees == frees_before + int(L), "last release frees it");
+  auto gone = kv.length(id);
+  CHECK(!gone && is_err(gone.error(), std::errc::invalid_argument), "released sequence is gone");
+
+  // capacity boundary
+  auto s2 = kv.create_sequence();
+  CHECK(s2 && kv.reserve_append(*s2, cap) && kv.commit_append(*s2), "fill to capacity");
+  auto full = kv.reserve_append(*s2, 1);
+  CHECK(!full && is_err(full.error(), std::errc::not_enough_memory), "no room after capacity");
+  CHECK(kv.reserve_append(*s2, 0), "empty append at capacity");
+  kv.abort_append(*s2);
+
+  // context: busy while accesses are outstanding; theta table matches the oracle
+  {
+    GraphContext ctx(&be);
+    auto s3 = kv.create_sequence();
+    CHECK(ctx.set_kv_cache(&kv, *s3) && kv.reserve_append(*s3, 2), "context bind");
+    auto acc = ctx.acquire_kv_layer(0);
+    auto sw = ctx.set_kv_cache(&kv, *s2);
+    CHECK(acc && !sw && is_err(sw.error(), std::errc::device_or_resource_busy), "context busy while acquired");
+    CHECK(ctx.release_kv_access() && ctx.outstanding_kv_accesses() == 0 && ctx.set_kv_cache(&kv, *s2),
+          "context release then rebind");
+    kv.abort_append(*s3);
+    auto th = ctx.get_rope_theta_table(1e6f, 128, 40960);
+    std::vector<float> want(64 * 40960);
+    oracle_rope_theta_table(1e6f, 128, 40960, want.data());
+    CHECK(th && (*th)->dims[0] == 64 && (*th)->dims[1] == 40960 &&
+              std::memcmp((*th)->data, want.data(), want.size() * 4) == 0,
+          "rope angle table bit-exact with the oracle");
+    auto th2 = ctx.get_rope_theta_table(1e6f, 128, 40960);
+    CHECK(th2 && *th2 == *th, "rope angle table cached");
+  }
+
+  // graph order and append_kv wiring
+  {
+    Graph g;
+    Tensor x("x", GGML_TYPE_F32, {128, 8, 1, 1}), w("w", GGML_TYPE_F32, {128, 1, 1, 1});
+    float xb[1024] = {0}, wb[128] = {0};
+    x.data = xb;
+    w.data = wb;
+    Tensor cache_w("cw", GGML_TYPE_F32, {128, 8, 1, 1}), cache_r("cr", GGML_TYPE_F32, {128, 8, 3, 1});
+    std::vector<float> cache(3 * 1024);
+    cache_r.data = cache.data();
+    cache_w.data = cache.data() + 2 * 1024;
+    Tensor *n = OpFactory::rms_norm(g, &x, &w, 1e-6f, "n");
+    Tensor *view = append_kv(g, n, cache_w, cache_r);
+    g.mark_output(view);
+    CHECK(g.compute() && g.nodes().size() == 3 && g.nodes()[0] == n &&
+              g.nodes()[1]->op == OperationType::GGML_OP_CPY && g.nodes()[2] == view &&
+              view->src[0] == g.nodes()[1] && g.nodes()[1]->src[0] == n && g.nodes()[1]->pinned &&
+              g.nodes()[1]->data == cache_w.data && view->data == cache_r.data && g.leafs().size() == 2,
+          "graph topo order; append_kv = CPY then VIEW over the cache");
+  }
+}
+
+// ---------------------------------------------------------------------------
+// GPU: attention slice on HIPBackend vs the oracle
+
+static bool attn_close(const float *got, const float *want, size_t n, double *worst) {
+  bool ok = true;
+  *worst = 0;
+  for (size_t i = 0; i < n; ++i) {
+    const double e = std::fabs(double(got[i]) - double(want[i]));
+    const double b = 1e-5 + 1e-4 * std::fabs(double(want[i]));
+    if (e > b) ok = false;
+    *worst = std::max(*worst, e - b);
+  }
+  return ok;
+}
+
+static void gpu_tests() {
+  register_hip_backend();
+  auto &reg = BackendRegistry::instance();
+  reg.probe_all();
+  auto created = reg.create("hip:0", {});
+  CHECK(bool(created), "create hip:0");
+  if (!created) return;
+  auto *hip = static_cast<HIPBackend *>(created->get());
+  CHECK(hip->device_type() == DeviceType::HIP && !hip->is_host(), "hip backend identity");
+
+  oracle_set_workers(4);
+  const int Hq = 16, Hkv = 8, D = 128, L = 2, P = 37, N = 5;
+  const size_t cap = P + N + 1;  // one spare row for the bad-position check
+  AttentionSliceParams sp;  // Qwen3-0.6B attention shape
+  std::vector<KVLayerSpec> specs(L, KVLayerSpec{size_t(Hkv), size_t(D), size_t(D)});
+  std::vector<Backend *> place(L, hip);
+  KVCacheManager kv(std::make_unique<ContiguousKVStrategy>(std::make_unique<NaiveKVStorage>()));
+  CHECK(kv.init(specs, place, KVCacheConfig{.layers = L, .max_tokens_per_sequence = cap}), "kv init on hip");
+  auto sid = kv.create_sequence();
+  CHECK(bool(sid), "sequence with HBM caches");
+  CHECK(hip->reserve_decode_workspace(Hq, Hkv, D, cap), "reserve decode workspace");
+
+  Rng rng(0x1F0000 + 7);
+  auto upload = [&](const std::vector<float> &h, std::initializer_list<int64_t> shape, const char *name) {
+    auto t = std::make_unique<Tensor>(name, GGML_TYPE_F32, shape);
+    t->data = *hip->alloc(BufferKind::WEIGHTS, t->byte_size());
+    t->backend = hip;
+    t->device = DeviceType::HIP;
+    t->tensorRole = TensorRole::TENSOR_ROLE_WEIGHT;
+    hip->copy_tensor_set(t.get(), h.data(), 0, h.size() * 4);
+    return t;
+  };
+  std::vector<std::vector<float>> qw(L), kw(L);
+  std::vector<std::unique_ptr<Tensor>> qw_d, kw_d;
+  for (int l = 0; l < L; ++l) {
+    qw[l] = rng.normal(D, 0.5);
+    kw[l] = rng.normal(D, 0.5);
+    for (auto &x : qw[l]) x += 1.0f;
+    for (auto &x : kw[l]) x += 1.0f;
+    qw_d.push_back(upload(qw[l], {D, 1, 1, 1}, "q_norm_w"));
+    kw_d.push_back(upload(kw[l], {D, 1, 1, 1}, "k_norm_w"));
+  }
+
+  // oracle state: host caches per layer
+  std::vector<std::vector<float>> hk(L, std::vector<float>(cap * Hkv * D)), hv = hk;
+  std::vector<float> theta(size_t(64) * sp.n_ctx_train);
+  oracle_rope_theta_table(sp.rope_theta, D, sp.n_ctx_train, theta.data());
+
+  Scheduler sched(hip);
+  GraphContext ctx(nullptr);
+  CHECK(ctx.set_kv_cache(&kv, *sid), "bind context");
+  Tensor *pos_t = ctx.make_tensor("inp_pos", GGML_TYPE_I32, {1});
+  pos_t->device = DeviceType::CPU;
+  pos_t->tensorRole = TensorRole::TNESOR_ROLE_INPUT;
+  ctx.set_input_pos(pos_t);
+  std::vector<int32_t> pos;
+
+  size_t n_past = 0;
+  for (int step = 0; step <= N; ++step) {
+    const int n = step == 0 ? P : 1;
+    const std::string tag = step == 0 ? "prefill" : "decode step " + std::to_string(step);
+    pos.resize(n);
+    for (int i = 0; i < n; ++i) pos[i] = int32_t(n_past + i);
+    pos_t->dims = {n, 1, 1, 1};
+    pos_t->set_contiguous_strides();
+    pos_t->data = pos.data();
+    if (!kv.reserve_append(*sid, n)) {
+      CHECK(false, "reserve");
+      return;
+    }
+    Graph g;
+    std::vector<std::unique_ptr<Tensor>> inputs;
+    std::vector<std::vector<float>> hq(L), hkp(L), hvp(L);
+    std::vector<Tensor *> outs;
+    for (int l = 0; l < L; ++l) {
+      hq[l] = rng.normal(size_t(n) * Hq * D);
+      hkp[l] = rng.normal(size_t(n) * Hkv * D);
+      hvp[l] = rng.normal(size_t(n) * Hkv * D);
+      inputs.push_back(upload(hq[l], {Hq * D, n, 1, 1}, "q_proj"));
+      inputs.push_back(upload(hkp[l], {Hkv * D, n, 1, 1}, "k_proj"));
+      inputs.push_back(upload(hvp[l], {Hkv * D, n, 1, 1}, "v_proj"));
+      auto out = build_attention_slice(g, ctx, inputs[3 * l].get(), inputs[3 * l + 1].get(),
+                                       inputs[3 * l + 2].get(), qw_d[l].get(), kw_d[l].get(), l, sp);
+      if (!out) {
+        CHECK(false, ("build slice " + tag).c_str());
+        return;
+      }
+      g.mark_output(*out);
+      outs.push_back(*out);
+    }
+    auto ex = sched.execute(g);
+    auto sy = hip->synchronize();
+    CHECK(ex && sy, ("execute " + tag).c_str());
+    const auto &stt = hip->last_stats();
+    CHECK(stt.fused_norm_rope == 2 * L && stt.fused_append_decode == (step == 0 ? 0 : L),
+          ("fusions " + tag).c_str());
+
+    for (int l = 0; l < L; ++l) {
+      // oracle: qk-norm -> rope -> append -> attention
+      std::vector<float> qn(hq[l].size()), kn(hkp[l].size()), qr(hq[l].size()), kr(hkp[l].size());
+      oracle_rms_norm_f32(hq[l].data(), qw[l].data(), qn.data(), int64_t(n) * Hq, D, sp.rms_norm_eps);
+      oracle_rms_norm_f32(hkp[l].data(), kw[l].data(), kn.data(), int64_t(n) * Hkv, D, sp.rms_norm_eps);
+      oracle_rope_neox_f32(qn.data(), pos.data(), theta.data(), sp.n_ctx_train, qr.data(), D, Hq, n);
+      oracle_rope_neox_f32(kn.data(), pos.data(), theta.data(), sp.n_ctx_train, kr.data(), D, Hkv, n);
+      oracle_cpy(hk[l].data() + n_past * Hkv * D, kr.data(), kr.size() * 4);
+      oracle_cpy(hv[l].data() + n_past * Hkv * D, hvp[l].data(), hvp[l].size() * 4);
+      std::vector<float> want(size_t(n) * Hq * D), got(want.size());
+      oracle_flash_attn_f32(qr.data(), hk[l].data(), hv[l].data(), want.data(), D, Hq, n, Hkv,
+                            int64_t(n_past + n), int64_t(n_past));
+      hip->copy_tensor_get(outs[l], got.data(), 0, got.size() * 4);
+      double worst;
+      const bool ok = attn_close(got.data(), want.data(), got.size(), &worst);
+      if (!ok) std::printf("  layer %d worst excess %.3e\n", l, worst);
+      CHECK(ok, ("attention within tolerance, layer " + std::to_string(l) + ", " + tag).c_str());
+      // cache bytes: committed prefix + this step's rows, K and V
+      const StorageState *ss = kv.strategy()->storage()->state(StorageId(l + 1));
+      const size_t bytes = (n_past + n) * Hkv * D * 4;
+      std::vector<float> dk(bytes / 4), dv(bytes / 4);
+      (void)hipMemcpy(dk.data(), ss->object.k_base, bytes, hipMemcpyDeviceToHost);
+      (void)hipMemcpy(dv.data(), ss->object.v_base, bytes, hipMemcpyDeviceToHost);
+      CHECK(std::memcmp(dk.data(), hk[l].data(), bytes) == 0 && std::memcmp(dv.data(), hv[l].data(), bytes) == 0,
+            ("cache bit-exact, layer " + std::to_string(l) + ", " + tag).c_str());
+    }
+    CHECK(ctx.release_kv_access() && kv.commit_append(*sid) && *kv.length(*sid) == n_past + n,
+          ("commit " + tag).c_str());
+    for (auto &t : inputs) hip->free(BufferKind::WEIGHTS, t->data);
+    n_past += n;
+  }
+
+  // A position beyond the angle table is reported at synchronize (no fault).
+  {
+    AttentionSliceParams small = sp;
+    small.n_ctx_train = 16;  // table of 16 positions; the next position is 42
+    if (kv.reserve_append(*sid, 1)) {
+      Graph g;
+      pos.assign(1, int32_t(n_past));
+      pos_t->dims = {1, 1, 1, 1};
+      pos_t->set_contiguous_strides();
+      pos_t->data = pos.data();
+      auto q = upload(rng.normal(Hq * D), {Hq * D, 1, 1, 1}, "q");
+      auto k = upload(rng.normal(Hkv * D), {Hkv * D, 1, 1, 1}, "k");
+      auto v = upload(rng.normal(Hkv * D), {Hkv * D, 1, 1, 1}, "v");
+      auto out = build_attention_slice(g, ctx, q.get(), k.get(), v.get(), qw_d[0].get(), kw_d[0].get(), 0, small);
+      if (out) g.mark_output(*out);
+      auto ex = out ? sched.execute(g) : infer::expected<void, std::error_code>(infer::fail(std::errc::io_error));
+      auto sy = hip->synchronize();
+      CHECK(ex && !sy && is_err(sy.error(), std::errc::invalid_argument), "bad RoPE position reported, no fault");
+      CHECK(hip->synchronize(), "status cleared after report");
+      ctx.release_kv_access();
+      kv.abort_append(*sid);
+      for (auto *t : {q.get(), k.get(), v.get()}) hip->free(BufferKind::WEIGHTS, t->data);
+    } else {
+      CHECK(false, "reserve for bad-position check");
+    }
+  }
+  CHECK(kv.release_sequence(*sid), "release sequence (frees HBM caches)");
+  for (auto &t : qw_d) hip->free(BufferKind::WEIGHTS, t->data);
+  for (auto &t : kw_d) hip->free(BufferKind::WEIGHTS, t->data);
+}
+
+int main(int argc, char **argv) {
+  const std::string mode = argc > 1 ? argv[1] : "--cpu";
+  if (mode == "--cpu") cpu_tests();
+  else if (mode == "--gpu") gpu_tests();
+  else {
+    std::fprintf(stderr, "usage: test_engine --cpu | --gpu\n");
+    return 2;
+  }
+  std::printf("%s: %d failure(s)\n", mode.c_str(), g_fail);
+  return g_fail;
+}
