@@ -1,5 +1,5 @@
 // attn_prefill.hip — causal GQA flash attention for n_q >= 1 query tokens on
-// F32 MFMA (v_mfma_f32_32x32x2_f32), never materialising the score matrix.
+// F32 MFMA (v_mfma_f32_16x16x4_f32), never materialising the score matrix.
 //
 // Replaces CUDA_F32::compute_flash_attn for prefill (reference
 // src/kernels/cuda/kernel_f32.cu:452-511), which allocated Hq*n_q*n_kv floats
@@ -8,23 +8,34 @@
 // j <= n_past + t; q head h reads KV head h / G, G = n_head / n_head_kv.
 //
 // Decomposition:
-//   * A workgroup (4 wavefronts) owns one KV head g and 128 query rows, a row
-//     being a (token, q head) pair of that group: 128/G tokens x G heads. The
-//     K/V tiles of head g (32 keys x 128 dims each) are staged once in LDS and
-//     shared by all G query heads, so K/V are read from HBM once per
-//     workgroup, not once per query head.
-//   * Each wavefront owns 32 rows and computes in the transposed form
-//       S^T = K Q^T   (32 keys x 32 rows, contraction over 128 dims)
-//       O^T += V^T P^T (128 dims x 32 rows, contraction over 32 keys)
-//     so that every lane holds one query row (lane % 32) in both products:
-//     row max / row sum of the online softmax are in-lane plus one exchange
-//     between the two half-waves, and the rescale of O^T needs no shuffles.
-//   * The contraction order is chosen so operands come straight from
-//     registers or 16-byte LDS reads: Q is held in registers (64 floats per
-//     lane); each ds_read_b128 of K feeds 4 MFMAs; each ds_read_b128 of V
-//     feeds the 4 output tiles, whose rows are the dims 4i+dt.
-//   * The next K/V tile is prefetched into registers while the current one is
-//     consumed from LDS. Workgroups are issued heaviest query block first.
+//   * A query block is NW*16 rows of one KV head's group: NW*16/G tokens x G
+//     query heads. K/V tiles (32 keys x 128 dims) of that KV head are staged
+//     in LDS once per block and shared by its NW wavefronts, i.e. by all G
+//     query heads. blockIdx % n_head_kv is the KV head, so with 8 KV heads each
+//     XCD (and its L2) serves one KV head.
+//   * Causal balance: a workgroup processes the pair of query blocks (i,
+//     n_blocks-1-i) of its KV head one after the other, so every workgroup
+//     walks the same number of key tiles (the heaviest block alone is twice
+//     the average).
+//   * Each wavefront owns 16 rows and computes, per 32-key tile,
+//       S^T = K Q^T    (2 x [16 keys x 16 rows], contraction over 128 dims)
+//       O^T += V^T P^T (8 x [16 dims x 16 rows], contraction over 32 keys)
+//     so a lane holds one query row (lane % 16) in both products. Operands
+//     come from registers (Q, P) or 16-byte LDS reads (one ds_read_b128 of K
+//     feeds 4 MFMAs); output tile t, register r of lane l holds dim
+//     64*(t/4) + 16*(l/16) + 4r + t%4.
+//   * Tiles move global -> LDS with global_load_lds_dwordx4 (no VGPR
+//     staging) into two LDS buffers: tile t+1 loads while tile t is used.
+//     The DMA writes each wave's 64 x 16 bytes contiguously, so K rows are
+//     stored with 16-byte chunk c at slot c ^ (key % 16): the 16 lanes that
+//     read one chunk index from 16 keys then hit 16 different bank groups.
+//     Keys past n_kv are clamped to the last row (finite data, masked out).
+//   * Softmax runs in base 2 on a per-row reference max that only moves when
+//     a score exceeds it by 2^8 (checked with one wave vote), so most tiles
+//     skip the cross-lane max and the O rescale; row sums stay per lane until
+//     the end. Cross-lane row reductions use v_permlane{32,16}_swap.
+//   * LDS fragment reads run one MFMA group ahead; sched_group_barrier keeps
+//     the compiler from sinking them next to their uses.
 #include "ikv_common.hpp"
 #include "../../include/ikv.h"
 
@@ -32,172 +43,259 @@
 
 namespace {
 
-typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void *lds_ptr;
 
 constexpr int D = 128;
-constexpr int NWAVE = 4;
-constexpr int WG = NWAVE * 64;
-constexpr int ROWS = NWAVE * 32;  // query rows per workgroup
-constexpr int BN = 32;            // keys per tile
-constexpr int KS = D + 4;         // LDS row stride of K (floats): conflict-free 16-byte reads
-constexpr int VS = D;             // LDS row stride of V: each half-wave reads one whole row
+constexpr int BN = 32;              // keys per tile
+constexpr int TILE = BN * D;        // floats of K (or V) per tile
+constexpr float kRescale = 8.0f;    // log2 headroom before the running max is moved
+#ifndef IKV_PREFILL_PAIR_MIN_WGS
+#define IKV_PREFILL_PAIR_MIN_WGS 256  // one workgroup per CU
+#endif
+#ifndef IKV_PREFILL_NW
+#define IKV_PREFILL_NW 0  // waves per workgroup; 0 = chosen per launch
+#endif
 
-__device__ __forceinline__ floatx16 mfma32(float a, float b, floatx16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+__device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-template <int G>
-__global__ __launch_bounds__(WG) void prefill_kernel(const float *__restrict__ q,
-                                                     const float *__restrict__ k,
-                                                     const float *__restrict__ v,
-                                                     float *__restrict__ out, int n_head_kv,
-                                                     int n_q, int n_kv, int n_past, int n_qblocks,
-                                                     float scale_log2) {
-  constexpr int BQ = ROWS / G;  // query tokens per workgroup
-  __shared__ float s_k[BN * KS];
-  __shared__ float s_v[BN * VS];
+// max / sum over the 4 lanes l, l^16, l^32, l^48 (one query row); every lane
+// gets the same bits.
+__device__ __forceinline__ float row_max4(float x) {
+  auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float row_sum4(float x) {
+  auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+template <int G, int NW>
+__global__ __launch_bounds__(NW * 64) void prefill_kernel(const float *__restrict__ q,
+                                                          const float *__restrict__ k,
+                                                          const float *__restrict__ v,
+                                                          float *__restrict__ out, int n_head_kv,
+                                                          int n_q, int n_kv, int n_past,
+                                                          int n_blocks, int paired,
+                                                          float scale_log2) {
+  constexpr int BQ = NW * 16 / G;
+  // [buffer][K | V]; K rows hold 16-byte chunk c at slot c ^ (key & 15)
+  __shared__ __attribute__((aligned(16))) float s_buf0[2 * TILE];
+  __shared__ __attribute__((aligned(16))) float s_buf1[2 * TILE];
 
   const int g = blockIdx.x % n_head_kv;
-  const int qb = n_qblocks - 1 - static_cast<int>(blockIdx.x / n_head_kv);
-  const int q0 = qb * BQ;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int half = lane >> 5;
-  const int j = lane & 31;
-  const int row = wave * 32 + j;
-  const int tok = q0 + row / G;
-  const int head = g * G + row % G;
+  const int item = blockIdx.x / n_head_kv;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kk = lane >> 4;
+  const int j = lane & 15;
+  const int row = wave * 16 + j;
   const int n_head = n_head_kv * G;
-  const bool row_ok = tok < n_q;
 
-  // Q row in registers: qr[u] = Q[tok][head][8u + 4*half .. +3].
-  float4 qr[16];
-  {
-    const float *qp = q + (static_cast<size_t>(row_ok ? tok : 0) * n_head + head) * D + 4 * half;
+  // this wave's share of one tile: chunks c = wave + NW*i, 1 KB (2 keys) each
+  auto issue = [&](float *buf, int tile) {
 #pragma unroll
-    for (int u = 0; u < 16; ++u)
-      qr[u] = row_ok ? *reinterpret_cast<const float4 *>(qp + 8 * u) : make_float4(0.f, 0.f, 0.f, 0.f);
-  }
-
-  const int last_tok = min(q0 + BQ, n_q) - 1;
-  const int k_end = min(n_kv, n_past + last_tok + 1);
-  const int n_tiles = (k_end + BN - 1) / BN;
-
-  floatx16 o0 = {}, o1 = {}, o2 = {}, o3 = {};
-  float m_row = -INFINITY, l_row = 0.f;
-
-  // Cooperative tile load: 32 keys x 32 float4 per K (and V) tile, 4 per thread.
-  float4 pk[4], pv[4];
-  auto load_tile = [&](int tile) {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int idx = tid + WG * c;
-      const int key = idx >> 5;
-      const int c4 = idx & 31;
-      const int kk = tile * BN + key;
-      if (kk < n_kv) {
-        const size_t off = (static_cast<size_t>(kk) * n_head_kv + g) * D + 4 * c4;
-        pk[c] = *reinterpret_cast<const float4 *>(k + off);
-        pv[c] = *reinterpret_cast<const float4 *>(v + off);
-      } else {
-        pk[c] = make_float4(0.f, 0.f, 0.f, 0.f);
-        pv[c] = make_float4(0.f, 0.f, 0.f, 0.f);
-      }
-    }
-  };
-  auto store_tile = [&]() {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int idx = tid + WG * c;
-      const int key = idx >> 5;
-      const int c4 = idx & 31;
-      *reinterpret_cast<float4 *>(&s_k[key * KS + 4 * c4]) = pk[c];
-      *reinterpret_cast<float4 *>(&s_v[key * VS + 4 * c4]) = pv[c];
+    for (int i = 0; i < 16 / NW; ++i) {
+      const int c = wave + NW * i;
+      const int key = 2 * c + (lane >> 5);
+      const int slot = lane & 31;
+      const int kg = min(tile * BN + key, n_kv - 1);
+      const size_t rowoff = (static_cast<size_t>(kg) * n_head_kv + g) * D;
+      __builtin_amdgcn_global_load_lds(k + rowoff + 4 * (slot ^ (key & 15)),
+                                       (lds_ptr)(buf + c * 256), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(v + rowoff + 4 * slot, (lds_ptr)(buf + TILE + c * 256),
+                                       16, 0, 0);
     }
   };
 
-  if (n_tiles > 0) load_tile(0);
-  for (int tile = 0; tile < n_tiles; ++tile) {
-    __syncthreads();
-    store_tile();
-    __syncthreads();
-    if (tile + 1 < n_tiles) load_tile(tile + 1);
-
-    // S^T[key][row] over this tile.
-    floatx16 s = {};
-    const float *krow = &s_k[j * KS + 4 * half];
+  int koff[8];
 #pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      const float4 kv = *reinterpret_cast<const float4 *>(krow + 8 * u);
-      s = mfma32(kv.x, qr[u].x, s);
-      s = mfma32(kv.y, qr[u].y, s);
-      s = mfma32(kv.z, qr[u].z, s);
-      s = mfma32(kv.w, qr[u].w, s);
+  for (int u = 0; u < 8; ++u) koff[u] = j * D + 4 * ((4 * u + kk) ^ j);
+  const int voff = 4 * kk * D + 4 * j;
+
+  const int n_items = paired ? 2 : 1;
+  for (int it = 0; it < n_items; ++it) {
+    const int blk = paired ? (it == 0 ? item : n_blocks - 1 - item) : n_blocks - 1 - item;
+    if (it == 1 && blk == item) break;
+    const int q0 = blk * BQ;
+    const int tok = q0 + row / G;
+    const int head = g * G + row % G;
+    const bool row_ok = tok < n_q;
+    const int last_tok = min(q0 + BQ, n_q) - 1;
+    const int k_end = min(n_kv, n_past + last_tok + 1);
+    const int n_tiles = (k_end + BN - 1) / BN;
+
+    __syncthreads();  // the previous item's readers are done with both buffers
+    issue(s_buf0, 0);
+
+    float4 qr[8];
+    {
+      const float *qp = q + (static_cast<size_t>(row_ok ? tok : 0) * n_head + head) * D + 4 * kk;
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        qr[u] = row_ok ? *reinterpret_cast<const float4 *>(qp + 16 * u) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
 
-    // Register r of lane holds key (r&3) + 4*half + 8*(r>>2) of the tile.
-    const int kbase = tile * BN;
-    const bool need_mask = (kbase + BN - 1 > n_past + q0) || (kbase + BN > n_kv);
-    float mx = m_row;
+    floatx4 o[8];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      float sv = s[r] * scale_log2;
-      if (need_mask) {
-        const int kk = kbase + (r & 3) + 4 * half + 8 * (r >> 2);
-        if (kk > n_past + tok || kk >= n_kv) sv = -INFINITY;
+    for (int t = 0; t < 8; ++t) o[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+    float m_row = -INFINITY, l_part = 0.f;
+
+    auto step = [&](const float *buf, int tile, float *nbuf, bool more) {
+      floatx4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+      // K fragments are read one step ahead so LDS latency hides under MFMAs
+      float4 ka0 = *reinterpret_cast<const float4 *>(buf + koff[0]);
+      float4 ka1 = *reinterpret_cast<const float4 *>(buf + 16 * D + koff[0]);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float4 a0 = ka0, a1 = ka1;
+        if (u < 7) {
+          ka0 = *reinterpret_cast<const float4 *>(buf + koff[u + 1]);
+          ka1 = *reinterpret_cast<const float4 *>(buf + 16 * D + koff[u + 1]);
+        }
+        s0 = mfma16(a0.x, qr[u].x, s0);
+        s1 = mfma16(a1.x, qr[u].x, s1);
+        s0 = mfma16(a0.y, qr[u].y, s0);
+        s1 = mfma16(a1.y, qr[u].y, s1);
+        s0 = mfma16(a0.z, qr[u].z, s0);
+        s1 = mfma16(a1.z, qr[u].z, s1);
+        s0 = mfma16(a0.w, qr[u].w, s0);
+        s1 = mfma16(a1.w, qr[u].w, s1);
       }
-      s[r] = sv;
-      mx = fmaxf(mx, sv);
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float alpha = ikv::fast_exp2(m_row - mx);
-    float psum = 0.f;
+      const float *vb = buf + TILE + voff;
+      float4 va_n = *reinterpret_cast<const float4 *>(vb);
+      float4 vc_n = *reinterpret_cast<const float4 *>(vb + 64);
+      // schedule: K(0) K(1) | MMA(0) K(2) | MMA(1) K(3) | ... | MMA(6) V(0) | MMA(7)
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float p = ikv::fast_exp2(s[r] - mx);
-      s[r] = p;
-      psum += p;
-    }
-    psum += __shfl_xor(psum, 32, 64);
-    l_row = l_row * alpha + psum;
-    m_row = mx;
-    o0 *= alpha;
-    o1 *= alpha;
-    o2 *= alpha;
-    o3 *= alpha;
+      for (int u = 0; u < 7; ++u) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+      if (more) issue(nbuf, tile + 1);
+      const int kbase = tile * BN;
+      float p[8];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        p[r] = s0[r] * scale_log2;
+        p[4 + r] = s1[r] * scale_log2;
+      }
+      if ((kbase + BN - 1 > n_past + q0) || (kbase + BN > n_kv)) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int kg = kbase + 16 * (i >> 2) + 4 * kk + (i & 3);
+          if (kg > n_past + tok || kg >= n_kv) p[i] = -INFINITY;
+        }
+      }
+      float mt = p[0];
+#pragma unroll
+      for (int i = 1; i < 8; ++i) mt = fmaxf(mt, p[i]);
+      // move the row's reference max only when a score exceeds it by 2^8
+      if (__builtin_amdgcn_ballot_w64(mt > m_row + kRescale) != 0) {
+        const float m_new = fmaxf(m_row, row_max4(mt));
+        const float alpha = ikv::fast_exp2(m_row - m_new);
+        m_row = m_new;
+        l_part *= alpha;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) o[t] *= alpha;
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        p[i] = ikv::fast_exp2(p[i] - m_row);
+        l_part += p[i];
+      }
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float4 va = va_n, vc = vc_n;
+          if (4 * st + r < 7) {
+            const int nx = 4 * st + r + 1;
+            va_n = *reinterpret_cast<const float4 *>(vb + (16 * (nx >> 2) + (nx & 3)) * D);
+            vc_n = *reinterpret_cast<const float4 *>(vb + (16 * (nx >> 2) + (nx & 3)) * D + 64);
+          }
+          const float pp = p[4 * st + r];
+          o[0] = mfma16(va.x, pp, o[0]);
+          o[1] = mfma16(va.y, pp, o[1]);
+          o[2] = mfma16(va.z, pp, o[2]);
+          o[3] = mfma16(va.w, pp, o[3]);
+          o[4] = mfma16(vc.x, pp, o[4]);
+          o[5] = mfma16(vc.y, pp, o[5]);
+          o[6] = mfma16(vc.z, pp, o[6]);
+          o[7] = mfma16(vc.w, pp, o[7]);
+        }
+      }
+      // schedule: V(1) | MMA(0) V(2) | ... | MMA(6) | MMA(7)
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+#pragma unroll
+      for (int r = 0; r < 6; ++r) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 8, 1);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 16, 1);
+    };
 
-    // O^T[dim 4i+dt][row] += V^T P^T.
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int key = (r & 3) + 4 * half + 8 * (r >> 2);
-      const float4 vv = *reinterpret_cast<const float4 *>(&s_v[key * VS + 4 * j]);
-      o0 = mfma32(vv.x, s[r], o0);
-      o1 = mfma32(vv.y, s[r], o1);
-      o2 = mfma32(vv.z, s[r], o2);
-      o3 = mfma32(vv.w, s[r], o3);
+    for (int tile = 0; tile < n_tiles; tile += 2) {
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's loads of `tile` landed
+      __syncthreads();                      // everyone's landed; buffer 1 is free
+      step(s_buf0, tile, s_buf1, tile + 1 < n_tiles);
+      if (tile + 1 >= n_tiles) break;
+      __builtin_amdgcn_s_waitcnt(0x0F70);
+      __syncthreads();
+      step(s_buf1, tile + 1, s_buf0, tile + 2 < n_tiles);
     }
-  }
 
-  if (row_ok) {
-    const float inv = 1.0f / l_row;
-    float *op = out + (static_cast<size_t>(tok) * n_head + head) * D;
+    const float l_row = row_sum4(l_part);
+    if (row_ok) {
+      const float inv = 1.0f / l_row;
+      float *op = out + (static_cast<size_t>(tok) * n_head + head) * D;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int i = (r & 3) + 4 * half + 8 * (r >> 2);
-      *reinterpret_cast<float4 *>(op + 4 * i) =
-          make_float4(o0[r] * inv, o1[r] * inv, o2[r] * inv, o3[r] * inv);
+      for (int hh = 0; hh < 2; ++hh) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int d0 = 64 * hh + 16 * kk + 4 * r;
+          *reinterpret_cast<float4 *>(op + d0) =
+              make_float4(o[4 * hh][r] * inv, o[4 * hh + 1][r] * inv, o[4 * hh + 2][r] * inv,
+                          o[4 * hh + 3][r] * inv);
+        }
+      }
     }
   }
 }
 
+template <int G, int NW>
+void launch_nw(const float *q, const float *k, const float *v, float *out, int n_head_kv, int n_q,
+               int n_kv, int n_past, float scale_log2, int paired, hipStream_t s) {
+  constexpr int BQ = NW * 16 / G;
+  const int n_blocks = (n_q + BQ - 1) / BQ;
+  const int items = paired ? (n_blocks + 1) / 2 : n_blocks;
+  prefill_kernel<G, NW><<<n_head_kv * items, NW * 64, 0, s>>>(
+      q, k, v, out, n_head_kv, n_q, n_kv, n_past, n_blocks, paired, scale_log2);
+}
+
+// Shape choice: 4-wave blocks (64 rows) share each staged K/V tile among the
+// most rows; 2-wave blocks are used when 4-wave blocks would leave CUs idle.
+// Pairing balances the causal triangle but halves the workgroup count, so it
+// is used only when the paired grid still gives every CU a workgroup.
 template <int G>
 void launch(const float *q, const float *k, const float *v, float *out, int n_head_kv, int n_q,
             int n_kv, int n_past, float scale_log2, hipStream_t s) {
-  constexpr int BQ = ROWS / G;
-  const int n_qblocks = (n_q + BQ - 1) / BQ;
-  prefill_kernel<G><<<n_head_kv * n_qblocks, WG, 0, s>>>(q, k, v, out, n_head_kv, n_q, n_kv,
-                                                         n_past, n_qblocks, scale_log2);
+  int nw = IKV_PREFILL_NW;
+  auto blocks = [&](int w) { return (n_q + w * 16 / G - 1) / (w * 16 / G); };
+  if (nw == 0) nw = blocks(4) * n_head_kv >= IKV_PREFILL_PAIR_MIN_WGS ? 4 : 2;
+  const int nb = blocks(nw);
+  const int paired = (nb >= 2 && (nb + 1) / 2 * n_head_kv >= IKV_PREFILL_PAIR_MIN_WGS) ? 1 : 0;
+  if (nw == 4)
+    launch_nw<G, 4>(q, k, v, out, n_head_kv, n_q, n_kv, n_past, scale_log2, paired, s);
+  else
+    launch_nw<G, 2>(q, k, v, out, n_head_kv, n_q, n_kv, n_past, scale_log2, paired, s);
 }
 
 }  // namespace

@@ -168,19 +168,19 @@ def run_prefill_case(dev, n_q, n_past, Hq=16, Hkv=8, seed=0):
     return out.cpu().numpy(), want
 
 
-@pytest.mark.parametrize("P", [1, 2, 31, 32, 33, 64, 65, 128, 256, 2048])
+@pytest.mark.parametrize("P", [1, 2, 31, 32, 33, 64, 65, 128, 256, 1024, 2000, 2048])
 def test_prefill_causal_qwen3_06b(dev, P):
     out, want = run_prefill_case(dev, P, 0)
     assert_attn_close(out, want, f"P={P}")
 
 
-@pytest.mark.parametrize("n_q,n_past", [(17, 100), (64, 1000), (3, 4093), (128, 128)])
+@pytest.mark.parametrize("n_q,n_past", [(17, 100), (64, 1000), (3, 4093), (128, 128), (1999, 77)])
 def test_prefill_with_history(dev, n_q, n_past):
     out, want = run_prefill_case(dev, n_q, n_past, seed=2)
     assert_attn_close(out, want, f"n_q={n_q} n_past={n_past}")
 
 
-@pytest.mark.parametrize("Hq,Hkv,P", [(8, 8, 200), (32, 8, 300), (64, 8, 100), (8, 1, 150)])
+@pytest.mark.parametrize("Hq,Hkv,P", [(8, 8, 200), (32, 8, 300), (64, 8, 100), (64, 8, 600), (8, 1, 150)])
 def test_prefill_group_sizes(dev, Hq, Hkv, P):
     out, want = run_prefill_case(dev, P, 0, Hq, Hkv, seed=4)
     assert_attn_close(out, want, f"Hq={Hq} Hkv={Hkv} P={P}")
