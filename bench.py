@@ -209,6 +209,55 @@ def hbm_probes(torch, ikv):
     return res
 
 
+def pmc_per_dispatch(csv_path, kernel_substr):
+    """Mean over dispatches of one counter (summed over its instances) for
+    the kernels whose name contains kernel_substr, from a rocprofv3
+    run_counter_collection.csv."""
+    import collections
+    import csv
+
+    per = collections.defaultdict(float)
+    with open(csv_path) as f:
+        for r in csv.DictReader(f):
+            if kernel_substr in r["Kernel_Name"]:
+                per[r["Dispatch_Id"]] += float(r["Counter_Value"])
+    if not per:
+        raise SystemExit(f"no dispatch of *{kernel_substr}* in {csv_path}")
+    return len(per), sum(per.values()) / len(per)
+
+
+def traffic_summary(fetch_dir, write_dir, cal_fetch_dir, cal_write_dir, ctx):
+    """HBM bytes per decode launch from two rocprofv3 --pmc runs (FETCH_SIZE,
+    WRITE_SIZE, KiB per dispatch), each scaled by what the same counter reads
+    for the --pmc-calibrate copy of known size (256 MiB read and written)."""
+    csv_name = "run_counter_collection.csv"
+    cal_bytes = 256 * 2**20
+    n_f, fetch = pmc_per_dispatch(f"{fetch_dir}/{csv_name}", "decode_kernel")
+    n_w, write = pmc_per_dispatch(f"{write_dir}/{csv_name}", "decode_kernel")
+    _, cal_f = pmc_per_dispatch(f"{cal_fetch_dir}/{csv_name}", "copy")
+    _, cal_w = pmc_per_dispatch(f"{cal_write_dir}/{csv_name}", "copy")
+    f_factor = cal_bytes / (cal_f * 1024)
+    w_factor = cal_bytes / (cal_w * 1024)
+    fetch_b = fetch * 1024 * f_factor
+    write_b = write * 1024 * w_factor
+    return {
+        "ctx": ctx,
+        "workload": "ikv_attn_decode_f32 with fused append, Qwen3-0.6B layer shape (16 q heads, "
+                    f"8 KV heads, head_dim 128), n_kv {ctx + 1}",
+        "kernel": "decode_kernel<2>",
+        "dispatches": {"fetch": n_f, "write": n_w},
+        "fetch_kib_raw": round(fetch, 2),
+        "write_kib_raw": round(write, 2),
+        "fetch_bytes": round(fetch_b),
+        "write_bytes": round(write_b),
+        "hbm_bytes_per_launch": round(fetch_b + write_b),
+        "algorithmic_bytes_per_launch": decode_bytes(ctx),
+        "calibration": {"kernel": "ikv_append_f32 copy of 256 MiB (bench.py --pmc-calibrate)",
+                        "fetch_kib_raw": round(cal_f, 2), "write_kib_raw": round(cal_w, 2),
+                        "fetch_factor": round(f_factor, 5), "write_factor": round(w_factor, 5)},
+    }
+
+
 def cpu_baseline(ctx, seconds):
     """The oracle (restated reference CPU backend) on this host: the same
     decode step (append + attention) of one layer, rotated over 8 layers."""
@@ -258,9 +307,17 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the ctx sweep and prefill")
     ap.add_argument("--eager", action="store_true", help="launch without HIP-graph capture")
+    ap.add_argument("--traffic-from", nargs=4, metavar=("FETCH", "WRITE", "CAL_FETCH", "CAL_WRITE"),
+                    help="summarise four rocprofv3 --pmc output folders into the traffic file "
+                         "(no GPU needed)")
     ap.add_argument("--pmc-calibrate", action="store_true",
                     help="only run 3 copies of 256 MiB through ikv_append_f32 (counter calibration)")
     args = ap.parse_args()
+    if args.traffic_from:
+        t = traffic_summary(*args.traffic_from, ctx=args.ctx)
+        TRAFFIC_FILE.write_text(json.dumps(t, indent=1) + "\n")
+        print(json.dumps(t))
+        return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the hot path has no "
               "multi-GPU leg in this build", file=sys.stderr)

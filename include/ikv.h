@@ -49,8 +49,8 @@ int ikv_append_f32(void *dst_rows, const void *src_rows, size_t n_rows, size_t r
 
 /* ---------------------------------------------------------------------
  * Decode attention, one query token, GQA, split-K over the context, with an
- * optional fused KV append. Enqueues a split kernel and, when the context
- * needs more than one split, a kernel that merges the splits.
+ * optional fused KV append. One kernel launch: the last split of each KV head
+ * to finish merges that head's split partials.
  * Replaces compute_flash_attn for n_q == 1 (src/kernels/cuda/kernel_f32.cu:
  * 452-511; CPU semantics src/backends/cpu_backend.cpp:525-634).
  *
@@ -63,10 +63,13 @@ int ikv_append_f32(void *dst_rows, const void *src_rows, size_t n_rows, size_t r
  *   out      [n_head][head_dim]
  *   scale    softmax scale; <= 0 selects 1/sqrtf(head_dim)
  *   workspace  device memory of ikv_attn_decode_workspace_bytes() bytes
- *            for the split partials; needs no initialisation. Unused, and
- *            may be NULL, when the context fits one split. Launches that
- *            share one workspace must be ordered (same stream); concurrent
- *            ones race.
+ *            for the split partials and one arrival counter per KV head.
+ *            It must be zero-filled once before its first use (hipMemset at
+ *            allocation); every launch leaves the counters at zero, so the
+ *            same workspace serves every later launch and context length.
+ *            Unused, and may be NULL, when the context fits one split.
+ *            Launches that share one workspace must be ordered (same
+ *            stream); concurrent ones race.
  * head_dim must be 128; n_head/n_head_kv must be 1, 2, 4 or 8.
  * ------------------------------------------------------------------- */
 size_t ikv_attn_decode_workspace_bytes(int n_head, int n_head_kv, int head_dim, int64_t n_kv);

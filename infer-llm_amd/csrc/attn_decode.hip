@@ -1,5 +1,5 @@
 // attn_decode.hip — GQA decode attention over the contiguous KV cache, split-K
-// over the context, with the KV append of the new token fused in.
+// over the context, with the KV append of the new token fused in. One launch.
 //
 // Replaces the score + softmax kernel pair of CUDA_F32::compute_flash_attn for
 // one query token (reference src/kernels/cuda/kernel_f32.cu:330-511), which
@@ -8,30 +8,28 @@
 // CPUBackend::compute_flash_attn (src/backends/cpu_backend.cpp:525-634):
 // q head h reads KV head h / (n_head / n_head_kv); softmax(q.k * scale) . v.
 //
-// Two launches, no device-scope fences or atomics:
-//   split kernel  one workgroup (4 wavefronts) per (KV head g, context split).
-//                 blockIdx = split * n_head_kv + g, so with 8 KV heads every
-//                 split of head g lands on XCD g. Each half-wave (32 lanes x
-//                 float4) owns one 512-byte K or V row at a time: coalesced
-//                 16-byte non-temporal loads along the token-major cache
-//                 ([token][kv head][128] F32, 4096 B per token at Qwen3
-//                 shapes), every row read from HBM once and used by all G
-//                 query heads of the group. The next R rows per lane are
-//                 prefetched into registers while the current ones are
-//                 scored. Online softmax in base 2 per half-wave, merged
-//                 across half-waves by lane exchange and across waves through
-//                 LDS. With one split the output is written directly;
-//                 otherwise (max, sum, unnormalised output) per split goes to
-//                 the workspace.
-//   merge kernel  four workgroups per query head rescale and sum the split
-//                 partials in one memory round trip.
-// Why a second launch: the kernel boundary makes the partials of all 8 XCDs
-// visible. Merging inside the split kernel ("last workgroup to arrive merges")
-// was measured on MI355X and is slower than the extra launch at every context
-// length: agent-scope release/acquire fences write back / invalidate the
-// XCD's L2 (buffer_wbl2 / buffer_inv), and device-scope atomics on one
-// counter serialise at about 0.14 us per arriving workgroup, while a kernel
-// boundary in a HIP graph costs about 1.6 us.
+// One workgroup (8 wavefronts) per (KV head g, context split).
+// blockIdx = split * n_head_kv + g, so with 8 KV heads every split of head g
+// lands on XCD g (workgroups are dealt to the 8 XCDs round-robin) and shares
+// that XCD's L2. Each half-wave (32 lanes x float4) owns one 512-byte K or V
+// row at a time: coalesced 16-byte non-temporal loads along the token-major
+// cache ([token][kv head][128] F32, 4096 B per token at Qwen3 shapes), every
+// row read from HBM once and used by all G query heads of the group. The next
+// R rows per lane are prefetched into registers while the current ones are
+// scored. Online softmax in base 2 per half-wave, merged across half-waves by
+// lane exchange and across waves through LDS.
+//
+// Split merge, inside the same launch: every split publishes (max, sum,
+// unnormalised output) for its G query heads with agent-coherent stores, waits
+// for them to complete, and counts itself in the KV head's arrival counter
+// (an agent-scope atomic; one counter per KV head, 256 bytes apart, so the 8
+// heads never contend). The split that arrives last rescales and sums all
+// partials of its head, loading every partial of a chunk of splits before
+// using any (one memory round trip per chunk), writes the output, and resets
+// the counter to zero for the next launch. Nothing waits or spins: every
+// workgroup runs to completion whatever the arrival order. The workspace's
+// counters must be zero before the first launch; each launch leaves them zero.
+//
 // Fused append: the row of the new token (n_kv-1) is read from k_new/v_new
 // instead of the cache, and the workgroup that owns it stores it into the
 // cache unchanged (a 16-byte copy, bit-exact).
@@ -42,39 +40,51 @@
 
 namespace {
 
-constexpr int D = 128;         // head_dim supported by this kernel
-constexpr int NWAVE = 4;       // wavefronts per workgroup
+constexpr int D = 128;  // head_dim supported by this kernel
+#ifndef IKV_DECODE_NWAVE
+#define IKV_DECODE_NWAVE 8
+#endif
+constexpr int NWAVE = IKV_DECODE_NWAVE;  // wavefronts per workgroup
 constexpr int WG = NWAVE * 64;
 #ifndef IKV_DECODE_R
 #define IKV_DECODE_R 4
 #endif
 constexpr int R = IKV_DECODE_R;      // K and V rows per lane per iteration
 constexpr int TILE = NWAVE * 2 * R;  // tokens per workgroup iteration
-constexpr int kMaxSplits = 1024;
 
 #ifndef IKV_DECODE_TARGET_WGS
-// Split-kernel workgroups aimed for: four per CU on MI355X (256 CUs).
-#define IKV_DECODE_TARGET_WGS 1024
+// Workgroups aimed for over all KV heads: one 8-wave workgroup per CU of
+// MI355X's 256 plus one per KV head (33 splits per head with 8 KV heads).
+// Fewer splits keep the merge short (it reads G x splits x 512 B in one
+// workgroup); more would not add bandwidth.
+#define IKV_DECODE_TARGET_WGS 264
 #endif
 #ifndef IKV_DECODE_NT
 #define IKV_DECODE_NT 1  // 1: K/V history read with non-temporal (streaming) loads
 #endif
+
+// The merging workgroup keeps one weight and one sum per (query head of the
+// group, split) in LDS: G * n_splits <= kMergeCap.
+constexpr int kMergeCap = 1024;
+// Partial-output loads in flight per lane while merging (float4 each).
+constexpr int kMergeChunk = 16;
+// Arrival counters: one int per KV head, kCounterStride ints apart.
+constexpr int kCounterStride = 64;
 
 struct Plan {
   int n_splits;
   int tokens_per_split;
 };
 
-Plan plan_for(int n_head_kv, int64_t n_kv) {
-  // Whole tiles per split, as few per split as the target allows: at ctx 4096
-  // (129 tiles per head) every split is one tile and all workgroups are
-  // resident at once. Splits stay below 2*target <= kMaxSplits.
+Plan plan_for(int n_head, int n_head_kv, int64_t n_kv) {
+  // Whole tiles per split; at most `target` splits per KV head, and at most
+  // kMergeCap / G so that the merge's weights fit in LDS.
+  const int G = n_head / n_head_kv;
   int64_t target = (IKV_DECODE_TARGET_WGS + n_head_kv - 1) / n_head_kv;
+  if (target > kMergeCap / G) target = kMergeCap / G;
   if (target < 1) target = 1;
-  if (target > kMaxSplits / 2) target = kMaxSplits / 2;
   const int64_t n_tiles = (n_kv + TILE - 1) / TILE;
-  int64_t tiles_per_split = n_tiles / target;
-  if (tiles_per_split < 1) tiles_per_split = 1;
+  const int64_t tiles_per_split = (n_tiles + target - 1) / target;
   const int64_t tokens = tiles_per_split * TILE;
   const int64_t splits = (n_kv + tokens - 1) / tokens;
   return {static_cast<int>(splits), static_cast<int>(tokens)};
@@ -83,16 +93,53 @@ Plan plan_for(int n_head_kv, int64_t n_kv) {
 size_t align256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
 
 struct WsLayout {
-  size_t part_ml, part_o, total;
+  size_t counters, part_ml, part_o, total;
 };
 
-// [n_head x n_splits x (max, sum)][n_head x n_splits x D]
-WsLayout ws_layout(int n_head, int n_splits) {
+// [n_head_kv counters, 256 B apart][n_head x n_splits x (max, sum)]
+// [n_head x n_splits x D]. The counters sit at offset 0 for every n_kv, so one
+// workspace serves every context length.
+WsLayout ws_layout(int n_head, int n_head_kv, int n_splits) {
   WsLayout w;
-  w.part_ml = 0;
-  w.part_o = align256(sizeof(float) * 2 * static_cast<size_t>(n_head) * n_splits);
+  w.counters = 0;
+  w.part_ml = align256(sizeof(int) * kCounterStride * static_cast<size_t>(n_head_kv));
+  w.part_o = w.part_ml + align256(sizeof(float) * 2 * static_cast<size_t>(n_head) * n_splits);
   w.total = w.part_o + sizeof(float) * static_cast<size_t>(n_head) * n_splits * D;
   return w;
+}
+
+// Stores and loads of the split partials, coherent across the XCDs of the
+// device (agent scope): the stores are performed at the device's coherence
+// point and the loads (sc1) read from it, so no L2 writeback or invalidate
+// is needed on either side.
+__device__ __forceinline__ void store_agent(float *p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// A (max, sum) pair as one 8-byte store.
+__device__ __forceinline__ void store2_agent(float *p, float a, float b) {
+  const unsigned long long u = static_cast<unsigned long long>(__float_as_uint(a)) |
+                               (static_cast<unsigned long long>(__float_as_uint(b)) << 32);
+  __hip_atomic_store(reinterpret_cast<unsigned long long *>(p), u, __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Agent-coherent 8- and 16-byte loads through a buffer resource over the
+// partials (raw buffer: loads past num_records return zeros).
+constexpr int kBufWord3 = 0x00020000;  // raw dword buffer, gfx9 family
+constexpr int kCpolSc1 = 16;           // cache policy: agent scope
+typedef float f2v __attribute__((ext_vector_type(2)));
+typedef float f4v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t partial_rsrc(const float *base, size_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), 0,
+                                           static_cast<int>(bytes), kBufWord3);
+}
+__device__ __forceinline__ float2 load2_agent(__amdgpu_buffer_rsrc_t r, unsigned byte_off) {
+  const f2v v = __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, kCpolSc1);
+  return make_float2(v.x, v.y);
+}
+__device__ __forceinline__ float4 load4_agent(__amdgpu_buffer_rsrc_t r, unsigned byte_off) {
+  const f4v v = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kCpolSc1);
+  return make_float4(v.x, v.y, v.z, v.w);
 }
 
 template <int G>
@@ -108,7 +155,6 @@ __device__ __forceinline__ void load_rows(float4 (&kr)[R], float4 (&vr)[R], int 
       const float *kp = fresh ? k_new + head_off : kc + static_cast<size_t>(t) * tok_stride + head_off;
       const float *vp = fresh ? v_new + head_off : vc + static_cast<size_t>(t) * tok_stride + head_off;
 #if IKV_DECODE_NT
-      typedef float f4v __attribute__((ext_vector_type(4)));
       const f4v a = __builtin_nontemporal_load(reinterpret_cast<const f4v *>(kp));
       const f4v b = __builtin_nontemporal_load(reinterpret_cast<const f4v *>(vp));
       kr[r] = make_float4(a.x, a.y, a.z, a.w);
@@ -145,14 +191,122 @@ __device__ __forceinline__ void merge_waves(const float (&s_acc)[NWAVE][G][D],
   }
 }
 
+// LDS of the merging workgroup.
+struct MergeLds {
+  float w[kMergeCap];    // per (h, split): max, then the weight 2^(max - M_h)
+  float l[kMergeCap];    // per (h, split): sum
+  float part[WG / 32 * D];  // per (lane group p, h, d): partial sums of the output
+  float L[8];            // per h: sum of the weighted split sums
+};
+
+// Run by the last split of KV head g to arrive: out = sum_s w_s O_s / sum_s w_s l_s
+// over the n_splits partials of each of the G query heads. The statistics and
+// the first chunk of partial outputs are loaded together, so a context whose
+// splits fit one chunk costs one memory round trip.
 template <int G>
-__global__ __launch_bounds__(WG) void decode_split_kernel(
+__device__ void merge_splits(const float *part_ml, const float *part_o, float *out, int g,
+                             int n_splits, MergeLds &lds) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int S = n_splits;
+  // Lane (p, hh, c) sums float4 column c of query head hh over splits
+  // p, p + P, ...
+  constexpr int P = WG / (32 * G);
+  const int c = tid & 31;
+  const int hh = (tid >> 5) % G;
+  const int p = tid / (32 * G);
+  // This KV head's partials: G x S (max, sum) pairs and G x S x D outputs.
+  const __amdgpu_buffer_rsrc_t rml =
+      partial_rsrc(part_ml + static_cast<size_t>(g * G) * S * 2, sizeof(float) * 2 * G * S);
+  const __amdgpu_buffer_rsrc_t ro =
+      partial_rsrc(part_o + static_cast<size_t>(g * G) * S * D, sizeof(float) * G * S * D);
+  const unsigned o_base = static_cast<unsigned>(sizeof(float) * (hh * S * D + 4 * c));
+
+  // The partials were published with agent-coherent stores before their
+  // workgroups were counted; agent-coherent loads observe them.
+  constexpr int kStat = (kMergeCap + WG - 1) / WG;  // (max, sum) pairs per lane
+  float2 st[kStat];
+#pragma unroll
+  for (int k = 0; k < kStat; ++k) {
+    const int i = tid + k * WG;
+    st[k] = (i < G * S) ? load2_agent(rml, static_cast<unsigned>(sizeof(float) * 2 * i))
+                        : make_float2(-INFINITY, 0.f);
+  }
+  float4 v[kMergeChunk];
+#pragma unroll
+  for (int j = 0; j < kMergeChunk; ++j) {
+    const int s = p + j * P;
+    v[j] = (s < S) ? load4_agent(ro, o_base + static_cast<unsigned>(sizeof(float) * s * D))
+                   : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+#pragma unroll
+  for (int k = 0; k < kStat; ++k) {
+    const int i = tid + k * WG;
+    if (i < G * S) {
+      lds.w[i] = st[k].x;
+      lds.l[i] = st[k].y;
+    }
+  }
+  __syncthreads();
+  for (int h = wave; h < G; h += NWAVE) {
+    float mx = -INFINITY;
+    for (int s = lane; s < S; s += 64) mx = fmaxf(mx, lds.w[h * S + s]);
+    mx = ikv::wave_max(mx);
+    float lsum = 0.f;
+    for (int s = lane; s < S; s += 64) {
+      const float m = lds.w[h * S + s];
+      const float w = (m == -INFINITY) ? 0.f : ikv::fast_exp2(m - mx);
+      lds.w[h * S + s] = w;
+      lsum += lds.l[h * S + s] * w;
+    }
+    lsum = ikv::wave_sum(lsum);
+    if (lane == 0) lds.L[h] = lsum;
+  }
+  __syncthreads();
+
+  const float *wrow = lds.w + hh * S;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int j = 0; j < kMergeChunk; ++j) {
+    const int s = p + j * P;
+    if (s < S) acc = ikv::fma4(wrow[s], v[j], acc);
+  }
+  for (int s0 = p + P * kMergeChunk; s0 < S; s0 += P * kMergeChunk) {
+#pragma unroll
+    for (int j = 0; j < kMergeChunk; ++j) {
+      const int s = s0 + j * P;
+      v[j] = (s < S) ? load4_agent(ro, o_base + static_cast<unsigned>(sizeof(float) * s * D))
+                     : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int j = 0; j < kMergeChunk; ++j) {
+      const int s = s0 + j * P;
+      if (s < S) acc = ikv::fma4(wrow[s], v[j], acc);
+    }
+  }
+  *reinterpret_cast<float4 *>(&lds.part[(p * G + hh) * D + 4 * c]) = acc;
+  __syncthreads();
+  for (int i = tid; i < G * D; i += WG) {
+    const int h = i / D;
+    const int d = i - h * D;
+    float o = 0.f;
+#pragma unroll
+    for (int q = 0; q < P; ++q) o += lds.part[(q * G + h) * D + d];
+    out[static_cast<size_t>(g * G + h) * D + d] = o / lds.L[h];
+  }
+}
+
+template <int G>
+__global__ __launch_bounds__(WG) void decode_kernel(
     const float *__restrict__ q, float *kc, float *vc, const float *k_new, const float *v_new,
-    float *__restrict__ out, float *__restrict__ part_ml, float *__restrict__ part_o,
-    int n_head_kv, int n_kv, int tokens_per_split, int n_splits, float scale_log2) {
+    float *__restrict__ out, int *counters, float *part_ml, float *part_o, int n_head_kv, int n_kv,
+    int tokens_per_split, int n_splits, float scale_log2) {
   __shared__ float s_acc[NWAVE][G][D];
   __shared__ float s_m[NWAVE][G];
   __shared__ float s_l[NWAVE][G];
+  __shared__ MergeLds s_merge;
+  __shared__ int s_last;
 
   const int g = blockIdx.x % n_head_kv;
   const int split = blockIdx.x / n_head_kv;
@@ -284,127 +438,47 @@ __global__ __launch_bounds__(WG) void decode_split_kernel(
     float O, L, M;
     merge_waves<G>(s_acc, s_m, s_l, h, d, O, L, M);
     const size_t slot = static_cast<size_t>(g * G + h) * n_splits + split;
-    part_o[slot * D + d] = O;
-    if (d == 0) {
-      part_ml[2 * slot] = M;
-      part_ml[2 * slot + 1] = L;
-    }
+    store_agent(part_o + slot * D + d, O);
+    if (d == 0) store2_agent(part_ml + 2 * slot, M, L);
   }
-}
-
-// Merge of the split partials: 4 workgroups per query head, each owning 32
-// dims. Thread (grp, dd) of 8 x 32 sums splits grp, grp+8, ... for dim dd.
-// All partial loads of a chunk of 256 splits are issued before any is used,
-// so a chunk costs one memory round trip.
-constexpr int kMergeThreads = 256;
-constexpr int kMergeDims = 32;
-constexpr int kMergeGroups = kMergeThreads / kMergeDims;  // 8
-constexpr int kMergeChunk = 256;                          // splits per round trip
-constexpr int kMergeJ = kMergeChunk / kMergeGroups;       // 32 loads per thread
-
-__global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
-    const float *__restrict__ part_ml, const float *__restrict__ part_o, float *__restrict__ out,
-    int n_splits) {
-  __shared__ float s_w[kMaxSplits];
-  __shared__ float s_red[kMergeGroups][kMergeDims];
-  __shared__ float s_stat[4];
-  const int qh = blockIdx.x / (D / kMergeDims);
-  const int d0 = (blockIdx.x % (D / kMergeDims)) * kMergeDims;
-  const int tid = threadIdx.x;
-  const int grp = tid / kMergeDims;
-  const int dd = tid % kMergeDims;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const float *ml = part_ml + static_cast<size_t>(qh) * n_splits * 2;
-  const float *po = part_o + static_cast<size_t>(qh) * n_splits * D + d0 + dd;
-
-  float v[kMergeJ];
-#pragma unroll
-  for (int j = 0; j < kMergeJ; ++j) {
-    const int s = grp + kMergeGroups * j;
-    v[j] = (s < n_splits) ? po[static_cast<size_t>(s) * D] : 0.f;
-  }
-  // Split statistics, one (max, sum) pair per split, loaded together with the
-  // partials above: weights 2^(m - M) and the weighted sum of l.
-  float2 st[kMergeChunk / kMergeThreads];
-#pragma unroll
-  for (int k = 0; k < kMergeChunk / kMergeThreads; ++k) {
-    const int i = tid + k * kMergeThreads;
-    st[k] = (i < n_splits) ? reinterpret_cast<const float2 *>(ml)[i] : make_float2(-INFINITY, 0.f);
-  }
-  float mloc = -INFINITY;
-  for (int i = tid + kMergeChunk; i < n_splits; i += kMergeThreads) mloc = fmaxf(mloc, ml[2 * i]);
-#pragma unroll
-  for (int k = 0; k < kMergeChunk / kMergeThreads; ++k) mloc = fmaxf(mloc, st[k].x);
-  mloc = ikv::wave_max(mloc);
-  if (lane == 0) s_stat[wave] = mloc;
+  // Publish: this lane's partial stores have completed (vmcnt counts stores
+  // on CDNA) before the workgroup's arrival is counted.
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __syncthreads();
-  const float M = fmaxf(fmaxf(s_stat[0], s_stat[1]), fmaxf(s_stat[2], s_stat[3]));
-  float lsum = 0.f;
-#pragma unroll
-  for (int k = 0; k < kMergeChunk / kMergeThreads; ++k) {
-    const int i = tid + k * kMergeThreads;
-    if (i < n_splits) {
-      const float w = ikv::fast_exp2(st[k].x - M);
-      s_w[i] = w;
-      lsum += st[k].y * w;
-    }
+  if (tid == 0) {
+    int *ctr = counters + static_cast<size_t>(g) * kCounterStride;
+    const int before = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = (before == n_splits - 1);
+    if (s_last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  for (int i = tid + kMergeChunk; i < n_splits; i += kMergeThreads) {
-    const float w = ikv::fast_exp2(ml[2 * i] - M);
-    s_w[i] = w;
-    lsum += ml[2 * i + 1] * w;
-  }
-  lsum = ikv::wave_sum(lsum);
   __syncthreads();
-  if (lane == 0) s_stat[wave] = lsum;
-  __syncthreads();
-  const float inv = 1.0f / ((s_stat[0] + s_stat[1]) + (s_stat[2] + s_stat[3]));
-
-  float acc = 0.f;
-#pragma unroll
-  for (int j = 0; j < kMergeJ; ++j) {
-    const int s = grp + kMergeGroups * j;
-    if (s < n_splits) acc += v[j] * s_w[s];
-  }
-  for (int base = kMergeChunk; base < n_splits; base += kMergeChunk) {
-#pragma unroll
-    for (int j = 0; j < kMergeJ; ++j) {
-      const int s = base + grp + kMergeGroups * j;
-      v[j] = (s < n_splits) ? po[static_cast<size_t>(s) * D] : 0.f;
-    }
-#pragma unroll
-    for (int j = 0; j < kMergeJ; ++j) {
-      const int s = base + grp + kMergeGroups * j;
-      if (s < n_splits) acc += v[j] * s_w[s];
-    }
-  }
-  s_red[grp][dd] = acc;
-  __syncthreads();
-  if (grp == 0) {
-    float o = 0.f;
-#pragma unroll
-    for (int k = 0; k < kMergeGroups; ++k) o += s_red[k][dd];
-    out[static_cast<size_t>(qh) * D + d0 + dd] = o * inv;
-  }
+  if (!s_last) return;
+  merge_splits<G>(part_ml, part_o, out, g, n_splits, s_merge);
 }
 
 template <int G>
-void launch_split(const float *q, float *kc, float *vc, const float *kn, const float *vn,
-                  float *out, float *part_ml, float *part_o, int n_head_kv, int n_kv,
-                  const Plan &p, float scale_log2, hipStream_t s) {
-  decode_split_kernel<G><<<n_head_kv * p.n_splits, WG, 0, s>>>(
-      q, kc, vc, kn, vn, out, part_ml, part_o, n_head_kv, n_kv, p.tokens_per_split, p.n_splits,
-      scale_log2);
+void launch(const float *q, float *kc, float *vc, const float *kn, const float *vn, float *out,
+            int *counters, float *part_ml, float *part_o, int n_head_kv, int n_kv, const Plan &p,
+            float scale_log2, hipStream_t s) {
+  decode_kernel<G><<<n_head_kv * p.n_splits, WG, 0, s>>>(q, kc, vc, kn, vn, out, counters,
+                                                          part_ml, part_o, n_head_kv, n_kv,
+                                                          p.tokens_per_split, p.n_splits,
+                                                          scale_log2);
 }
+
+bool supported_group(int G) { return G == 1 || G == 2 || G == 4 || G == 8; }
 
 }  // namespace
 
 extern "C" size_t ikv_attn_decode_workspace_bytes(int n_head, int n_head_kv, int head_dim,
                                                   int64_t n_kv) {
-  if (n_head <= 0 || n_head_kv <= 0 || head_dim != D || n_kv <= 0) return 0;
-  const Plan p = plan_for(n_head_kv, n_kv);
-  return ws_layout(n_head, p.n_splits).total;
+  if (n_head <= 0 || n_head_kv <= 0 || n_head % n_head_kv != 0 || head_dim != D || n_kv <= 0)
+    return 0;
+  if (!supported_group(n_head / n_head_kv) || n_kv > INT_MAX - 2 * TILE) return 0;
+  const Plan p = plan_for(n_head, n_head_kv, n_kv);
+  return ws_layout(n_head, n_head_kv, p.n_splits).total;
 }
 
 extern "C" int ikv_attn_decode_f32(const float *q, float *k_cache, float *v_cache,
@@ -417,31 +491,31 @@ extern "C" int ikv_attn_decode_f32(const float *q, float *k_cache, float *v_cach
   if (n_kv <= 0) return -EINVAL;
   if (head_dim != D) return -ENOTSUP;
   const int G = n_head / n_head_kv;
-  if (G != 1 && G != 2 && G != 4 && G != 8) return -ENOTSUP;
+  if (!supported_group(G)) return -ENOTSUP;
   if (n_kv > INT_MAX - 2 * TILE) return -EOVERFLOW;
   if (!ikv::aligned16(q) || !ikv::aligned16(k_cache) || !ikv::aligned16(v_cache) ||
       !ikv::aligned16(out) || (k_new && (!ikv::aligned16(k_new) || !ikv::aligned16(v_new))))
     return -EINVAL;
-  const Plan p = plan_for(n_head_kv, n_kv);
-  const WsLayout L = ws_layout(n_head, p.n_splits);
+  const Plan p = plan_for(n_head, n_head_kv, n_kv);
+  const WsLayout L = ws_layout(n_head, n_head_kv, p.n_splits);
+  int *counters = nullptr;
   float *part_ml = nullptr, *part_o = nullptr;
   if (p.n_splits > 1) {
     if (!workspace || workspace_bytes < L.total || !ikv::aligned16(workspace)) return -EINVAL;
-    part_ml = reinterpret_cast<float *>(static_cast<char *>(workspace) + L.part_ml);
-    part_o = reinterpret_cast<float *>(static_cast<char *>(workspace) + L.part_o);
+    char *base = static_cast<char *>(workspace);
+    counters = reinterpret_cast<int *>(base + L.counters);
+    part_ml = reinterpret_cast<float *>(base + L.part_ml);
+    part_o = reinterpret_cast<float *>(base + L.part_o);
   }
   if (!(scale > 0.0f)) scale = 1.0f / sqrtf(static_cast<float>(head_dim));
   const float sl2 = scale * ikv::kLog2e;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int nk = static_cast<int>(n_kv);
   switch (G) {
-    case 1: launch_split<1>(q, k_cache, v_cache, k_new, v_new, out, part_ml, part_o, n_head_kv, nk, p, sl2, s); break;
-    case 2: launch_split<2>(q, k_cache, v_cache, k_new, v_new, out, part_ml, part_o, n_head_kv, nk, p, sl2, s); break;
-    case 4: launch_split<4>(q, k_cache, v_cache, k_new, v_new, out, part_ml, part_o, n_head_kv, nk, p, sl2, s); break;
-    default: launch_split<8>(q, k_cache, v_cache, k_new, v_new, out, part_ml, part_o, n_head_kv, nk, p, sl2, s); break;
+    case 1: launch<1>(q, k_cache, v_cache, k_new, v_new, out, counters, part_ml, part_o, n_head_kv, nk, p, sl2, s); break;
+    case 2: launch<2>(q, k_cache, v_cache, k_new, v_new, out, counters, part_ml, part_o, n_head_kv, nk, p, sl2, s); break;
+    case 4: launch<4>(q, k_cache, v_cache, k_new, v_new, out, counters, part_ml, part_o, n_head_kv, nk, p, sl2, s); break;
+    default: launch<8>(q, k_cache, v_cache, k_new, v_new, out, counters, part_ml, part_o, n_head_kv, nk, p, sl2, s); break;
   }
-  if (p.n_splits > 1)
-    decode_merge_kernel<<<n_head * (D / kMergeDims), kMergeThreads, 0, s>>>(part_ml, part_o, out,
-                                                                          p.n_splits);
   return ikv::launch_status();
 }

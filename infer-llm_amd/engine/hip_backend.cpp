@@ -210,6 +210,14 @@ infer::expected<void, std::error_code> HIPBackend::ensure_workspace(size_t bytes
     _workspace = nullptr;
     return infer::fail(std::errc::not_enough_memory);
   }
+  // The decode kernel's arrival counters live in the workspace and must start
+  // at zero; every launch leaves them at zero again.
+  if (hipMemset(_workspace, 0, bytes) != hipSuccess) {
+    (void)hipGetLastError();
+    (void)hipFree(_workspace);
+    _workspace = nullptr;
+    return infer::fail(std::errc::io_error);
+  }
   _workspace_bytes = bytes;
   return {};
 }
