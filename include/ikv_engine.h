@@ -1,0 +1,83 @@
+/*
+ * ikv_engine.h — C-ABI of the engine level: a Qwen3 model on the HIP backend
+ * and the benchmark runner's greedy generation loop.
+ *
+ * This is the caller of the KV-cache path at model level. It stands in for
+ * what the reference's benchmark drives through C++ (ModelBase::load_model /
+ * load_weight, src/model.cpp:60-311; Runner::evaluate and run,
+ * benchmarks/cpu/bench.cpp:130-281), so that tests and bench.py can run a
+ * whole model from Python: the graph is Qwen3Model::build_graph
+ * (src/models/Qwen3.cpp:4-136), executed by the engine's Scheduler on
+ * HIPBackend, KV cache in HBM through KVCacheManager / ContiguousKVStrategy /
+ * NaiveKVStorage.
+ *
+ * Unlike include/ikv.h, these entry points allocate: the model's weights,
+ * KV caches and activation arena live in device memory until
+ * ikv_qwen3_destroy. Return values: 0, or a negative errno.
+ */
+#ifndef IKV_ENGINE_H
+#define IKV_ENGINE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Hyperparameters (the GGUF keys of src/model.cpp:60-163). */
+typedef struct ikv_qwen3_config {
+    uint32_t n_layer, n_embd, n_head, n_head_kv, head_dim, n_ff, n_vocab, n_ctx_train;
+    float rope_theta, rms_norm_eps;
+} ikv_qwen3_config;
+
+/* TTFT and TPOT as benchmarks/cpu/bench.cpp:239-281 defines them:
+ * ttft = first sampled token - start, tpot = (last - first) / (n_gen - 1);
+ * build / execute / sample: graph construction, scheduling + enqueue, and
+ * device argmax + token read-back (which waits for the step's kernels),
+ * summed over steps. */
+typedef struct ikv_qwen3_timing {
+    double ttft_s, tpot_s, wall_s, build_s, execute_s, sample_s;
+} ikv_qwen3_timing;
+
+typedef struct ikv_qwen3 ikv_qwen3;
+
+/* Creates the model on HIP device `device` with weights allocated (not yet
+ * initialised) and a KV cache of max_ctx tokens per layer. */
+int ikv_qwen3_create(const ikv_qwen3_config *cfg, int device, int64_t max_ctx, ikv_qwen3 **out);
+
+/* Weight tensors by GGUF name (ModelBase::load_weight, src/model.cpp:
+ * 164-311): "token_embd.weight", "blk.<i>.attn_q.weight", ...,
+ * "output_norm.weight"; the output projection is the tied token embedding.
+ * Index order is the synthetic initialiser's draw order. */
+int ikv_qwen3_tensor_count(const ikv_qwen3 *m);
+const char *ikv_qwen3_tensor_name(const ikv_qwen3 *m, int index);
+/* Element count of a named tensor, or 0 when the name is unknown. */
+size_t ikv_qwen3_tensor_size(const ikv_qwen3 *m, const char *name);
+int ikv_qwen3_set_tensor(ikv_qwen3 *m, const char *name, const float *host, size_t count);
+/* Random-init weights of the benchmark configurations: every matrix
+ * N(0, std^2) drawn from one ikv_synth_normal_f32 stream in tensor order,
+ * every norm weight 1.0. */
+int ikv_qwen3_init_synthetic(ikv_qwen3 *m, uint64_t seed, double std, int threads);
+
+/* Greedy generation: prompt, then n_gen tokens (the first from the prompt's
+ * last logits row, each next one from feeding back the previous token).
+ * tokens_out holds n_gen ids. Each call starts a new sequence. */
+int ikv_qwen3_generate(ikv_qwen3 *m, const int32_t *prompt, int64_t n_prompt, int64_t n_gen,
+                       int32_t *tokens_out, ikv_qwen3_timing *timing);
+
+/* Fusions taken and kernel launches in the last step. */
+typedef struct ikv_qwen3_stats {
+    int launches, fused_norm_rope, fused_append_decode, fused_swiglu, fused_residual, fused_qkv;
+} ikv_qwen3_stats;
+int ikv_qwen3_last_stats(const ikv_qwen3 *m, ikv_qwen3_stats *out);
+/* 0 disables the HIP backend's graph fusions (every node its own launch). */
+int ikv_qwen3_set_fusion(ikv_qwen3 *m, int on);
+
+void ikv_qwen3_destroy(ikv_qwen3 *m);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* IKV_ENGINE_H */

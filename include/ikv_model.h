@@ -1,0 +1,95 @@
+/*
+ * ikv_model.h — C-ABI of the ops around the KV-cache path that a whole
+ * Qwen3 step needs on the MI355X (gfx950): the projections (mul_mat), the
+ * token-embedding gather, the elementwise ops of the FFN and residuals, the
+ * greedy sampler, and the synthetic weight initialiser of the benchmarks.
+ *
+ * These replace the reference's CPU / CUDA ops of the same names
+ * (src/backends/cpu_backend.cpp:259-332, 386-424, 636-703;
+ * src/kernels/cuda/kernel_f32.cu:94-205, 515-630; src/sampler.cpp:42-65) so
+ * that the scheduler keeps a whole Qwen3 graph on the HIP backend instead of
+ * copying weights to the CPU every step (src/scheduler.cpp:67-69).
+ * Conventions as in ikv.h: device pointers unless a name ends in _host,
+ * stream as void*, 0 / negative errno / positive hipError_t, F32 row-major
+ * with the reference Tensor layout (dims[0] innermost).
+ */
+#ifndef IKV_MODEL_H
+#define IKV_MODEL_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------------------------------------------------------------
+ * mul_mat: out[m][n] = sum_k x[m][k] * w[n][k]   (w: [n_out][k] rows, the
+ * ggml [K, N] weight of CPUBackend::compute_mul_mat,
+ * src/backends/cpu_backend.cpp:386-424; x: [m][k]; out: [m][n_out]).
+ * m == 1 (decode) runs a hand-written streaming GEMV; m > 1 runs rocBLAS
+ * SGEMM (full F32). The first m > 1 call on a device creates that device's
+ * rocBLAS handle (kept until exit); calls that share a device must come
+ * from one host thread at a time.
+ * residual: NULL, or [m][n_out] added to the result (out may equal residual
+ * for m == 1).
+ * ------------------------------------------------------------------- */
+int ikv_mul_mat_f32(const float *w, const float *x, float *out, int64_t n_out, int64_t k,
+                    int64_t m, const float *residual, void *stream);
+
+/* Three projections of one input in one launch (the q, k, v projections of
+ * a Qwen3 layer, src/models/Qwen3.cpp:56-58), m == 1:
+ * out_i = w_i · x for i = 0, 1, 2 with w_i [n_i][k]. */
+int ikv_gemv3_f32(const float *w0, const float *w1, const float *w2, const float *x, float *out0,
+                  float *out1, float *out2, int64_t n0, int64_t n1, int64_t n2, int64_t k,
+                  void *stream);
+
+/* SwiGLU FFN input, m == 1: out[n] = (w_up[n] · x) * silu(w_gate[n] · x) —
+ * mul_mat(ffn_gate), mul_mat(ffn_up), silu, mul of Qwen3Model::build_graph
+ * (src/models/Qwen3.cpp:103-113) in one launch; silu(g) = g / (1 + exp(-g))
+ * (src/backends/cpu_backend.cpp:660-673). */
+int ikv_gemv_swiglu_f32(const float *w_gate, const float *w_up, const float *x, float *out,
+                        int64_t n_out, int64_t k, void *stream);
+
+/* ---------------------------------------------------------------------
+ * get_rows: out[i][:] = table[ids[i]][:] for i < n_ids, rows of row_len
+ * floats (CPUBackend::compute_get_rows, src/backends/cpu_backend.cpp:
+ * 259-332; the token embedding). An id outside [0, n_rows) does not fault:
+ * its output row is zeros and *status (device int, if non-NULL) is set to 1.
+ * ------------------------------------------------------------------- */
+int ikv_get_rows_f32(const float *table, const int32_t *ids, float *out, int64_t n_ids,
+                     int64_t row_len, int64_t n_rows, int *status, void *stream);
+
+/* Elementwise over n floats (src/backends/cpu_backend.cpp:636-703):
+ * add: out = a + b; mul: out = a * b; silu: out = x / (1 + exp(-x)).
+ * out may equal an input. */
+int ikv_add_f32(const float *a, const float *b, float *out, int64_t n, void *stream);
+int ikv_mul_f32(const float *a, const float *b, float *out, int64_t n, void *stream);
+int ikv_silu_f32(const float *x, float *out, int64_t n, void *stream);
+
+/* ---------------------------------------------------------------------
+ * Greedy sampling on the device (sample_greedy, src/sampler.cpp:42-65):
+ * *token = the index of the largest of logits[0, n); ties go to the lowest
+ * index. A NaN or +inf logit, or all logits -inf, writes *token = -1 (the
+ * reference returns invalid_argument). n must be in [1, 2^31). token is a
+ * device int32.
+ * ------------------------------------------------------------------- */
+int ikv_argmax_f32(const float *logits, int64_t n, int32_t *token, void *stream);
+
+/* ---------------------------------------------------------------------
+ * Host helper: the benchmarks' synthetic weights. out_host[i] =
+ * std * N(0,1) sample number (offset + i) of the stream `seed`:
+ * splitmix64 outputs 2j+1 and 2j+2 of the seed give the uniforms of
+ * Box-Muller pair j (u1 = (z1 >> 11 + 1) 2^-53, u2 = (z2 >> 11) 2^-53,
+ * r = sqrt(-2 ln u1), normals r cos(2 pi u2), r sin(2 pi u2)), times std,
+ * computed in double and rounded once to float. Any split of [0, n) over calls gives the
+ * same values. Uses up to `threads` host threads (<= 1: the calling thread).
+ * ------------------------------------------------------------------- */
+int ikv_synth_normal_f32(uint64_t seed, uint64_t offset, size_t n, double std, float *out_host,
+                         int threads);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* IKV_MODEL_H */

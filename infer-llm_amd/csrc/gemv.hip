@@ -1,0 +1,301 @@
+// gemv.hip — the projections of a Qwen3 step: out[m][n] = sum_k x[m][k] w[n][k].
+//
+// Replaces CPUBackend::compute_mul_mat (src/backends/cpu_backend.cpp:386-424)
+// and CUDA_F32 mul_mat (src/kernels/cuda/kernel_f32.cu:142-205), which gave
+// every output element its own thread and re-read x per element.
+//
+// Decode (m == 1) is a matrix-vector product that streams the weight from
+// HBM once (F32 weights: 4 bytes per multiply-add, far below the FP32
+// ridge), so the kernel is built for bandwidth: each wavefront owns RPW
+// weight rows; a lane loads 16-byte pieces k = 4*lane + 256*j of every row
+// (1 KiB per wave per load, coalesced) with non-temporal loads, the next
+// 1024-column batch of every row in flight while the current one is
+// multiplied; x comes through L1/L2 (it is shared by every wave); the row
+// sums finish with DPP/swizzle half-wave reductions. Fused variants: a
+// residual add (o_proj, ffn_down), three projections of one input in one
+// launch (q, k, v), and the SwiGLU pair gate/up (each wave owns matching
+// gate and up rows and writes up * silu(gate)).
+//
+// Prefill (m > 1) is a dense F32 GEMM and goes to rocBLAS SGEMM.
+#include <rocblas/rocblas.h>
+
+#include <climits>
+#include <mutex>
+
+#include "ikv_common.hpp"
+#include "../../include/ikv_model.h"
+
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * 64;
+constexpr int kBatch = 4;                // float4 loads per lane per row per batch
+constexpr int kBatchCols = kBatch * 256; // 1024 columns
+
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float4 nt_load4(const float *p) {
+  const f4v v = __builtin_nontemporal_load(reinterpret_cast<const f4v *>(p));
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ float wave_sum64(float v) {
+  v = ikv::half_wave_sum(v);
+  return v + __shfl_xor(v, 32, 64);
+}
+
+// Sums of NR rows (row r at rows[r], K columns, K % 1024 == 0) dotted with
+// x; every lane gets the sums.
+template <int NR>
+__device__ __forceinline__ void wave_dots(const float *const (&rows)[NR], const float *x, int K,
+                                          float (&out)[NR]) {
+  const int lane = threadIdx.x & 63;
+  float4 cur[NR][kBatch], nxt[NR][kBatch];
+  float4 acc[NR];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    acc[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) cur[r][j] = nt_load4(rows[r] + 4 * lane + 256 * j);
+  }
+  for (int k0 = 0; k0 < K; k0 += kBatchCols) {
+    const bool more = k0 + kBatchCols < K;
+    if (more) {
+#pragma unroll
+      for (int r = 0; r < NR; ++r)
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j)
+          nxt[r][j] = nt_load4(rows[r] + k0 + kBatchCols + 4 * lane + 256 * j);
+    }
+    float4 xv[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j)
+      xv[j] = *reinterpret_cast<const float4 *>(x + k0 + 4 * lane + 256 * j);
+#pragma unroll
+    for (int r = 0; r < NR; ++r)
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        acc[r].x = fmaf(cur[r][j].x, xv[j].x, acc[r].x);
+        acc[r].y = fmaf(cur[r][j].y, xv[j].y, acc[r].y);
+        acc[r].z = fmaf(cur[r][j].z, xv[j].z, acc[r].z);
+        acc[r].w = fmaf(cur[r][j].w, xv[j].w, acc[r].w);
+      }
+    if (more) {
+#pragma unroll
+      for (int r = 0; r < NR; ++r)
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) cur[r][j] = nxt[r][j];
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < NR; ++r) out[r] = wave_sum64((acc[r].x + acc[r].y) + (acc[r].z + acc[r].w));
+}
+
+// out[n] = w[n] . x (+ residual[n]); RPW rows per wave, n_out % RPW == 0.
+template <int RPW>
+__global__ __launch_bounds__(kThreads) void gemv_kernel(const float *__restrict__ w,
+                                                        const float *__restrict__ x, float *out,
+                                                        const float *residual, int n_out, int K) {
+  const int wave = blockIdx.x * kWaves + (threadIdx.x >> 6);
+  const int row0 = wave * RPW;
+  if (row0 >= n_out) return;
+  const float *rows[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) rows[r] = w + static_cast<size_t>(row0 + r) * K;
+  float s[RPW];
+  wave_dots<RPW>(rows, x, K, s);
+  const int lane = threadIdx.x & 63;
+  if (lane < RPW) {
+    float v = s[0];
+#pragma unroll
+    for (int r = 1; r < RPW; ++r)
+      if (lane == r) v = s[r];
+    if (residual) v += residual[row0 + lane];
+    out[row0 + lane] = v;
+  }
+}
+
+// Three weight matrices sharing x; wave rows fall in exactly one of them
+// (each n_i % RPW == 0).
+template <int RPW>
+__global__ __launch_bounds__(kThreads) void gemv3_kernel(const float *__restrict__ w0,
+                                                         const float *__restrict__ w1,
+                                                         const float *__restrict__ w2,
+                                                         const float *__restrict__ x, float *out0,
+                                                         float *out1, float *out2, int n0, int n1,
+                                                         int n2, int K) {
+  const int wave = blockIdx.x * kWaves + (threadIdx.x >> 6);
+  int row0 = wave * RPW;
+  const float *w;
+  float *out;
+  if (row0 < n0) {
+    w = w0;
+    out = out0;
+  } else if (row0 < n0 + n1) {
+    row0 -= n0;
+    w = w1;
+    out = out1;
+  } else if (row0 < n0 + n1 + n2) {
+    row0 -= n0 + n1;
+    w = w2;
+    out = out2;
+  } else {
+    return;
+  }
+  const float *rows[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) rows[r] = w + static_cast<size_t>(row0 + r) * K;
+  float s[RPW];
+  wave_dots<RPW>(rows, x, K, s);
+  const int lane = threadIdx.x & 63;
+  if (lane < RPW) {
+    float v = s[0];
+#pragma unroll
+    for (int r = 1; r < RPW; ++r)
+      if (lane == r) v = s[r];
+    out[row0 + lane] = v;
+  }
+}
+
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
+
+// out[n] = (w_up[n] . x) * silu(w_gate[n] . x); one output per wave.
+__global__ __launch_bounds__(kThreads) void gemv_swiglu_kernel(const float *__restrict__ wg,
+                                                               const float *__restrict__ wu,
+                                                               const float *__restrict__ x,
+                                                               float *__restrict__ out, int n_out,
+                                                               int K) {
+  const int n = blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (n >= n_out) return;
+  const float *rows[2] = {wg + static_cast<size_t>(n) * K, wu + static_cast<size_t>(n) * K};
+  float s[2];
+  wave_dots<2>(rows, x, K, s);
+  if ((threadIdx.x & 63) == 0) out[n] = s[1] * silu(s[0]);
+}
+
+// Any shape: one wave per output row, scalar loads (sizes the fast kernels
+// do not take: K % 1024 != 0 or unaligned pointers).
+__global__ __launch_bounds__(kThreads) void gemv_generic_kernel(const float *__restrict__ w,
+                                                                const float *__restrict__ x,
+                                                                float *out, const float *residual,
+                                                                int n_out, int K, int mode,
+                                                                const float *__restrict__ w_up) {
+  const int n = blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (n >= n_out) return;
+  const int lane = threadIdx.x & 63;
+  const float *row = w + static_cast<size_t>(n) * K;
+  float a = 0.f, b = 0.f;
+  for (int k = lane; k < K; k += 64) {
+    a = fmaf(row[k], x[k], a);
+    if (mode == 2) b = fmaf(w_up[static_cast<size_t>(n) * K + k], x[k], b);
+  }
+  a = wave_sum64(a);
+  b = wave_sum64(b);
+  if (lane == 0) {
+    float v = a;
+    if (mode == 2) v = b * silu(a);
+    if (residual) v += residual[n];
+    out[n] = v;
+  }
+}
+
+bool fast_ok(int64_t k, std::initializer_list<const void *> ptrs) {
+  if (k % kBatchCols != 0) return false;
+  for (const void *p : ptrs)
+    if (p && !ikv::aligned16(p)) return false;
+  return true;
+}
+
+int grid_for(int64_t waves) { return static_cast<int>((waves + kWaves - 1) / kWaves); }
+
+// rocBLAS handle of the current device, created on first use.
+rocblas_handle blas_handle() {
+  static std::mutex mu;
+  static rocblas_handle handles[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!handles[dev] && rocblas_create_handle(&handles[dev]) != rocblas_status_success)
+    handles[dev] = nullptr;
+  return handles[dev];
+}
+
+}  // namespace
+
+extern "C" int ikv_mul_mat_f32(const float *w, const float *x, float *out, int64_t n_out,
+                               int64_t k, int64_t m, const float *residual, void *stream) {
+  if (!w || !x || !out) return -EINVAL;
+  if (n_out < 0 || k < 0 || m < 0) return -EINVAL;
+  if (n_out == 0 || m == 0) return 0;
+  if (k == 0) return -EINVAL;
+  if (n_out > INT_MAX / 2 || k > INT_MAX / 2 || m > INT_MAX / 2) return -EOVERFLOW;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (m == 1) {
+    if (fast_ok(k, {w, x})) {
+      const int rpw = (n_out >= 8192 && n_out % 2 == 0) ? 2 : 1;
+      if (rpw == 2)
+        gemv_kernel<2><<<grid_for(n_out / 2), kThreads, 0, s>>>(w, x, out, residual, int(n_out), int(k));
+      else
+        gemv_kernel<1><<<grid_for(n_out), kThreads, 0, s>>>(w, x, out, residual, int(n_out), int(k));
+    } else {
+      gemv_generic_kernel<<<grid_for(n_out), kThreads, 0, s>>>(w, x, out, residual, int(n_out),
+                                                                int(k), 0, nullptr);
+    }
+    return ikv::launch_status();
+  }
+  rocblas_handle h = blas_handle();
+  if (!h) return static_cast<int>(hipErrorNotInitialized);
+  if (rocblas_set_stream(h, s) != rocblas_status_success) return static_cast<int>(hipErrorUnknown);
+  float beta = 0.f;
+  if (residual) {
+    beta = 1.f;
+    if (residual != out) {
+      const hipError_t e = hipMemcpyAsync(out, residual, sizeof(float) * n_out * m,
+                                          hipMemcpyDeviceToDevice, s);
+      if (e != hipSuccess) return static_cast<int>(e);
+    }
+  }
+  const float alpha = 1.f;
+  // Row-major out[m][n] is the column-major n x m matrix C = W^T(col) * X:
+  // A = w viewed column-major k x n, transposed; B = x viewed k x m.
+  const rocblas_status st = rocblas_sgemm(h, rocblas_operation_transpose, rocblas_operation_none,
+                                          int(n_out), int(m), int(k), &alpha, w, int(k), x, int(k),
+                                          &beta, out, int(n_out));
+  if (st != rocblas_status_success) return static_cast<int>(hipErrorLaunchFailure);
+  return ikv::launch_status();
+}
+
+extern "C" int ikv_gemv3_f32(const float *w0, const float *w1, const float *w2, const float *x,
+                             float *out0, float *out1, float *out2, int64_t n0, int64_t n1,
+                             int64_t n2, int64_t k, void *stream) {
+  if (!w0 || !w1 || !w2 || !x || !out0 || !out1 || !out2) return -EINVAL;
+  if (n0 < 0 || n1 < 0 || n2 < 0 || k <= 0) return -EINVAL;
+  if (n0 + n1 + n2 > INT_MAX / 2 || k > INT_MAX / 2) return -EOVERFLOW;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (!fast_ok(k, {w0, w1, w2, x})) {
+    int rc = ikv_mul_mat_f32(w0, x, out0, n0, k, 1, nullptr, stream);
+    if (rc == 0) rc = ikv_mul_mat_f32(w1, x, out1, n1, k, 1, nullptr, stream);
+    if (rc == 0) rc = ikv_mul_mat_f32(w2, x, out2, n2, k, 1, nullptr, stream);
+    return rc;
+  }
+  const int64_t total = n0 + n1 + n2;
+  if (total == 0) return 0;
+  gemv3_kernel<1><<<grid_for(total), kThreads, 0, s>>>(w0, w1, w2, x, out0, out1, out2, int(n0),
+                                                      int(n1), int(n2), int(k));
+  return ikv::launch_status();
+}
+
+extern "C" int ikv_gemv_swiglu_f32(const float *w_gate, const float *w_up, const float *x,
+                                   float *out, int64_t n_out, int64_t k, void *stream) {
+  if (!w_gate || !w_up || !x || !out) return -EINVAL;
+  if (n_out < 0 || k <= 0) return -EINVAL;
+  if (n_out == 0) return 0;
+  if (n_out > INT_MAX / 2 || k > INT_MAX / 2) return -EOVERFLOW;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (fast_ok(k, {w_gate, w_up, x}))
+    gemv_swiglu_kernel<<<grid_for(n_out), kThreads, 0, s>>>(w_gate, w_up, x, out, int(n_out), int(k));
+  else
+    gemv_generic_kernel<<<grid_for(n_out), kThreads, 0, s>>>(w_gate, x, out, nullptr, int(n_out),
+                                                              int(k), 2, w_up);
+  return ikv::launch_status();
+}

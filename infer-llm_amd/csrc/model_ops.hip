@@ -1,0 +1,181 @@
+// model_ops.hip — the small ops of a Qwen3 step around the KV-cache path:
+// token-embedding gather, elementwise add / mul / silu, and greedy sampling
+// on the device.
+//
+//   get_rows  CPUBackend::compute_get_rows (src/backends/cpu_backend.cpp:
+//             259-332): one workgroup per index copies a table row with
+//             16-byte accesses; an out-of-range id writes zeros and raises a
+//             status flag instead of reading outside the table.
+//   add/mul/silu  src/backends/cpu_backend.cpp:636-703: grid-stride float4.
+//   argmax    sample_greedy (src/sampler.cpp:42-65): one workgroup of 1024
+//             threads scans the logits (16-byte loads), keeps (max, lowest
+//             index) per lane, and reduces through DPP shuffles and LDS;
+//             NaN or +inf anywhere, or no finite maximum, gives -1.
+#include <climits>
+
+#include "ikv_common.hpp"
+#include "../../include/ikv_model.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+
+__global__ __launch_bounds__(kThreads) void get_rows_kernel(const float *__restrict__ table,
+                                                            const int32_t *__restrict__ ids,
+                                                            float *__restrict__ out, int64_t row_len,
+                                                            int64_t n_rows, int *status, int vec) {
+  const int64_t i = blockIdx.x;
+  const int32_t id = ids[i];
+  float *dst = out + i * row_len;
+  const bool ok = id >= 0 && id < n_rows;
+  if (!ok && threadIdx.x == 0 && status) atomicOr(status, 1);
+  const float *src = table + static_cast<int64_t>(ok ? id : 0) * row_len;
+  if (vec) {
+    for (int64_t c = threadIdx.x; c < row_len / 4; c += kThreads) {
+      const float4 v = ok ? reinterpret_cast<const float4 *>(src)[c] : make_float4(0.f, 0.f, 0.f, 0.f);
+      reinterpret_cast<float4 *>(dst)[c] = v;
+    }
+  } else {
+    for (int64_t c = threadIdx.x; c < row_len; c += kThreads) dst[c] = ok ? src[c] : 0.f;
+  }
+}
+
+enum class Ew { kAdd, kMul, kSilu };
+
+template <Ew OP>
+__device__ __forceinline__ float ew(float a, float b) {
+  if constexpr (OP == Ew::kAdd) return a + b;
+  else if constexpr (OP == Ew::kMul) return a * b;
+  else return a / (1.0f + expf(-a));
+}
+
+template <Ew OP>
+__global__ __launch_bounds__(kThreads) void elementwise_kernel(const float *a, const float *b,
+                                                               float *out, int64_t n, int vec) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+  int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (vec) {
+    const int64_t n4 = n / 4;
+    for (int64_t j = i; j < n4; j += stride) {
+      const float4 x = reinterpret_cast<const float4 *>(a)[j];
+      const float4 y = b ? reinterpret_cast<const float4 *>(b)[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+      reinterpret_cast<float4 *>(out)[j] =
+          make_float4(ew<OP>(x.x, y.x), ew<OP>(x.y, y.y), ew<OP>(x.z, y.z), ew<OP>(x.w, y.w));
+    }
+    for (int64_t j = 4 * n4 + i; j < n; j += stride) out[j] = ew<OP>(a[j], b ? b[j] : 0.f);
+  } else {
+    for (int64_t j = i; j < n; j += stride) out[j] = ew<OP>(a[j], b ? b[j] : 0.f);
+  }
+}
+
+template <Ew OP>
+int launch_ew(const float *a, const float *b, float *out, int64_t n, void *stream) {
+  if (!a || !out || (OP != Ew::kSilu && !b)) return -EINVAL;
+  if (n < 0) return -EINVAL;
+  if (n == 0) return 0;
+  const bool vec = ikv::aligned16(a) && ikv::aligned16(out) && (!b || ikv::aligned16(b));
+  const int64_t work = vec ? (n + 3) / 4 : n;
+  int64_t blocks = (work + kThreads - 1) / kThreads;
+  if (blocks > 4096) blocks = 4096;
+  elementwise_kernel<OP><<<static_cast<int>(blocks), kThreads, 0, static_cast<hipStream_t>(stream)>>>(
+      a, b, out, n, vec ? 1 : 0);
+  return ikv::launch_status();
+}
+
+constexpr int kArgThreads = 1024;
+
+// (value, index) pair order of the greedy sampler: larger value wins, equal
+// values go to the lower index.
+__device__ __forceinline__ void better(float &v, int &i, float ov, int oi) {
+  if (ov > v || (ov == v && oi < i)) {
+    v = ov;
+    i = oi;
+  }
+}
+
+__device__ __forceinline__ void visit(float x, int idx, float &best, int &bi, int &bad) {
+  if (x != x || x == INFINITY) bad = 1;
+  if (x > best) {  // strictly greater: the first (lowest) index of a tie stays
+    best = x;
+    bi = idx;
+  }
+}
+
+__global__ __launch_bounds__(kArgThreads) void argmax_kernel(const float *__restrict__ logits,
+                                                             int n, int32_t *token, int vec) {
+  __shared__ float s_v[kArgThreads / 64];
+  __shared__ int s_i[kArgThreads / 64];
+  __shared__ int s_bad;
+  const int tid = threadIdx.x;
+  if (tid == 0) s_bad = 0;
+  float best = -INFINITY;
+  int bi = INT_MAX;
+  int bad = 0;
+  if (vec) {
+    // Lane t reads float4 t, t + 1024, ...: its indices increase.
+    const int n4 = n / 4;
+    for (int j = tid; j < n4; j += kArgThreads) {
+      const float4 v = reinterpret_cast<const float4 *>(logits)[j];
+      visit(v.x, 4 * j, best, bi, bad);
+      visit(v.y, 4 * j + 1, best, bi, bad);
+      visit(v.z, 4 * j + 2, best, bi, bad);
+      visit(v.w, 4 * j + 3, best, bi, bad);
+    }
+    for (int j = 4 * n4 + tid; j < n; j += kArgThreads) visit(logits[j], j, best, bi, bad);
+  } else {
+    for (int j = tid; j < n; j += kArgThreads) visit(logits[j], j, best, bi, bad);
+  }
+  __syncthreads();
+  if (bad) s_bad = 1;  // benign race: every writer stores 1
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(best, o, 64);
+    const int oi = __shfl_xor(bi, o, 64);
+    better(best, bi, ov, oi);
+  }
+  if ((tid & 63) == 0) {
+    s_v[tid >> 6] = best;
+    s_i[tid >> 6] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float v = s_v[0];
+    int i = s_i[0];
+    for (int w = 1; w < kArgThreads / 64; ++w) better(v, i, s_v[w], s_i[w]);
+    *token = (s_bad || v == -INFINITY || i == INT_MAX) ? -1 : i;
+  }
+}
+
+}  // namespace
+
+extern "C" int ikv_get_rows_f32(const float *table, const int32_t *ids, float *out, int64_t n_ids,
+                                int64_t row_len, int64_t n_rows, int *status, void *stream) {
+  if (!table || !ids || !out) return -EINVAL;
+  if (n_ids < 0 || row_len < 0 || n_rows < 0) return -EINVAL;
+  if (n_ids == 0 || row_len == 0) return 0;
+  if (n_ids > INT_MAX) return -EOVERFLOW;
+  const bool vec = row_len % 4 == 0 && ikv::aligned16(table) && ikv::aligned16(out);
+  get_rows_kernel<<<static_cast<int>(n_ids), kThreads, 0, static_cast<hipStream_t>(stream)>>>(
+      table, ids, out, row_len, n_rows, status, vec ? 1 : 0);
+  return ikv::launch_status();
+}
+
+extern "C" int ikv_add_f32(const float *a, const float *b, float *out, int64_t n, void *stream) {
+  return launch_ew<Ew::kAdd>(a, b, out, n, stream);
+}
+
+extern "C" int ikv_mul_f32(const float *a, const float *b, float *out, int64_t n, void *stream) {
+  return launch_ew<Ew::kMul>(a, b, out, n, stream);
+}
+
+extern "C" int ikv_silu_f32(const float *x, float *out, int64_t n, void *stream) {
+  return launch_ew<Ew::kSilu>(x, nullptr, out, n, stream);
+}
+
+extern "C" int ikv_argmax_f32(const float *logits, int64_t n, int32_t *token, void *stream) {
+  if (!logits || !token) return -EINVAL;
+  if (n < 1) return -EINVAL;
+  if (n > INT_MAX) return -EOVERFLOW;
+  argmax_kernel<<<1, kArgThreads, 0, static_cast<hipStream_t>(stream)>>>(
+      logits, static_cast<int>(n), token, ikv::aligned16(logits) ? 1 : 0);
+  return ikv::launch_status();
+}

@@ -5,6 +5,7 @@
 #include <vector>
 
 #include "../../include/ikv.h"
+#include "../../include/ikv_model.h"
 #include "op_params.hpp"
 
 namespace {
@@ -115,7 +116,16 @@ bool HIPBackend::supports_op(OperationType op, const Tensor &t) const {
     case OperationType::GGML_OP_RMS_NORM:
     case OperationType::GGML_OP_ROPE:
     case OperationType::GGML_OP_FLASH_ATTN_EXT:
+    case OperationType::GGML_OP_GET_ROWS:
+    case OperationType::GGML_OP_MUL_MAT:
+    case OperationType::GGML_OP_ADD:
+    case OperationType::GGML_OP_MUL:
       return true;
+    case OperationType::GGML_OP_UNARY: {
+      uint32_t sub = 0;
+      std::memcpy(&sub, &t.op_params[0], sizeof(sub));
+      return sub == static_cast<uint32_t>(UnaryOp::GGML_UNARY_OP_SILU);
+    }
     default:
       return false;
   }
@@ -307,6 +317,9 @@ infer::expected<void, std::error_code> HIPBackend::compute(Graph &graph) {
   _stats = Stats{};
   _norm_into_rope.clear();
   _append_into_attn.clear();
+  _swiglu.clear();
+  _residual.clear();
+  _qkv.clear();
   _skip.clear();
 
   if (_fusion) {
@@ -347,6 +360,7 @@ infer::expected<void, std::error_code> HIPBackend::compute(Graph &graph) {
         _skip[vc] = true;
       }
     }
+    plan_model_fusions(graph, uses);
   }
 
   for (Tensor *node : graph.nodes()) {
@@ -359,6 +373,75 @@ infer::expected<void, std::error_code> HIPBackend::compute(Graph &graph) {
     }
   }
   return {};
+}
+
+namespace {
+
+bool is_mm(const Tensor *t) { return t && t->op == OperationType::GGML_OP_MUL_MAT; }
+
+bool is_silu(const Tensor *t) {
+  if (!t || t->op != OperationType::GGML_OP_UNARY) return false;
+  uint32_t sub = 0;
+  std::memcpy(&sub, &t->op_params[0], sizeof(sub));
+  return sub == static_cast<uint32_t>(UnaryOp::GGML_UNARY_OP_SILU);
+}
+
+// Weight [K, N] times activation [K, M] with contiguous F32 operands.
+bool mm_operands_ok(const Tensor *mm) {
+  const Tensor *w = mm->src[0], *x = mm->src[1];
+  return contiguous_f32(w) && contiguous_f32(x) && w->dims[0] == x->dims[0] && w->dims[2] == 1 &&
+         w->dims[3] == 1 && x->dims[2] == 1 && x->dims[3] == 1;
+}
+
+}  // namespace
+
+// Model-level fusions of the Qwen3 graph (src/models/Qwen3.cpp:53-113):
+//  * MUL(up, SILU(gate)) with gate = MUL_MAT(w_gate, x), up = MUL_MAT(w_up, x)
+//    and one token -> one ikv_gemv_swiglu_f32;
+//  * ADD(MUL_MAT(w, x), r) -> the product with the residual added in its
+//    epilogue (o_proj and ffn_down);
+//  * three single-token MUL_MATs of one input (q, k, v) -> one ikv_gemv3_f32.
+// Every fused intermediate has exactly one use.
+void HIPBackend::plan_model_fusions(Graph &graph, std::unordered_map<const Tensor *, int> &uses) {
+  for (Tensor *n : graph.nodes()) {
+    if (n->op != OperationType::GGML_OP_MUL || !n->src[0] || !n->src[1]) continue;
+    for (int side = 0; side < 2; ++side) {
+      const Tensor *up = n->src[side], *act = n->src[1 - side];
+      if (!is_mm(up) || !is_silu(act) || !is_mm(act->src[0])) continue;
+      const Tensor *gate = act->src[0];
+      if (up->src[1] != gate->src[1] || up->src[1]->dims[1] != 1) continue;
+      if (uses[up] != 1 || uses[act] != 1 || uses[gate] != 1) continue;
+      if (!mm_operands_ok(up) || !mm_operands_ok(gate) || up->dims != gate->dims) continue;
+      _swiglu[n] = {gate, up};
+      _skip[up] = _skip[act] = _skip[gate] = true;
+      break;
+    }
+  }
+  for (Tensor *n : graph.nodes()) {
+    if (n->op != OperationType::GGML_OP_ADD || !n->src[0] || !n->src[1]) continue;
+    for (int side = 0; side < 2; ++side) {
+      const Tensor *mm = n->src[side], *res = n->src[1 - side];
+      if (!is_mm(mm) || _skip.count(mm) || uses[mm] != 1 || !mm_operands_ok(mm)) continue;
+      if (!contiguous_f32(res) || res->dims != mm->dims) continue;
+      _residual[n] = {mm, res};
+      _skip[mm] = true;
+      break;
+    }
+  }
+  std::unordered_map<const Tensor *, std::vector<const Tensor *>> by_input;
+  std::vector<const Tensor *> order;
+  for (Tensor *n : graph.nodes()) {
+    if (!is_mm(n) || _skip.count(n) || !mm_operands_ok(n) || n->src[1]->dims[1] != 1) continue;
+    auto &v = by_input[n->src[1]];
+    if (v.empty()) order.push_back(n->src[1]);
+    v.push_back(n);
+  }
+  for (const Tensor *x : order) {
+    const auto &v = by_input[x];
+    if (v.size() != 3) continue;
+    _qkv[v[0]] = {v[0], v[1], v[2]};
+    _skip[v[1]] = _skip[v[2]] = true;
+  }
 }
 
 infer::expected<void, std::error_code> HIPBackend::dispatch(Tensor *node) {
@@ -471,6 +554,95 @@ infer::expected<void, std::error_code> HIPBackend::dispatch(Tensor *node) {
                                             static_cast<float *>(node->data), int(Hq), int(Hkv), int(D),
                                             nq, nkv, p.n_ctx, p.scale, s),
                        "attn_prefill");
+    }
+
+    case OperationType::GGML_OP_GET_ROWS: {
+      const Tensor *table = node->src[0], *ids = node->src[1];
+      if (!contiguous_f32(table) || !ids || !ids->data || ids->dataType != GGML_TYPE_I32 ||
+          !node->data || table->dims[0] != node->dims[0] ||
+          ids->element_count() != static_cast<size_t>(node->dims[1]))
+        return infer::fail(std::errc::invalid_argument);
+      ++_stats.launches;
+      return check_ikv(ikv_get_rows_f32(static_cast<const float *>(table->data),
+                                        static_cast<const int32_t *>(ids->data),
+                                        static_cast<float *>(node->data), node->dims[1],
+                                        table->dims[0], table->dims[1], _status, s),
+                       "get_rows");
+    }
+
+    case OperationType::GGML_OP_MUL_MAT: {
+      if (!mm_operands_ok(node) || !node->data) return infer::fail(std::errc::invalid_argument);
+      const Tensor *w = node->src[0], *x = node->src[1];
+      ++_stats.launches;
+      if (const auto g = _qkv.find(node); g != _qkv.end()) {
+        const Tensor *a = g->second[0], *b = g->second[1], *c = g->second[2];
+        ++_stats.fused_qkv;
+        return check_ikv(
+            ikv_gemv3_f32(static_cast<const float *>(a->src[0]->data),
+                          static_cast<const float *>(b->src[0]->data),
+                          static_cast<const float *>(c->src[0]->data),
+                          static_cast<const float *>(x->data), static_cast<float *>(a->data),
+                          static_cast<float *>(b->data), static_cast<float *>(c->data),
+                          a->dims[0], b->dims[0], c->dims[0], w->dims[0], s),
+            "gemv3");
+      }
+      return check_ikv(ikv_mul_mat_f32(static_cast<const float *>(w->data),
+                                       static_cast<const float *>(x->data),
+                                       static_cast<float *>(node->data), w->dims[1], w->dims[0],
+                                       x->dims[1], nullptr, s),
+                       "mul_mat");
+    }
+
+    case OperationType::GGML_OP_ADD: {
+      const Tensor *a = node->src[0], *b = node->src[1];
+      if (!node->data) return infer::fail(std::errc::invalid_argument);
+      ++_stats.launches;
+      if (const auto f = _residual.find(node); f != _residual.end()) {
+        const Tensor *mm = f->second.first, *res = f->second.second;
+        const Tensor *w = mm->src[0], *x = mm->src[1];
+        ++_stats.fused_residual;
+        return check_ikv(ikv_mul_mat_f32(static_cast<const float *>(w->data),
+                                         static_cast<const float *>(x->data),
+                                         static_cast<float *>(node->data), w->dims[1], w->dims[0],
+                                         x->dims[1], static_cast<const float *>(res->data), s),
+                         "mul_mat+add");
+      }
+      if (!contiguous_f32(a) || !contiguous_f32(b) || a->dims != node->dims || b->dims != node->dims)
+        return infer::fail(std::errc::invalid_argument);
+      return check_ikv(ikv_add_f32(static_cast<const float *>(a->data), static_cast<const float *>(b->data),
+                                   static_cast<float *>(node->data), int64_t(node->element_count()), s),
+                       "add");
+    }
+
+    case OperationType::GGML_OP_MUL: {
+      const Tensor *a = node->src[0], *b = node->src[1];
+      if (!node->data) return infer::fail(std::errc::invalid_argument);
+      ++_stats.launches;
+      if (const auto f = _swiglu.find(node); f != _swiglu.end()) {
+        const Tensor *gate = f->second.first, *up = f->second.second;
+        ++_stats.fused_swiglu;
+        return check_ikv(ikv_gemv_swiglu_f32(static_cast<const float *>(gate->src[0]->data),
+                                             static_cast<const float *>(up->src[0]->data),
+                                             static_cast<const float *>(gate->src[1]->data),
+                                             static_cast<float *>(node->data), gate->dims[0],
+                                             gate->src[0]->dims[0], s),
+                         "gemv_swiglu");
+      }
+      if (!contiguous_f32(a) || !contiguous_f32(b) || a->dims != node->dims || b->dims != node->dims)
+        return infer::fail(std::errc::invalid_argument);
+      return check_ikv(ikv_mul_f32(static_cast<const float *>(a->data), static_cast<const float *>(b->data),
+                                   static_cast<float *>(node->data), int64_t(node->element_count()), s),
+                       "mul");
+    }
+
+    case OperationType::GGML_OP_UNARY: {
+      const Tensor *x = node->src[0];
+      if (!is_silu(node) || !contiguous_f32(x) || !node->data || x->dims != node->dims)
+        return infer::fail(std::errc::not_supported);
+      ++_stats.launches;
+      return check_ikv(ikv_silu_f32(static_cast<const float *>(x->data), static_cast<float *>(node->data),
+                                    int64_t(node->element_count()), s),
+                       "silu");
     }
 
     default:

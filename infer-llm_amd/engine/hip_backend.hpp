@@ -20,6 +20,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <array>
 #include <string>
 #include <unordered_map>
 #include <vector>
@@ -62,6 +63,9 @@ class HIPBackend : public Backend {
     int launches = 0;
     int fused_norm_rope = 0;
     int fused_append_decode = 0;
+    int fused_swiglu = 0;
+    int fused_residual = 0;
+    int fused_qkv = 0;
   };
   const Stats &last_stats() const { return _stats; }
 
@@ -75,6 +79,7 @@ class HIPBackend : public Backend {
   infer::expected<const RopeTables *, std::error_code> rope_tables(const Tensor &theta);
   infer::expected<void, std::error_code> ensure_workspace(size_t bytes);
   infer::expected<void, std::error_code> dispatch(Tensor *node);
+  void plan_model_fusions(Graph &graph, std::unordered_map<const Tensor *, int> &uses);
   infer::expected<void, std::error_code> set_device() const;
 
   hipStream_t _stream = nullptr;
@@ -89,5 +94,8 @@ class HIPBackend : public Backend {
   // per-compute() fusion plan
   std::unordered_map<const Tensor *, const Tensor *> _norm_into_rope;  // rope -> its rms_norm
   std::unordered_map<const Tensor *, std::pair<const Tensor *, const Tensor *>> _append_into_attn;
+  std::unordered_map<const Tensor *, std::pair<const Tensor *, const Tensor *>> _swiglu;    // mul -> gate, up
+  std::unordered_map<const Tensor *, std::pair<const Tensor *, const Tensor *>> _residual;  // add -> mm, r
+  std::unordered_map<const Tensor *, std::array<const Tensor *, 3>> _qkv;  // first mm -> group
   std::unordered_map<const Tensor *, bool> _skip;
 };

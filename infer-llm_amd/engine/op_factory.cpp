@@ -17,6 +17,48 @@ Tensor *new_node(Graph &g, std::string_view name, DataType type, std::initialize
 
 }  // namespace
 
+Tensor *OpFactory::add(Graph &g, Tensor *a, Tensor *b, std::string_view name) {
+  assert(a->dims == b->dims && a->dataType == b->dataType);
+  Tensor *r = new_node(g, name, a->dataType, {a->dims[0], a->dims[1], a->dims[2], a->dims[3]},
+                       OperationType::GGML_OP_ADD);
+  r->src[0] = a;
+  r->src[1] = b;
+  return r;
+}
+
+Tensor *OpFactory::mul(Graph &g, Tensor *a, Tensor *b, std::string_view name) {
+  assert(a->dims == b->dims && a->dataType == b->dataType);
+  Tensor *r = new_node(g, name, a->dataType, {a->dims[0], a->dims[1], a->dims[2], a->dims[3]},
+                       OperationType::GGML_OP_MUL);
+  r->src[0] = a;
+  r->src[1] = b;
+  return r;
+}
+
+Tensor *OpFactory::silu(Graph &g, Tensor *x, std::string_view name) {
+  Tensor *r = new_node(g, name, x->dataType, {x->dims[0], x->dims[1], x->dims[2], x->dims[3]},
+                       OperationType::GGML_OP_UNARY);
+  r->src[0] = x;
+  const uint32_t sub = static_cast<uint32_t>(UnaryOp::GGML_UNARY_OP_SILU);
+  std::memcpy(&r->op_params[0], &sub, sizeof(sub));
+  return r;
+}
+
+Tensor *OpFactory::mul_mat(Graph &g, Tensor *w, Tensor *x, std::string_view name) {
+  Tensor *r = new_node(g, name, x->dataType, {w->dims[1], x->dims[1]}, OperationType::GGML_OP_MUL_MAT);
+  r->src[0] = w;
+  r->src[1] = x;
+  return r;
+}
+
+Tensor *OpFactory::embedding(Graph &g, Tensor *token_embd, Tensor *input_token) {
+  Tensor *r = new_node(g, "embedding", token_embd->dataType, {token_embd->dims[0], input_token->dims[0]},
+                       OperationType::GGML_OP_GET_ROWS);
+  r->src[0] = token_embd;
+  r->src[1] = input_token;
+  return r;
+}
+
 Tensor *OpFactory::rms_norm(Graph &g, Tensor *x, Tensor *weight, float eps, std::string_view name) {
   Tensor *r = new_node(g, name, x->dataType, {x->dims[0], x->dims[1], x->dims[2], x->dims[3]},
                        OperationType::GGML_OP_RMS_NORM);

@@ -15,6 +15,18 @@
 #include "tensor.hpp"
 
 struct OpFactory {
+  // Elementwise a + b, a * b of equal shapes (src/op_factory.cpp:16-59).
+  static Tensor *add(Graph &g, Tensor *a, Tensor *b, std::string_view name);
+  static Tensor *mul(Graph &g, Tensor *a, Tensor *b, std::string_view name);
+  // x / (1 + exp(-x)): UNARY with GGML_UNARY_OP_SILU in op_params[0]
+  // (src/op_factory.cpp:126-136).
+  static Tensor *silu(Graph &g, Tensor *x, std::string_view name);
+  // w [n_embd, n_out] (rows of n_embd), x [n_embd, n_tokens] ->
+  // out [n_out, n_tokens] (src/op_factory.cpp:98-108).
+  static Tensor *mul_mat(Graph &g, Tensor *w, Tensor *x, std::string_view name);
+  // GET_ROWS of token_embd [n_embd, n_vocab] by input_token [n_tokens] ->
+  // [n_embd, n_tokens] (src/op_factory.cpp:78-94).
+  static Tensor *embedding(Graph &g, Tensor *token_embd, Tensor *input_token);
   // out = rms_norm(x) * weight along dims[0]; eps in op_params[0].
   static Tensor *rms_norm(Graph &g, Tensor *x, Tensor *weight, float eps, std::string_view name);
   // NeoX RoPE of x [head_dim, n_heads, n_tokens] at positions pos [n_tokens]

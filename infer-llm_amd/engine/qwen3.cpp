@@ -1,0 +1,304 @@
+#include "qwen3.hpp"
+
+#include <cstring>
+
+#include "../../include/ikv_model.h"
+#include "kvcache/kvstorage.hpp"
+#include "kvcache/kvstrategy.hpp"
+#include "op_factory.hpp"
+
+namespace {
+
+size_t align256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
+
+double seconds(std::chrono::steady_clock::time_point a, std::chrono::steady_clock::time_point b) {
+  return std::chrono::duration<double>(b - a).count();
+}
+
+bool is_norm(const std::string &name) { return name.find("norm") != std::string::npos; }
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// model
+
+Qwen3Model::Qwen3Model(const Qwen3Hparams &hp) : _hp(hp) {
+  const int64_t E = hp.n_embd, D = hp.head_dim, Q = int64_t(hp.n_head) * D,
+                KV = int64_t(hp.n_head_kv) * D, F = hp.n_ff;
+  _token_embd = make("token_embd.weight", {E, hp.n_vocab});
+  _layers.resize(hp.n_layer);
+  for (uint32_t l = 0; l < hp.n_layer; ++l) {
+    const std::string p = "blk." + std::to_string(l) + ".";
+    Qwen3LayerWeights &L = _layers[l];
+    L.attn_norm = make(p + "attn_norm.weight", {E});
+    L.wq = make(p + "attn_q.weight", {E, Q});
+    L.wk = make(p + "attn_k.weight", {E, KV});
+    L.wv = make(p + "attn_v.weight", {E, KV});
+    L.attn_q_norm = make(p + "attn_q_norm.weight", {D});
+    L.attn_k_norm = make(p + "attn_k_norm.weight", {D});
+    L.wo = make(p + "attn_output.weight", {Q, E});
+    L.ffn_norm = make(p + "ffn_norm.weight", {E});
+    L.ffn_gate = make(p + "ffn_gate.weight", {E, F});
+    L.ffn_up = make(p + "ffn_up.weight", {E, F});
+    L.ffn_down = make(p + "ffn_down.weight", {F, E});
+  }
+  _output_norm = make("output_norm.weight", {E});
+}
+
+Qwen3Model::~Qwen3Model() {
+  if (_arena && _backend) _backend->free(BufferKind::WEIGHTS, _arena);
+}
+
+Tensor *Qwen3Model::make(const std::string &name, std::initializer_list<int64_t> shape) {
+  auto t = std::make_unique<Tensor>(name, GGML_TYPE_F32, shape);
+  t->tensorRole = TensorRole::TENSOR_ROLE_WEIGHT;
+  Tensor *raw = t.get();
+  _map.emplace(name, raw);
+  _tensors.push_back(std::move(t));
+  return raw;
+}
+
+std::vector<std::string> Qwen3Model::tensor_names() const {
+  std::vector<std::string> names;
+  for (const auto &t : _tensors) names.push_back(t->name);
+  return names;
+}
+
+Tensor *Qwen3Model::find(const std::string &name) const {
+  auto it = _map.find(name);
+  return it == _map.end() ? nullptr : it->second;
+}
+
+infer::expected<void, std::error_code> Qwen3Model::alloc_weights(Backend *backend) {
+  if (!backend || _arena) return infer::fail(std::errc::invalid_argument);
+  size_t total = 0;
+  for (const auto &t : _tensors) total += align256(t->byte_size());
+  auto mem = backend->alloc(BufferKind::WEIGHTS, total);
+  if (!mem) return infer::unexpected(mem.error());
+  _backend = backend;
+  _arena = *mem;
+  _arena_bytes = total;
+  char *cursor = static_cast<char *>(_arena);
+  for (const auto &t : _tensors) {
+    t->data = cursor;
+    t->backend = backend;
+    t->device = backend->device_type();
+    cursor += align256(t->byte_size());
+  }
+  return {};
+}
+
+infer::expected<void, std::error_code> Qwen3Model::set_tensor(const std::string &name,
+                                                              const float *host, size_t count) {
+  Tensor *t = find(name);
+  if (!t || !t->data || !host) return infer::fail(std::errc::invalid_argument);
+  if (count != t->element_count()) return infer::fail(std::errc::invalid_argument);
+  return _backend->copy_tensor_set(t, host, 0, count * sizeof(float));
+}
+
+infer::expected<void, std::error_code> Qwen3Model::init_synthetic(uint64_t seed, double std,
+                                                                  int threads) {
+  if (!_arena) return infer::fail(std::errc::invalid_argument);
+  size_t largest = 0;
+  for (const auto &t : _tensors) largest = std::max(largest, t->element_count());
+  std::vector<float> host(largest);
+  uint64_t offset = 0;
+  for (const auto &t : _tensors) {
+    const size_t n = t->element_count();
+    if (is_norm(t->name)) {
+      std::fill(host.begin(), host.begin() + n, 1.0f);
+    } else {
+      if (ikv_synth_normal_f32(seed, offset, n, std, host.data(), threads) != 0)
+        return infer::fail(std::errc::invalid_argument);
+      offset += n;
+    }
+    if (auto r = _backend->copy_tensor_set(t.get(), host.data(), 0, n * sizeof(float)); !r) return r;
+  }
+  return {};
+}
+
+infer::expected<Graph, std::error_code> Qwen3Model::build_graph(GraphContext &ctx) const {
+  Graph g;
+  Tensor *input_token = ctx.get_input_tokens();
+  Tensor *inp_pos = ctx.get_input_pos();
+  if (!input_token || !inp_pos) return infer::fail(std::errc::invalid_argument);
+  g.mark_input(input_token);
+  g.mark_input(inp_pos);
+  const int64_t n_tokens = inp_pos->dims[0];
+
+  AttentionSliceParams sp;
+  sp.n_head = _hp.n_head;
+  sp.n_head_kv = _hp.n_head_kv;
+  sp.head_dim = _hp.head_dim;
+  sp.rms_norm_eps = _hp.rms_norm_eps;
+  sp.rope_theta = _hp.rope_theta;
+  sp.n_ctx_train = _hp.n_ctx_train;
+  const float eps = _hp.rms_norm_eps;
+
+  Tensor *inpL = OpFactory::embedding(g, _token_embd, input_token);
+  for (uint32_t i = 0; i < _hp.n_layer; ++i) {
+    const Qwen3LayerWeights &L = _layers[i];
+    const std::string s = std::to_string(i);
+    Tensor *inpSA = inpL;
+    Tensor *cur = OpFactory::rms_norm(g, inpL, L.attn_norm, eps, "attn_norm_" + s);
+    Tensor *q = OpFactory::mul_mat(g, L.wq, cur, "q_proj" + s);
+    Tensor *k = OpFactory::mul_mat(g, L.wk, cur, "k_proj" + s);
+    Tensor *v = OpFactory::mul_mat(g, L.wv, cur, "v_proj" + s);
+    auto attn = build_attention_slice(g, ctx, q, k, v, L.attn_q_norm, L.attn_k_norm, i, sp);
+    if (!attn) return infer::unexpected(attn.error());
+    cur = OpFactory::reshape(g, *attn, {int64_t(_hp.head_dim) * _hp.n_head, n_tokens, 1, 1},
+                             "attn_reshape_" + s);
+    cur = OpFactory::mul_mat(g, L.wo, cur, "o_proj" + s);
+    Tensor *ffn_inp = OpFactory::add(g, cur, inpSA, "ffn_inp_" + s);
+    cur = OpFactory::rms_norm(g, ffn_inp, L.ffn_norm, eps, "ffn_norm_" + s);
+    Tensor *gate = OpFactory::mul_mat(g, L.ffn_gate, cur, "ffn_gate_" + s);
+    Tensor *up = OpFactory::mul_mat(g, L.ffn_up, cur, "ffn_up_" + s);
+    Tensor *gate_silu = OpFactory::silu(g, gate, "ffn_gate_silu_" + s);
+    Tensor *inter = OpFactory::mul(g, up, gate_silu, "ffn_inter_" + s);
+    Tensor *ffn_out = OpFactory::mul_mat(g, L.ffn_down, inter, "ffn_out_" + s);
+    inpL = OpFactory::add(g, ffn_out, ffn_inp, "result_out_" + s);
+  }
+  Tensor *final_norm = OpFactory::rms_norm(g, inpL, _output_norm, eps, "result_norm");
+  Tensor *logits = OpFactory::mul_mat(g, _token_embd, final_norm, "logits");  // tied output
+  g.mark_output(logits);
+  return g;
+}
+
+// ---------------------------------------------------------------------------
+// runner
+
+Qwen3Runner::Qwen3Runner(Qwen3Model &model, HIPBackend &backend, size_t capacity)
+    : _model(model), _backend(backend), _capacity(capacity) {}
+
+Qwen3Runner::~Qwen3Runner() {
+  if (_ctx) (void)_ctx->release_kv_access();
+  if (_kv && _seq != kInvalidSequenceId) (void)_kv->release_sequence(_seq);
+  if (_token_dev) (void)hipFree(_token_dev);
+}
+
+infer::expected<void, std::error_code> Qwen3Runner::init() {
+  const Qwen3Hparams &hp = _model.hparams();
+  std::vector<KVLayerSpec> specs(hp.n_layer, KVLayerSpec{hp.n_head_kv, hp.head_dim, hp.head_dim});
+  std::vector<Backend *> place(hp.n_layer, &_backend);
+  _kv = std::make_unique<KVCacheManager>(
+      std::make_unique<ContiguousKVStrategy>(std::make_unique<NaiveKVStorage>()));
+  if (auto r = _kv->init(specs, place,
+                         KVCacheConfig{.layers = hp.n_layer, .max_tokens_per_sequence = _capacity});
+      !r)
+    return r;
+  if (auto r = _backend.reserve_decode_workspace(int(hp.n_head), int(hp.n_head_kv), int(hp.head_dim),
+                                                 int64_t(_capacity));
+      !r)
+    return r;
+  _sched = std::make_unique<Scheduler>(&_backend);
+  _ctx = std::make_unique<GraphContext>(nullptr);
+  _tokens = _ctx->make_tensor("inp_tokens", GGML_TYPE_I32, {1});
+  _pos = _ctx->make_tensor("inp_pos", GGML_TYPE_I32, {1});
+  for (Tensor *t : {_tokens, _pos}) {
+    t->device = DeviceType::CPU;
+    t->tensorRole = TensorRole::TNESOR_ROLE_INPUT;
+  }
+  _ctx->set_input_tokens(_tokens);
+  _ctx->set_input_pos(_pos);
+  if (hipMalloc(&_token_dev, sizeof(int32_t)) != hipSuccess) {
+    (void)hipGetLastError();
+    return infer::fail(std::errc::not_enough_memory);
+  }
+  return {};
+}
+
+infer::expected<int32_t, std::error_code> Qwen3Runner::evaluate(const std::vector<int32_t> &input,
+                                                                bool sample,
+                                                                GenerationTiming &timing) {
+  using Clock = std::chrono::steady_clock;
+  const auto t0 = Clock::now();
+  auto n_past = _kv->length(_seq);
+  if (!n_past) return infer::unexpected(n_past.error());
+  if (auto r = _kv->reserve_append(_seq, input.size()); !r) return infer::unexpected(r.error());
+  _input = input;
+  _positions.resize(input.size());
+  for (size_t i = 0; i < input.size(); ++i) _positions[i] = int32_t(*n_past + i);
+  const int64_t n = int64_t(input.size());
+  for (Tensor *t : {_tokens, _pos}) {
+    t->dims = {n, 1, 1, 1};
+    t->set_contiguous_strides();
+  }
+  _tokens->data = _input.data();
+  _pos->data = _positions.data();
+
+  auto graph = _model.build_graph(*_ctx);
+  if (!graph) {
+    (void)_ctx->release_kv_access();
+    (void)_kv->abort_append(_seq);
+    return infer::unexpected(graph.error());
+  }
+  const auto t1 = Clock::now();
+  auto fail = [&](std::error_code e) -> infer::expected<int32_t, std::error_code> {
+    (void)_backend.synchronize();
+    (void)_ctx->release_kv_access();
+    (void)_kv->abort_append(_seq);
+    return infer::unexpected(e);
+  };
+  if (auto r = _sched->execute(*graph); !r) return fail(r.error());
+  const auto t2 = Clock::now();
+  int32_t token = -1;
+  if (sample) {
+    const Tensor *logits = graph->outputs().front();
+    const int64_t vocab = logits->dims[0];
+    const float *row = static_cast<const float *>(logits->data) + (n - 1) * vocab;
+    if (int rc = ikv_argmax_f32(row, vocab, _token_dev, _backend.stream()); rc != 0)
+      return fail(std::make_error_code(std::errc::io_error));
+    if (hipMemcpyAsync(&token, _token_dev, sizeof(int32_t), hipMemcpyDeviceToHost,
+                       _backend.stream()) != hipSuccess)
+      return fail(std::make_error_code(std::errc::io_error));
+  }
+  if (auto r = _backend.synchronize(); !r) return fail(r.error());
+  const auto t3 = Clock::now();
+  if (sample && token < 0) return fail(std::make_error_code(std::errc::invalid_argument));
+  if (auto r = _ctx->release_kv_access(); !r) return infer::unexpected(r.error());
+  if (auto r = _kv->commit_append(_seq); !r) return infer::unexpected(r.error());
+  timing.build_s += seconds(t0, t1);
+  timing.execute_s += seconds(t1, t2);
+  timing.sample_s += seconds(t2, t3);
+  return token;
+}
+
+infer::expected<void, std::error_code> Qwen3Runner::generate(const std::vector<int32_t> &prompt,
+                                                             size_t n_gen,
+                                                             std::vector<int32_t> &tokens_out,
+                                                             GenerationTiming &timing) {
+  using Clock = std::chrono::steady_clock;
+  if (prompt.empty() || n_gen == 0) return infer::fail(std::errc::invalid_argument);
+  if (prompt.size() + n_gen - 1 > _capacity) return infer::fail(std::errc::value_too_large);
+  if (!_kv) return infer::fail(std::errc::invalid_argument);
+  auto sid = _kv->create_sequence();
+  if (!sid) return infer::unexpected(sid.error());
+  _seq = *sid;
+  if (auto r = _ctx->set_kv_cache(_kv.get(), _seq); !r) return r;
+  timing = GenerationTiming{};
+  tokens_out.clear();
+  const auto start = Clock::now();
+  Clock::time_point first{}, last{};
+  std::vector<int32_t> ids = prompt;
+  for (size_t i = 0; i < n_gen; ++i) {
+    auto tok = evaluate(ids, true, timing);
+    if (!tok) {
+      (void)_ctx->set_kv_cache(nullptr, kInvalidSequenceId);
+      (void)_kv->release_sequence(_seq);
+      _seq = kInvalidSequenceId;
+      return infer::unexpected(tok.error());
+    }
+    const auto ready = Clock::now();
+    if (i == 0) first = ready;
+    last = ready;
+    tokens_out.push_back(*tok);
+    ids.assign(1, *tok);
+  }
+  timing.wall_s = seconds(start, Clock::now());
+  timing.ttft_s = seconds(start, first);
+  timing.tpot_s = n_gen > 1 ? seconds(first, last) / double(n_gen - 1) : 0.0;
+  (void)_ctx->set_kv_cache(nullptr, kInvalidSequenceId);
+  if (auto r = _kv->release_sequence(_seq); !r) return r;
+  _seq = kInvalidSequenceId;
+  return {};
+}

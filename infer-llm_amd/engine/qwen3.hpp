@@ -1,0 +1,123 @@
+// qwen3.hpp — the Qwen3 model graph and a generation runner on the HIP
+// backend: the caller side of the KV-cache path at model level.
+//
+// Qwen3Model restates Qwen3Model::build_graph (reference
+// src/models/Qwen3.cpp:4-136): embedding -> per layer [RMSNorm -> q/k/v
+// projections -> attention slice (reshape, qk-RMSNorm, RoPE, KV append,
+// flash attention) -> o_proj -> residual -> RMSNorm -> gate/up -> SiLU ->
+// mul -> down -> residual] -> RMSNorm -> logits. Weights carry the GGUF names
+// of ModelBase::load_weight (src/model.cpp:164-311) and live in one HBM
+// arena of the backend's WEIGHTS pool; the output projection is the tied
+// token embedding.
+//
+// Qwen3Runner restates the benchmark Runner (benchmarks/cpu/bench.cpp:
+// 130-219): per step reserve -> build graph -> execute -> sample -> commit,
+// with greedy sampling on the device (ikv_argmax_f32) and the reference's
+// TTFT / TPOT definitions (benchmarks/cpu/bench.cpp:239-281).
+#pragma once
+
+#include <chrono>
+#include <cstdint>
+#include <memory>
+#include <string>
+#include <system_error>
+#include <unordered_map>
+#include <vector>
+
+#include "expected.hpp"
+#include "graph.hpp"
+#include "hip_backend.hpp"
+#include "kvcache/kvcache_manager.hpp"
+#include "scheduler.hpp"
+
+struct Qwen3Hparams {
+  uint32_t n_layer = 28;
+  uint32_t n_embd = 1024;
+  uint32_t n_head = 16;
+  uint32_t n_head_kv = 8;
+  uint32_t head_dim = 128;
+  uint32_t n_ff = 3072;
+  uint32_t n_vocab = 151936;
+  uint32_t n_ctx_train = 40960;
+  float rope_theta = 1e6f;
+  float rms_norm_eps = 1e-6f;
+};
+
+struct Qwen3LayerWeights {
+  Tensor *attn_norm = nullptr, *wq = nullptr, *wk = nullptr, *wv = nullptr;
+  Tensor *attn_q_norm = nullptr, *attn_k_norm = nullptr, *wo = nullptr, *ffn_norm = nullptr;
+  Tensor *ffn_gate = nullptr, *ffn_up = nullptr, *ffn_down = nullptr;
+};
+
+class Qwen3Model {
+ public:
+  explicit Qwen3Model(const Qwen3Hparams &hp);
+  ~Qwen3Model();
+  Qwen3Model(const Qwen3Model &) = delete;
+  Qwen3Model &operator=(const Qwen3Model &) = delete;
+
+  // One WEIGHTS allocation for every tensor (256-byte aligned each).
+  infer::expected<void, std::error_code> alloc_weights(Backend *backend);
+  // Names in the order the synthetic initialiser draws them.
+  std::vector<std::string> tensor_names() const;
+  Tensor *find(const std::string &name) const;
+  // Host -> device copy of one weight (count floats).
+  infer::expected<void, std::error_code> set_tensor(const std::string &name, const float *host,
+                                                    size_t count);
+  // Random-init weights of the benchmark configurations: every matrix
+  // N(0, std^2) from one counter-based stream (ikv_synth_normal_f32) in
+  // tensor_names() order, norm weights 1.0.
+  infer::expected<void, std::error_code> init_synthetic(uint64_t seed, double std, int threads);
+
+  infer::expected<Graph, std::error_code> build_graph(GraphContext &ctx) const;
+  const Qwen3Hparams &hparams() const { return _hp; }
+  size_t weight_bytes() const { return _arena_bytes; }
+
+ private:
+  Tensor *make(const std::string &name, std::initializer_list<int64_t> shape);
+
+  Qwen3Hparams _hp;
+  Backend *_backend = nullptr;
+  void *_arena = nullptr;
+  size_t _arena_bytes = 0;
+  std::vector<std::unique_ptr<Tensor>> _tensors;
+  std::unordered_map<std::string, Tensor *> _map;
+  Tensor *_token_embd = nullptr, *_output_norm = nullptr;
+  std::vector<Qwen3LayerWeights> _layers;
+};
+
+struct GenerationTiming {
+  double ttft_s = 0;      // first sampled token - start
+  double tpot_s = 0;      // (last - first) / (n_gen - 1)
+  double wall_s = 0;
+  double build_s = 0;     // graph construction, summed over steps
+  double execute_s = 0;   // scheduling + enqueue, summed
+  double sample_s = 0;    // device argmax + token read-back (waits for the step), summed
+};
+
+class Qwen3Runner {
+ public:
+  Qwen3Runner(Qwen3Model &model, HIPBackend &backend, size_t capacity);
+  ~Qwen3Runner();
+  infer::expected<void, std::error_code> init();
+  // prompt, then n_gen greedy tokens (the first from the prompt's last
+  // logits row); tokens_out receives the n_gen sampled ids.
+  infer::expected<void, std::error_code> generate(const std::vector<int32_t> &prompt, size_t n_gen,
+                                                  std::vector<int32_t> &tokens_out,
+                                                  GenerationTiming &timing);
+
+ private:
+  infer::expected<int32_t, std::error_code> evaluate(const std::vector<int32_t> &input, bool sample,
+                                                     GenerationTiming &timing);
+
+  Qwen3Model &_model;
+  HIPBackend &_backend;
+  size_t _capacity;
+  std::unique_ptr<KVCacheManager> _kv;
+  std::unique_ptr<Scheduler> _sched;
+  std::unique_ptr<GraphContext> _ctx;
+  SequenceId _seq = kInvalidSequenceId;
+  Tensor *_tokens = nullptr, *_pos = nullptr;
+  std::vector<int32_t> _input, _positions;
+  int32_t *_token_dev = nullptr;
+};

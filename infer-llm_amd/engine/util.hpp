@@ -53,6 +53,21 @@ enum class OperationType : uint32_t {
   GGML_OP_COUNT = 101,
 };
 
+// Sub-op ids of GGML_OP_UNARY (include/util.hpp:198-215).
+enum class UnaryOp : uint32_t {
+  GGML_UNARY_OP_ABS = 0,
+  GGML_UNARY_OP_SGN,
+  GGML_UNARY_OP_NEG,
+  GGML_UNARY_OP_STEP,
+  GGML_UNARY_OP_TANH,
+  GGML_UNARY_OP_ELU,
+  GGML_UNARY_OP_RELU,
+  GGML_UNARY_OP_SIGMOID,
+  GGML_UNARY_OP_GELU,
+  GGML_UNARY_OP_GELU_QUICK,
+  GGML_UNARY_OP_SILU,
+};
+
 enum class DeviceType : uint8_t {
   CPU = 0,
   CUDA = 1,

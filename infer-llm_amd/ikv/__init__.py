@@ -56,6 +56,26 @@ SIGNATURES = {
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int64, _c_int, _c_int, _c_float,
          _c_void_p, _c_void_p, _c_int64, _c_void_p, _c_void_p],
     ),
+    # include/ikv_model.h
+    "ikv_mul_mat_f32": (
+        _c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int64, _c_int64, _c_int64, _c_void_p, _c_void_p]),
+    "ikv_gemv3_f32": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+         _c_int64, _c_int64, _c_int64, _c_int64, _c_void_p],
+    ),
+    "ikv_gemv_swiglu_f32": (
+        _c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int64, _c_int64, _c_void_p]),
+    "ikv_get_rows_f32": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_int64, _c_int64, _c_int64, _c_void_p, _c_void_p]),
+    "ikv_add_f32": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int64, _c_void_p]),
+    "ikv_mul_f32": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int64, _c_void_p]),
+    "ikv_silu_f32": (_c_int, [_c_void_p, _c_void_p, _c_int64, _c_void_p]),
+    "ikv_argmax_f32": (_c_int, [_c_void_p, _c_int64, _c_void_p, _c_void_p]),
+    "ikv_synth_normal_f32": (
+        _c_int, [ctypes.c_uint64, ctypes.c_uint64, _c_size_t, ctypes.c_double, _c_void_p, _c_int]),
+    # include/ikv_probe.h
     "ikv_probe_read": (_c_int, [_c_void_p, _c_size_t, _c_void_p, _c_int, _c_void_p]),
     "ikv_probe_empty": (_c_int, [_c_int, _c_void_p]),
 }
@@ -271,4 +291,87 @@ def qk_norm_rope(x, w, pos, eps: float, sin_tab, cos_tab, out=None, status=None,
                                      eps, _ptr(sin_tab), _ptr(cos_tab), sin_tab.shape[0],
                                      _ptr(status), _stream(stream))
     _check("ikv_qk_norm_rope_f32", rc)
+    return out
+
+
+# ----------------------------------------------------------------------------
+# ops around the path (include/ikv_model.h)
+# ----------------------------------------------------------------------------
+
+def mul_mat(w, x, out=None, residual=None, stream=None):
+    """out[m, n] = x[m, :] . w[n, :] (+ residual); w [n_out, k], x [m, k] or [k]."""
+    torch = _torch()
+    _need_f32_dev("w", w)
+    _need_f32_dev("x", x)
+    n_out, k = w.shape
+    m = x.numel() // k
+    if x.numel() != m * k:
+        raise ValueError("x length must be a multiple of k")
+    if out is None:
+        out = torch.empty((m, n_out) if x.dim() > 1 else (n_out,), device=x.device)
+    _check("ikv_mul_mat_f32", load().ikv_mul_mat_f32(_ptr(w), _ptr(x), _ptr(out), n_out, k, m,
+                                                      _ptr(residual), _stream(stream)))
+    return out
+
+
+def gemv3(w0, w1, w2, x, stream=None):
+    torch = _torch()
+    k = x.numel()
+    outs = [torch.empty(w.shape[0], device=x.device) for w in (w0, w1, w2)]
+    _check("ikv_gemv3_f32", load().ikv_gemv3_f32(
+        _ptr(w0), _ptr(w1), _ptr(w2), _ptr(x), _ptr(outs[0]), _ptr(outs[1]), _ptr(outs[2]),
+        w0.shape[0], w1.shape[0], w2.shape[0], k, _stream(stream)))
+    return outs
+
+
+def gemv_swiglu(w_gate, w_up, x, out=None, stream=None):
+    torch = _torch()
+    n_out, k = w_gate.shape
+    if out is None:
+        out = torch.empty(n_out, device=x.device)
+    _check("ikv_gemv_swiglu_f32", load().ikv_gemv_swiglu_f32(
+        _ptr(w_gate), _ptr(w_up), _ptr(x), _ptr(out), n_out, k, _stream(stream)))
+    return out
+
+
+def get_rows(table, ids, out=None, status=None, stream=None):
+    torch = _torch()
+    n_rows, row_len = table.shape
+    if out is None:
+        out = torch.empty((ids.numel(), row_len), device=table.device)
+    _check("ikv_get_rows_f32", load().ikv_get_rows_f32(
+        _ptr(table), _ptr(ids), _ptr(out), ids.numel(), row_len, n_rows, _ptr(status),
+        _stream(stream)))
+    return out
+
+
+def elementwise(op: str, a, b=None, out=None, stream=None):
+    torch = _torch()
+    if out is None:
+        out = torch.empty_like(a)
+    lib = load()
+    if op == "silu":
+        rc = lib.ikv_silu_f32(_ptr(a), _ptr(out), a.numel(), _stream(stream))
+    else:
+        rc = getattr(lib, f"ikv_{op}_f32")(_ptr(a), _ptr(b), _ptr(out), a.numel(), _stream(stream))
+    _check(f"ikv_{op}_f32", rc)
+    return out
+
+
+def argmax(logits, token=None, stream=None):
+    """Device int32 [1]: greedy token of logits (ties -> lowest id; -1 on NaN/+inf)."""
+    torch = _torch()
+    if token is None:
+        token = torch.empty(1, dtype=torch.int32, device=logits.device)
+    _check("ikv_argmax_f32", load().ikv_argmax_f32(_ptr(logits), logits.numel(), _ptr(token),
+                                                    _stream(stream)))
+    return token
+
+
+def synth_normal(seed: int, shape, std: float = 1.0, offset: int = 0, threads: int = 8):
+    """Host float32 N(0, std^2) array from the product's synthetic initialiser."""
+    import numpy as np
+    out = np.empty(shape, dtype=np.float32)
+    _check("ikv_synth_normal_f32", load().ikv_synth_normal_f32(
+        seed & 0xFFFFFFFFFFFFFFFF, offset, out.size, std, out.ctypes.data, threads))
     return out

@@ -14,6 +14,7 @@
  * std::sin / std::cos / std::pow on floats are expf / sinf / cosf / powf.
  */
 #include "oracle.h"
+#include "oracle_pool.h"
 
 #include <math.h>
 #include <pthread.h>
@@ -131,6 +132,10 @@ static void parallel_for(int64_t n, task_fn fn, void *ctx) {
     pthread_mutex_lock(&g_pool.mtx);
     while (g_pool.n_done != g_pool.n_threads) pthread_cond_wait(&g_pool.cv_done, &g_pool.mtx);
     pthread_mutex_unlock(&g_pool.mtx);
+}
+
+void oracle_pool_for(int64_t n, void (*fn)(int64_t i, void *ctx), void *ctx) {
+    parallel_for(n, fn, ctx);
 }
 
 /* ------------------------------------------------------------------ */

@@ -19,6 +19,14 @@
  *                          mean(V); GQA head permutation; causal future
  *                          perturbation; decode == prefill row
  *   oracle_cpy             byte equality + sentinel bytes untouched
+ *   oracle_mul_mat_f32     float64 brute force; identity matrix; rows of w
+ *                          selected by one-hot x are returned exactly
+ *   oracle_get_rows_f32    rows equal the table's rows bytewise
+ *   oracle_silu_f32        closed forms silu(0) = 0, silu(x) - silu(-x) = x
+ *   oracle_sample_greedy   ties -> lowest id; NaN / +inf / all -inf -> -1
+ *   oracle_qwen3_step      op-by-op recomposition from the functions above
+ *                          (float64 brute force of a one-layer model);
+ *                          cached decode == recompute of the whole prefix
  */
 #ifndef IKV_ORACLE_H
 #define IKV_ORACLE_H
@@ -80,6 +88,57 @@ void oracle_decode_append_attn_f32(const float *q, const float *k_new,
                                    float *v_cache, float *out,
                                    int64_t head_dim, int64_t n_head,
                                    int64_t n_head_kv, int64_t n_past);
+
+/* ---- ops around the path and the whole Qwen3 step (oracle_model.c) ---- */
+
+/* compute_get_rows (src/backends/cpu_backend.cpp:259-332): out[i] =
+ * table[ids[i]], rows of row_len floats. Returns -22 for an id outside
+ * [0, n_rows) (the reference reads outside the table there). */
+int oracle_get_rows_f32(const float *table, const int32_t *ids, float *out, int64_t n_ids,
+                        int64_t row_len, int64_t n_rows);
+
+/* compute_mul_mat (src/backends/cpu_backend.cpp:386-424): out[t][o] =
+ * sum_k x[t][k] * w[o][k], one float accumulator from 0.0f in index order,
+ * one pool task per output element. w: [n_out][k]; x: [m][k]. */
+void oracle_mul_mat_f32(const float *w, const float *x, float *out, int64_t n_out, int64_t k,
+                        int64_t m);
+
+/* compute_add / compute_mul / compute_silu (src/backends/cpu_backend.cpp:
+ * 636-703) over n floats; out may equal an input. */
+void oracle_add_f32(const float *a, const float *b, float *out, int64_t n);
+void oracle_mul_f32(const float *a, const float *b, float *out, int64_t n);
+void oracle_silu_f32(const float *x, float *out, int64_t n);
+
+/* sample_greedy (src/sampler.cpp:42-65): argmax, ties -> lowest id; -1 for
+ * NaN, +inf, all -inf or n <= 0 (the reference's invalid_argument). */
+int32_t oracle_sample_greedy(const float *logits, int64_t n);
+
+typedef struct {
+    int64_t n_layer, n_embd, n_head, n_head_kv, head_dim, n_ff, n_vocab, n_ctx_train;
+    float rms_eps, rope_theta;
+} oracle_qwen3_hparams;
+
+/* One layer's weights, rows as in the reference's ggml tensors
+ * (src/model.cpp:192-306): wq [n_head*head_dim][n_embd], wk/wv
+ * [n_head_kv*head_dim][n_embd], wo [n_embd][n_head*head_dim], ffn_gate/up
+ * [n_ff][n_embd], ffn_down [n_embd][n_ff]; norms [n_embd] / [head_dim]. */
+typedef struct {
+    const float *attn_norm, *wq, *wk, *wv, *q_norm, *k_norm, *wo, *ffn_norm, *ffn_gate, *ffn_up,
+        *ffn_down;
+} oracle_qwen3_layer;
+
+/* One step of Qwen3Model::build_graph (src/models/Qwen3.cpp:4-136) with the
+ * ops above, in graph order: tokens at positions n_past .. n_past+n_tokens-1;
+ * appends this step's K (after RoPE) and V to k_cache[l] / v_cache[l]
+ * ([capacity][n_head_kv][head_dim]) at n_past; theta: the angle table
+ * [n_ctx_train][head_dim/2]; logits: [n_tokens][n_vocab] (only the last row
+ * is computed when last_row_only). output is the tied token_embd when the
+ * model has no separate output weight. Returns 0, -22 or -12. */
+int oracle_qwen3_step(const oracle_qwen3_hparams *hp, const oracle_qwen3_layer *layers,
+                      const float *token_embd, const float *output_norm, const float *output,
+                      const float *theta, const int32_t *tokens, int64_t n_tokens, int64_t n_past,
+                      float *const *k_cache, float *const *v_cache, float *logits,
+                      int last_row_only);
 
 #ifdef __cplusplus
 }
