@@ -80,6 +80,27 @@ int ikv_attn_decode_f32(const float *q, float *k_cache, float *v_cache, const fl
                         void *stream);
 
 /* ---------------------------------------------------------------------
+ * Decode with the step's qk-RMSNorm + RoPE folded into the same launch:
+ *   q     = rope(rms_norm(q_raw, q_norm_w)),  k = rope(rms_norm(k_raw, k_norm_w))
+ * per head row (ikv_qk_norm_rope_f32's arithmetic, at position pos[0]), then
+ * k (rotated) and v_new are appended at row n_kv-1 and ikv_attn_decode_f32's
+ * attention runs — the RMS_NORM -> ROPE -> CPY -> VIEW -> FLASH_ATTN_EXT
+ * chain of one Qwen3 layer for one token (src/models/Qwen3.cpp:66-83). The
+ * appended key row is bit-identical to the one the separate ops produce.
+ * q_raw [n_head][head_dim], k_raw / v_new [n_head_kv][head_dim]; norm
+ * weights [head_dim]; pos: device int32; sin/cos tables [n_ctx][head_dim/2]
+ * as for ikv_rope_neox_f32. A position outside [0, n_ctx) does not fault:
+ * q and k become zero rows and *status (device int, if non-NULL) is set to 1.
+ * Workspace and other arguments as for ikv_attn_decode_f32.
+ * ------------------------------------------------------------------- */
+int ikv_attn_decode_rope_f32(const float *q_raw, const float *k_raw, const float *v_new,
+                             float *k_cache, float *v_cache, float *out, int n_head, int n_head_kv,
+                             int head_dim, int64_t n_kv, float scale, const float *q_norm_w,
+                             const float *k_norm_w, float eps, const int32_t *pos,
+                             const float *sin_tab, const float *cos_tab, int64_t n_ctx,
+                             int *status, void *workspace, size_t workspace_bytes, void *stream);
+
+/* ---------------------------------------------------------------------
  * Prefill / general attention, n_q >= 1 query tokens, causal: key j is
  * visible to query t iff j <= n_past + t (src/backends/cpu_backend.cpp:578,
  * src/kernels/cuda/kernel_f32.cu:346). F32 MFMA tiles; K/V tiles staged in
@@ -93,9 +114,16 @@ int ikv_attn_prefill_f32(const float *q, const float *k, const float *v, float *
 
 /* ---------------------------------------------------------------------
  * RMS norm over rows of `dim` floats: out = (x * s) * w with
- * s = float(1 / sqrt(sum_d double(x_d*x_d) / dim + eps)), the sum taken in
- * double in index order — the arithmetic of CPUBackend::compute_rms_norm
- * (src/backends/cpu_backend.cpp:335-382), so results are bit-identical to it.
+ * s = float(1 / sqrt(sum_d double(x_d*x_d) / dim + eps)) — the arithmetic of
+ * CPUBackend::compute_rms_norm (src/backends/cpu_backend.cpp:335-382).
+ * Rows shorter than 512 floats (head rows) take the double sum in index
+ * order, so results are bit-identical to the reference. Rows of 512 or more
+ * floats with dim % 256 == 0 (model-width rows) take it in a fixed
+ * lane-strided order (lane l of a wavefront adds elements 256*j + 4*l + c,
+ * then an xor butterfly): the float scale equals the reference's unless the
+ * two double sums straddle a float rounding boundary (about 2^-27 of rows),
+ * and equals that of the norm folded into ikv_gemv3_f32 /
+ * ikv_gemv_swiglu_f32 bit for bit.
  * Replaces CUDA_F32::compute_rms_norm (src/kernels/cuda/kernel_f32.cu:16-90).
  * ------------------------------------------------------------------- */
 int ikv_rms_norm_f32(const float *x, const float *w, float *out, int64_t rows, int64_t dim,

@@ -68,7 +68,8 @@ int ikv_qwen3_generate(ikv_qwen3 *m, const int32_t *prompt, int64_t n_prompt, in
 
 /* Fusions taken and kernel launches in the last step. */
 typedef struct ikv_qwen3_stats {
-    int launches, fused_norm_rope, fused_append_decode, fused_swiglu, fused_residual, fused_qkv;
+    int launches, fused_norm_rope, fused_append_decode, fused_swiglu, fused_residual, fused_qkv,
+        fused_norm_mm, fused_rope_decode;
 } ikv_qwen3_stats;
 int ikv_qwen3_last_stats(const ikv_qwen3 *m, ikv_qwen3_stats *out);
 /* 0 disables the HIP backend's graph fusions (every node its own launch). */

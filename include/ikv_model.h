@@ -39,17 +39,21 @@ int ikv_mul_mat_f32(const float *w, const float *x, float *out, int64_t n_out, i
 
 /* Three projections of one input in one launch (the q, k, v projections of
  * a Qwen3 layer, src/models/Qwen3.cpp:56-58), m == 1:
- * out_i = w_i · x for i = 0, 1, 2 with w_i [n_i][k]. */
+ * out_i = w_i · x' for i = 0, 1, 2 with w_i [n_i][k], where x' = x, or, when
+ * norm_w is not NULL, x' = ikv_rms_norm_f32(x, norm_w, eps) (the layer's
+ * attn_norm folded in; k % 1024 == 0 and 16-byte aligned operands, else
+ * -ENOTSUP). */
 int ikv_gemv3_f32(const float *w0, const float *w1, const float *w2, const float *x, float *out0,
                   float *out1, float *out2, int64_t n0, int64_t n1, int64_t n2, int64_t k,
-                  void *stream);
+                  const float *norm_w, float eps, void *stream);
 
-/* SwiGLU FFN input, m == 1: out[n] = (w_up[n] · x) * silu(w_gate[n] · x) —
+/* SwiGLU FFN input, m == 1: out[n] = (w_up[n] · x') * silu(w_gate[n] · x') —
  * mul_mat(ffn_gate), mul_mat(ffn_up), silu, mul of Qwen3Model::build_graph
  * (src/models/Qwen3.cpp:103-113) in one launch; silu(g) = g / (1 + exp(-g))
- * (src/backends/cpu_backend.cpp:660-673). */
+ * (src/backends/cpu_backend.cpp:660-673). x' as for ikv_gemv3_f32 (ffn_norm
+ * folded in when norm_w is not NULL). */
 int ikv_gemv_swiglu_f32(const float *w_gate, const float *w_up, const float *x, float *out,
-                        int64_t n_out, int64_t k, void *stream);
+                        int64_t n_out, int64_t k, const float *norm_w, float eps, void *stream);
 
 /* ---------------------------------------------------------------------
  * get_rows: out[i][:] = table[ids[i]][:] for i < n_ids, rows of row_len

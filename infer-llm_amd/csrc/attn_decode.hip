@@ -33,6 +33,15 @@
 // Fused append: the row of the new token (n_kv-1) is read from k_new/v_new
 // instead of the cache, and the workgroup that owns it stores it into the
 // cache unchanged (a 16-byte copy, bit-exact).
+//
+// Fused qk-RMSNorm + RoPE (ikv_attn_decode_rope_f32): q and k_new arrive as
+// projected; every workgroup stages its G query rows and the KV head's new
+// key row in LDS, one lane per row adds the float squares in double in index
+// order (the reference's loop), and all lanes then normalise and rotate the
+// RoPE pairs with the resident sin/cos tables — the arithmetic of
+// ikv_qk_norm_rope_f32 with contraction off, so the key row appended to the
+// cache is bit-identical to the one the separate ops produce. The K/V loads of
+// the first tile are issued before this prologue and land during it.
 #include "ikv_common.hpp"
 #include "../../include/ikv.h"
 
@@ -74,6 +83,16 @@ constexpr int kCounterStride = 64;
 struct Plan {
   int n_splits;
   int tokens_per_split;
+};
+
+// qk-RMSNorm + RoPE folded into the launch (all pointers device memory).
+struct Prologue {
+  const float *q_norm_w = nullptr, *k_norm_w = nullptr;
+  float eps = 0.f;
+  const int32_t *pos = nullptr;  // pos[0]: the new token's position
+  const float *sin_tab = nullptr, *cos_tab = nullptr;
+  int64_t n_ctx = 0;
+  int *status = nullptr;
 };
 
 Plan plan_for(int n_head, int n_head_kv, int64_t n_kv) {
@@ -191,6 +210,62 @@ __device__ __forceinline__ void merge_waves(const float (&s_acc)[NWAVE][G][D],
   }
 }
 
+// Stages q rows g*G .. g*G+G-1 and the new key row of KV head g into s, then
+// applies RMSNorm (ordered double sum per row, one lane per row) and NeoX
+// RoPE at position pos[0]: s[h] = rope(norm(q_h)), s[G] = rope(norm(k_g)).
+// A position outside [0, n_ctx) gives zero rows and raises *status.
+template <int G>
+__device__ __forceinline__ void qk_prologue(const Prologue &pro, const float *q, const float *k_new, int g,
+                            float (&s)[G + 1][D], float (&scl)[G + 1]) {
+#pragma clang fp contract(off)
+  const int tid = threadIdx.x;
+  const int32_t p = pro.pos[0];
+  const bool ok = p >= 0 && p < pro.n_ctx;
+  for (int i = tid; i < (G + 1) * D; i += WG) {
+    const int r = i / D;
+    const int d = i - r * D;
+    s[r][d] = r < G ? q[static_cast<size_t>(g * G + r) * D + d] : k_new[static_cast<size_t>(g) * D + d];
+  }
+  __syncthreads();
+  if (tid <= G) {
+    double sum = 0.0;
+#pragma unroll 8
+    for (int d = 0; d < D; ++d) {
+      const float xv = s[tid][d];
+      const float sq = xv * xv;
+      sum += static_cast<double>(sq);
+    }
+    scl[tid] = static_cast<float>(1.0 / sqrt(sum / static_cast<double>(D) + static_cast<double>(pro.eps)));
+  }
+  __syncthreads();
+  constexpr int hd = D / 2;
+  for (int i = tid; i < (G + 1) * hd; i += WG) {
+    const int r = i / hd;
+    const int j = i - r * hd;
+    const float *w = r < G ? pro.q_norm_w : pro.k_norm_w;
+    const float sc = scl[r];
+    const float t0 = s[r][j] * sc;
+    const float t1 = s[r][j + hd] * sc;
+    const float x0 = t0 * w[j];
+    const float x1 = t1 * w[j + hd];
+    float o0 = 0.f, o1 = 0.f;
+    if (ok) {
+      const float c = pro.cos_tab[static_cast<int64_t>(p) * hd + j];
+      const float sn = pro.sin_tab[static_cast<int64_t>(p) * hd + j];
+      const float a = x0 * c;
+      const float b = x1 * sn;
+      const float e = x0 * sn;
+      const float f = x1 * c;
+      o0 = a - b;
+      o1 = e + f;
+    }
+    s[r][j] = o0;
+    s[r][j + hd] = o1;
+  }
+  if (!ok && tid == 0 && pro.status) *pro.status = 1;
+  __syncthreads();
+}
+
 // LDS of the merging workgroup.
 struct MergeLds {
   float w[kMergeCap];    // per (h, split): max, then the weight 2^(max - M_h)
@@ -204,7 +279,7 @@ struct MergeLds {
 // the first chunk of partial outputs are loaded together, so a context whose
 // splits fit one chunk costs one memory round trip.
 template <int G>
-__device__ void merge_splits(const float *part_ml, const float *part_o, float *out, int g,
+__device__ __forceinline__ void merge_splits(const float *part_ml, const float *part_o, float *out, int g,
                              int n_splits, MergeLds &lds) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -297,11 +372,11 @@ __device__ void merge_splits(const float *part_ml, const float *part_o, float *o
   }
 }
 
-template <int G>
-__global__ __launch_bounds__(WG) void decode_kernel(
+template <int G, bool PRO>
+__global__ __launch_bounds__(WG, G <= 4 ? 4 : 2) void decode_kernel(
     const float *__restrict__ q, float *kc, float *vc, const float *k_new, const float *v_new,
     float *__restrict__ out, int *counters, float *part_ml, float *part_o, int n_head_kv, int n_kv,
-    int tokens_per_split, int n_splits, float scale_log2) {
+    int tokens_per_split, int n_splits, float scale_log2, Prologue pro) {
   __shared__ float s_acc[NWAVE][G][D];
   __shared__ float s_m[NWAVE][G];
   __shared__ float s_l[NWAVE][G];
@@ -326,9 +401,19 @@ __global__ __launch_bounds__(WG) void decode_kernel(
                head_off);
 
   float4 qv[G];
+  float4 knew_rot = make_float4(0.f, 0.f, 0.f, 0.f);  // this lane's piece of rope(norm(k_new))
+  if constexpr (PRO) {
+    __shared__ float s_qk[G + 1][D];
+    __shared__ float s_scl[G + 1];
+    qk_prologue<G>(pro, q, k_new, g, s_qk, s_scl);
 #pragma unroll
-  for (int h = 0; h < G; ++h)
-    qv[h] = *reinterpret_cast<const float4 *>(q + static_cast<size_t>(g * G + h) * D + 4 * sub);
+    for (int h = 0; h < G; ++h) qv[h] = *reinterpret_cast<const float4 *>(&s_qk[h][4 * sub]);
+    knew_rot = *reinterpret_cast<const float4 *>(&s_qk[G][4 * sub]);
+  } else {
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+      qv[h] = *reinterpret_cast<const float4 *>(q + static_cast<size_t>(g * G + h) * D + 4 * sub);
+  }
 
   float m[G], l[G];
   float4 acc[G];
@@ -351,6 +436,7 @@ __global__ __launch_bounds__(WG) void decode_kernel(
       for (int r = 0; r < R; ++r) {
         const int t = base + r * (NWAVE * 2) + wave * 2 + half;
         if (t == new_row) {
+          if constexpr (PRO) kr[r] = knew_rot;  // the appended key is the rotated one
           const size_t off = static_cast<size_t>(new_row) * tok_stride + head_off;
           *reinterpret_cast<float4 *>(kc + off) = kr[r];
           *reinterpret_cast<float4 *>(vc + off) = vr[r];
@@ -458,33 +544,26 @@ __global__ __launch_bounds__(WG) void decode_kernel(
   merge_splits<G>(part_ml, part_o, out, g, n_splits, s_merge);
 }
 
+bool supported_group(int G) { return G == 1 || G == 2 || G == 4 || G == 8; }
+
 template <int G>
 void launch(const float *q, float *kc, float *vc, const float *kn, const float *vn, float *out,
             int *counters, float *part_ml, float *part_o, int n_head_kv, int n_kv, const Plan &p,
-            float scale_log2, hipStream_t s) {
-  decode_kernel<G><<<n_head_kv * p.n_splits, WG, 0, s>>>(q, kc, vc, kn, vn, out, counters,
-                                                          part_ml, part_o, n_head_kv, n_kv,
-                                                          p.tokens_per_split, p.n_splits,
-                                                          scale_log2);
+            float scale_log2, const Prologue *pro, hipStream_t s) {
+  if (pro)
+    decode_kernel<G, true><<<n_head_kv * p.n_splits, WG, 0, s>>>(
+        q, kc, vc, kn, vn, out, counters, part_ml, part_o, n_head_kv, n_kv, p.tokens_per_split,
+        p.n_splits, scale_log2, *pro);
+  else
+    decode_kernel<G, false><<<n_head_kv * p.n_splits, WG, 0, s>>>(
+        q, kc, vc, kn, vn, out, counters, part_ml, part_o, n_head_kv, n_kv, p.tokens_per_split,
+        p.n_splits, scale_log2, Prologue{});
 }
 
-bool supported_group(int G) { return G == 1 || G == 2 || G == 4 || G == 8; }
-
-}  // namespace
-
-extern "C" size_t ikv_attn_decode_workspace_bytes(int n_head, int n_head_kv, int head_dim,
-                                                  int64_t n_kv) {
-  if (n_head <= 0 || n_head_kv <= 0 || n_head % n_head_kv != 0 || head_dim != D || n_kv <= 0)
-    return 0;
-  if (!supported_group(n_head / n_head_kv) || n_kv > INT_MAX - 2 * TILE) return 0;
-  const Plan p = plan_for(n_head, n_head_kv, n_kv);
-  return ws_layout(n_head, n_head_kv, p.n_splits).total;
-}
-
-extern "C" int ikv_attn_decode_f32(const float *q, float *k_cache, float *v_cache,
-                                   const float *k_new, const float *v_new, float *out, int n_head,
-                                   int n_head_kv, int head_dim, int64_t n_kv, float scale,
-                                   void *workspace, size_t workspace_bytes, void *stream) {
+int decode_common(const float *q, float *k_cache, float *v_cache, const float *k_new,
+                  const float *v_new, float *out, int n_head, int n_head_kv, int head_dim,
+                  int64_t n_kv, float scale, void *workspace, size_t workspace_bytes,
+                  const Prologue *pro, void *stream) {
   if (!q || !k_cache || !v_cache || !out) return -EINVAL;
   if ((k_new == nullptr) != (v_new == nullptr)) return -EINVAL;
   if (n_head <= 0 || n_head_kv <= 0 || n_head % n_head_kv != 0) return -EINVAL;
@@ -512,10 +591,51 @@ extern "C" int ikv_attn_decode_f32(const float *q, float *k_cache, float *v_cach
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int nk = static_cast<int>(n_kv);
   switch (G) {
-    case 1: launch<1>(q, k_cache, v_cache, k_new, v_new, out, counters, part_ml, part_o, n_head_kv, nk, p, sl2, s); break;
-    case 2: launch<2>(q, k_cache, v_cache, k_new, v_new, out, counters, part_ml, part_o, n_head_kv, nk, p, sl2, s); break;
-    case 4: launch<4>(q, k_cache, v_cache, k_new, v_new, out, counters, part_ml, part_o, n_head_kv, nk, p, sl2, s); break;
-    default: launch<8>(q, k_cache, v_cache, k_new, v_new, out, counters, part_ml, part_o, n_head_kv, nk, p, sl2, s); break;
+    case 1: launch<1>(q, k_cache, v_cache, k_new, v_new, out, counters, part_ml, part_o, n_head_kv, nk, p, sl2, pro, s); break;
+    case 2: launch<2>(q, k_cache, v_cache, k_new, v_new, out, counters, part_ml, part_o, n_head_kv, nk, p, sl2, pro, s); break;
+    case 4: launch<4>(q, k_cache, v_cache, k_new, v_new, out, counters, part_ml, part_o, n_head_kv, nk, p, sl2, pro, s); break;
+    default: launch<8>(q, k_cache, v_cache, k_new, v_new, out, counters, part_ml, part_o, n_head_kv, nk, p, sl2, pro, s); break;
   }
   return ikv::launch_status();
+}
+
+}  // namespace
+
+extern "C" size_t ikv_attn_decode_workspace_bytes(int n_head, int n_head_kv, int head_dim,
+                                                  int64_t n_kv) {
+  if (n_head <= 0 || n_head_kv <= 0 || n_head % n_head_kv != 0 || head_dim != D || n_kv <= 0)
+    return 0;
+  if (!supported_group(n_head / n_head_kv) || n_kv > INT_MAX - 2 * TILE) return 0;
+  const Plan p = plan_for(n_head, n_head_kv, n_kv);
+  return ws_layout(n_head, n_head_kv, p.n_splits).total;
+}
+
+extern "C" int ikv_attn_decode_f32(const float *q, float *k_cache, float *v_cache,
+                                   const float *k_new, const float *v_new, float *out, int n_head,
+                                   int n_head_kv, int head_dim, int64_t n_kv, float scale,
+                                   void *workspace, size_t workspace_bytes, void *stream) {
+  return decode_common(q, k_cache, v_cache, k_new, v_new, out, n_head, n_head_kv, head_dim, n_kv,
+                       scale, workspace, workspace_bytes, nullptr, stream);
+}
+
+extern "C" int ikv_attn_decode_rope_f32(const float *q_raw, const float *k_raw, const float *v_new,
+                                        float *k_cache, float *v_cache, float *out, int n_head,
+                                        int n_head_kv, int head_dim, int64_t n_kv, float scale,
+                                        const float *q_norm_w, const float *k_norm_w, float eps,
+                                        const int32_t *pos, const float *sin_tab,
+                                        const float *cos_tab, int64_t n_ctx, int *status,
+                                        void *workspace, size_t workspace_bytes, void *stream) {
+  if (!k_raw || !v_new || !q_norm_w || !k_norm_w || !pos || !sin_tab || !cos_tab || n_ctx <= 0)
+    return -EINVAL;
+  Prologue pro;
+  pro.q_norm_w = q_norm_w;
+  pro.k_norm_w = k_norm_w;
+  pro.eps = eps;
+  pro.pos = pos;
+  pro.sin_tab = sin_tab;
+  pro.cos_tab = cos_tab;
+  pro.n_ctx = n_ctx;
+  pro.status = status;
+  return decode_common(q_raw, k_cache, v_cache, k_raw, v_new, out, n_head, n_head_kv, head_dim,
+                       n_kv, scale, workspace, workspace_bytes, &pro, stream);
 }

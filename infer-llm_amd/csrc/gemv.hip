@@ -14,7 +14,13 @@
 // sums finish with DPP/swizzle half-wave reductions. Fused variants: a
 // residual add (o_proj, ffn_down), three projections of one input in one
 // launch (q, k, v), and the SwiGLU pair gate/up (each wave owns matching
-// gate and up rows and writes up * silu(gate)).
+// gate and up rows and writes up * silu(gate)). The q/k/v and SwiGLU forms
+// can also fold in the RMSNorm of their input (attn_norm, ffn_norm): every
+// wave computes the row's scale with the lane-strided double sum of
+// ikv::rms_scale_strided (the order ikv_rms_norm_f32 uses for such rows)
+// while its first weight batch is in flight, and multiplies x by scale and
+// the norm weight as it reads it — the same float operations as the
+// standalone norm, so the products see the same inputs bit for bit.
 //
 // Prefill (m > 1) is a dense F32 GEMM and goes to rocBLAS SGEMM.
 #include <rocblas/rocblas.h>
@@ -44,11 +50,20 @@ __device__ __forceinline__ float wave_sum64(float v) {
   return v + __shfl_xor(v, 32, 64);
 }
 
+// x[k] * scale * nw[k] for a float4 of x: the standalone RMSNorm's
+// (x * scale) * w, two roundings.
+__device__ __forceinline__ float4 normed(float4 v, float scale, float4 g) {
+  const float a = v.x * scale, b = v.y * scale, c = v.z * scale, d = v.w * scale;
+  return make_float4(a * g.x, b * g.y, c * g.z, d * g.w);
+}
+
 // Sums of NR rows (row r at rows[r], K columns, K % 1024 == 0) dotted with
-// x; every lane gets the sums.
+// x (RMS-normalised with weight nw when nw is not null); every lane gets the
+// sums.
 template <int NR>
 __device__ __forceinline__ void wave_dots(const float *const (&rows)[NR], const float *x, int K,
-                                          float (&out)[NR]) {
+                                          float (&out)[NR], const float *nw = nullptr,
+                                          float eps = 0.f) {
   const int lane = threadIdx.x & 63;
   float4 cur[NR][kBatch], nxt[NR][kBatch];
   float4 acc[NR];
@@ -58,6 +73,8 @@ __device__ __forceinline__ void wave_dots(const float *const (&rows)[NR], const 
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) cur[r][j] = nt_load4(rows[r] + 4 * lane + 256 * j);
   }
+  const float scale =
+      nw ? ikv::rms_scale_strided(reinterpret_cast<const float4 *>(x), K, eps, lane) : 1.f;
   for (int k0 = 0; k0 < K; k0 += kBatchCols) {
     const bool more = k0 + kBatchCols < K;
     if (more) {
@@ -71,6 +88,11 @@ __device__ __forceinline__ void wave_dots(const float *const (&rows)[NR], const 
 #pragma unroll
     for (int j = 0; j < kBatch; ++j)
       xv[j] = *reinterpret_cast<const float4 *>(x + k0 + 4 * lane + 256 * j);
+    if (nw) {
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j)
+        xv[j] = normed(xv[j], scale, *reinterpret_cast<const float4 *>(nw + k0 + 4 * lane + 256 * j));
+    }
 #pragma unroll
     for (int r = 0; r < NR; ++r)
 #pragma unroll
@@ -123,7 +145,7 @@ __global__ __launch_bounds__(kThreads) void gemv3_kernel(const float *__restrict
                                                          const float *__restrict__ w2,
                                                          const float *__restrict__ x, float *out0,
                                                          float *out1, float *out2, int n0, int n1,
-                                                         int n2, int K) {
+                                                         int n2, int K, const float *nw, float eps) {
   const int wave = blockIdx.x * kWaves + (threadIdx.x >> 6);
   int row0 = wave * RPW;
   const float *w;
@@ -146,7 +168,7 @@ __global__ __launch_bounds__(kThreads) void gemv3_kernel(const float *__restrict
 #pragma unroll
   for (int r = 0; r < RPW; ++r) rows[r] = w + static_cast<size_t>(row0 + r) * K;
   float s[RPW];
-  wave_dots<RPW>(rows, x, K, s);
+  wave_dots<RPW>(rows, x, K, s, nw, eps);
   const int lane = threadIdx.x & 63;
   if (lane < RPW) {
     float v = s[0];
@@ -164,12 +186,12 @@ __global__ __launch_bounds__(kThreads) void gemv_swiglu_kernel(const float *__re
                                                                const float *__restrict__ wu,
                                                                const float *__restrict__ x,
                                                                float *__restrict__ out, int n_out,
-                                                               int K) {
+                                                               int K, const float *nw, float eps) {
   const int n = blockIdx.x * kWaves + (threadIdx.x >> 6);
   if (n >= n_out) return;
   const float *rows[2] = {wg + static_cast<size_t>(n) * K, wu + static_cast<size_t>(n) * K};
   float s[2];
-  wave_dots<2>(rows, x, K, s);
+  wave_dots<2>(rows, x, K, s, nw, eps);
   if ((threadIdx.x & 63) == 0) out[n] = s[1] * silu(s[0]);
 }
 
@@ -267,11 +289,12 @@ extern "C" int ikv_mul_mat_f32(const float *w, const float *x, float *out, int64
 
 extern "C" int ikv_gemv3_f32(const float *w0, const float *w1, const float *w2, const float *x,
                              float *out0, float *out1, float *out2, int64_t n0, int64_t n1,
-                             int64_t n2, int64_t k, void *stream) {
+                             int64_t n2, int64_t k, const float *norm_w, float eps, void *stream) {
   if (!w0 || !w1 || !w2 || !x || !out0 || !out1 || !out2) return -EINVAL;
   if (n0 < 0 || n1 < 0 || n2 < 0 || k <= 0) return -EINVAL;
   if (n0 + n1 + n2 > INT_MAX / 2 || k > INT_MAX / 2) return -EOVERFLOW;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (norm_w && !fast_ok(k, {w0, w1, w2, x, norm_w})) return -ENOTSUP;
   if (!fast_ok(k, {w0, w1, w2, x})) {
     int rc = ikv_mul_mat_f32(w0, x, out0, n0, k, 1, nullptr, stream);
     if (rc == 0) rc = ikv_mul_mat_f32(w1, x, out1, n1, k, 1, nullptr, stream);
@@ -281,19 +304,22 @@ extern "C" int ikv_gemv3_f32(const float *w0, const float *w1, const float *w2, 
   const int64_t total = n0 + n1 + n2;
   if (total == 0) return 0;
   gemv3_kernel<1><<<grid_for(total), kThreads, 0, s>>>(w0, w1, w2, x, out0, out1, out2, int(n0),
-                                                      int(n1), int(n2), int(k));
+                                                      int(n1), int(n2), int(k), norm_w, eps);
   return ikv::launch_status();
 }
 
 extern "C" int ikv_gemv_swiglu_f32(const float *w_gate, const float *w_up, const float *x,
-                                   float *out, int64_t n_out, int64_t k, void *stream) {
+                                   float *out, int64_t n_out, int64_t k, const float *norm_w,
+                                   float eps, void *stream) {
   if (!w_gate || !w_up || !x || !out) return -EINVAL;
   if (n_out < 0 || k <= 0) return -EINVAL;
   if (n_out == 0) return 0;
   if (n_out > INT_MAX / 2 || k > INT_MAX / 2) return -EOVERFLOW;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (norm_w && !fast_ok(k, {w_gate, w_up, x, norm_w})) return -ENOTSUP;
   if (fast_ok(k, {w_gate, w_up, x}))
-    gemv_swiglu_kernel<<<grid_for(n_out), kThreads, 0, s>>>(w_gate, w_up, x, out, int(n_out), int(k));
+    gemv_swiglu_kernel<<<grid_for(n_out), kThreads, 0, s>>>(w_gate, w_up, x, out, int(n_out), int(k),
+                                                            norm_w, eps);
   else
     gemv_generic_kernel<<<grid_for(n_out), kThreads, 0, s>>>(w_gate, x, out, nullptr, int(n_out),
                                                               int(k), 2, w_up);

@@ -75,4 +75,24 @@ __device__ __forceinline__ float4 scale4(float s, const float4 v) {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// RMSNorm scale float(1 / sqrt(sum/dim + eps)) of a row of dim floats
+// (dim % 256 == 0, row 16-byte aligned) for one wavefront: lane l adds in
+// double, in this order, the float squares of elements 256*j + 4*l + c
+// (j ascending, c = 0..3); the 64 lane sums combine in a fixed xor butterfly
+// (32, 16, ..., 1), so every lane of every wave gets the same bits.
+__device__ __forceinline__ float rms_scale_strided(const float4 *row, int dim, float eps, int lane) {
+  double s = 0.0;
+#pragma unroll 4
+  for (int j = 0; j < dim / 256; ++j) {
+    const float4 v = row[64 * j + lane];
+    const float a = v.x * v.x, b = v.y * v.y, c = v.z * v.z, d = v.w * v.w;
+    s += static_cast<double>(a);
+    s += static_cast<double>(b);
+    s += static_cast<double>(c);
+    s += static_cast<double>(d);
+  }
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+  return static_cast<float>(1.0 / sqrt(s / static_cast<double>(dim) + static_cast<double>(eps)));
+}
+
 }  // namespace ikv

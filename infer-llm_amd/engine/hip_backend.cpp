@@ -320,6 +320,8 @@ infer::expected<void, std::error_code> HIPBackend::compute(Graph &graph) {
   _swiglu.clear();
   _residual.clear();
   _qkv.clear();
+  _norm_into_mm.clear();
+  _rope_into_attn.clear();
   _skip.clear();
 
   if (_fusion) {
@@ -442,6 +444,43 @@ void HIPBackend::plan_model_fusions(Graph &graph, std::unordered_map<const Tenso
     _qkv[v[0]] = {v[0], v[1], v[2]};
     _skip[v[1]] = _skip[v[2]] = true;
   }
+  // The single-row RMS_NORM feeding a q/k/v group (attn_norm) or a SwiGLU
+  // pair (ffn_norm), and nothing else, is folded into that launch.
+  auto foldable_norm = [&](const Tensor *x, int consumers) {
+    if (!x || x->op != OperationType::GGML_OP_RMS_NORM || uses[x] != consumers) return false;
+    const Tensor *in = x->src[0], *w = x->src[1];
+    return contiguous_f32(in) && contiguous_f32(w) && in->dims == x->dims && x->dims[1] == 1 &&
+           x->dims[2] == 1 && x->dims[3] == 1 && x->dims[0] % 1024 == 0 &&
+           w->element_count() == static_cast<size_t>(x->dims[0]);
+  };
+  for (const auto &[first, group] : _qkv) {
+    const Tensor *x = first->src[1];
+    if (foldable_norm(x, 3)) {
+      _norm_into_mm[first] = x;
+      _skip[x] = true;
+    }
+  }
+  for (const auto &[mul, pair] : _swiglu) {
+    const Tensor *x = pair.first->src[1];
+    if (foldable_norm(x, 2)) {
+      _norm_into_mm[mul] = x;
+      _skip[x] = true;
+    }
+  }
+  // qk-RMSNorm + RoPE of a one-token step folded into its decode launch.
+  for (const auto &[attn, kv_src] : _append_into_attn) {
+    const Tensor *qr = attn->src[0], *kr = kv_src.first;
+    if (!qr || !kr || qr->op != OperationType::GGML_OP_ROPE || kr->op != OperationType::GGML_OP_ROPE)
+      continue;
+    if (!_norm_into_rope.count(qr) || !_norm_into_rope.count(kr) || uses[qr] != 1 || uses[kr] != 1)
+      continue;
+    if (qr->src[1] != kr->src[1] || qr->src[2] != kr->src[2]) continue;  // same positions, table
+    const Tensor *qn = _norm_into_rope[qr], *kn = _norm_into_rope[kr];
+    if (std::memcmp(&qn->op_params[0], &kn->op_params[0], sizeof(float)) != 0) continue;  // same eps
+    if (!contiguous_f32(qn->src[0]) || !contiguous_f32(kn->src[0])) continue;
+    _rope_into_attn[attn] = {qr, kr};
+    _skip[qr] = _skip[kr] = true;
+  }
 }
 
 infer::expected<void, std::error_code> HIPBackend::dispatch(Tensor *node) {
@@ -541,6 +580,29 @@ infer::expected<void, std::error_code> HIPBackend::dispatch(Tensor *node) {
         }
         const size_t need = ikv_attn_decode_workspace_bytes(int(Hq), int(Hkv), int(D), nkv);
         if (auto r = ensure_workspace(need); !r) return r;
+        if (const auto rf = _rope_into_attn.find(node); rf != _rope_into_attn.end()) {
+          const Tensor *qr = rf->second.first, *kr = rf->second.second;
+          const Tensor *qn = _norm_into_rope[qr], *kn = _norm_into_rope[kr];
+          const Tensor *pos = qr->src[1];
+          if (!pos || !pos->data || pos->dataType != GGML_TYPE_I32 || !qr->src[2])
+            return infer::fail(std::errc::invalid_argument);
+          auto tab = rope_tables(*qr->src[2]);
+          if (!tab) return infer::unexpected(tab.error());
+          float eps;
+          std::memcpy(&eps, &qn->op_params[0], sizeof(eps));
+          ++_stats.fused_rope_decode;
+          return check_ikv(ikv_attn_decode_rope_f32(
+                               static_cast<const float *>(qn->src[0]->data),
+                               static_cast<const float *>(kn->src[0]->data),
+                               static_cast<const float *>(vn), static_cast<float *>(k->data),
+                               static_cast<float *>(v->data), static_cast<float *>(node->data),
+                               int(Hq), int(Hkv), int(D), nkv, p.scale,
+                               static_cast<const float *>(qn->src[1]->data),
+                               static_cast<const float *>(kn->src[1]->data), eps,
+                               static_cast<const int32_t *>(pos->data), (*tab)->sin, (*tab)->cos,
+                               (*tab)->n_ctx, _status, _workspace, _workspace_bytes, s),
+                           "attn_decode_rope");
+        }
         return check_ikv(ikv_attn_decode_f32(static_cast<const float *>(q->data),
                                              static_cast<float *>(k->data), static_cast<float *>(v->data),
                                              static_cast<const float *>(kn), static_cast<const float *>(vn),
@@ -576,14 +638,23 @@ infer::expected<void, std::error_code> HIPBackend::dispatch(Tensor *node) {
       ++_stats.launches;
       if (const auto g = _qkv.find(node); g != _qkv.end()) {
         const Tensor *a = g->second[0], *b = g->second[1], *c = g->second[2];
+        const Tensor *xin = x, *nw = nullptr;
+        float eps = 0.f;
+        if (const auto f = _norm_into_mm.find(node); f != _norm_into_mm.end()) {
+          xin = f->second->src[0];
+          nw = f->second->src[1];
+          std::memcpy(&eps, &f->second->op_params[0], sizeof(eps));
+          ++_stats.fused_norm_mm;
+        }
         ++_stats.fused_qkv;
         return check_ikv(
             ikv_gemv3_f32(static_cast<const float *>(a->src[0]->data),
                           static_cast<const float *>(b->src[0]->data),
                           static_cast<const float *>(c->src[0]->data),
-                          static_cast<const float *>(x->data), static_cast<float *>(a->data),
+                          static_cast<const float *>(xin->data), static_cast<float *>(a->data),
                           static_cast<float *>(b->data), static_cast<float *>(c->data),
-                          a->dims[0], b->dims[0], c->dims[0], w->dims[0], s),
+                          a->dims[0], b->dims[0], c->dims[0], w->dims[0],
+                          nw ? static_cast<const float *>(nw->data) : nullptr, eps, s),
             "gemv3");
       }
       return check_ikv(ikv_mul_mat_f32(static_cast<const float *>(w->data),
@@ -620,12 +691,22 @@ infer::expected<void, std::error_code> HIPBackend::dispatch(Tensor *node) {
       ++_stats.launches;
       if (const auto f = _swiglu.find(node); f != _swiglu.end()) {
         const Tensor *gate = f->second.first, *up = f->second.second;
+        const Tensor *xin = gate->src[1], *nw = nullptr;
+        float eps = 0.f;
+        if (const auto n = _norm_into_mm.find(node); n != _norm_into_mm.end()) {
+          xin = n->second->src[0];
+          nw = n->second->src[1];
+          std::memcpy(&eps, &n->second->op_params[0], sizeof(eps));
+          ++_stats.fused_norm_mm;
+        }
         ++_stats.fused_swiglu;
         return check_ikv(ikv_gemv_swiglu_f32(static_cast<const float *>(gate->src[0]->data),
                                              static_cast<const float *>(up->src[0]->data),
-                                             static_cast<const float *>(gate->src[1]->data),
+                                             static_cast<const float *>(xin->data),
                                              static_cast<float *>(node->data), gate->dims[0],
-                                             gate->src[0]->dims[0], s),
+                                             gate->src[0]->dims[0],
+                                             nw ? static_cast<const float *>(nw->data) : nullptr,
+                                             eps, s),
                          "gemv_swiglu");
       }
       if (!contiguous_f32(a) || !contiguous_f32(b) || a->dims != node->dims || b->dims != node->dims)

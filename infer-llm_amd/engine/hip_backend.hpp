@@ -66,6 +66,8 @@ class HIPBackend : public Backend {
     int fused_swiglu = 0;
     int fused_residual = 0;
     int fused_qkv = 0;
+    int fused_norm_mm = 0;      // RMSNorm folded into q/k/v or SwiGLU
+    int fused_rope_decode = 0;  // qk-norm + RoPE folded into the decode launch
   };
   const Stats &last_stats() const { return _stats; }
 
@@ -97,5 +99,7 @@ class HIPBackend : public Backend {
   std::unordered_map<const Tensor *, std::pair<const Tensor *, const Tensor *>> _swiglu;    // mul -> gate, up
   std::unordered_map<const Tensor *, std::pair<const Tensor *, const Tensor *>> _residual;  // add -> mm, r
   std::unordered_map<const Tensor *, std::array<const Tensor *, 3>> _qkv;  // first mm -> group
+  std::unordered_map<const Tensor *, const Tensor *> _norm_into_mm;  // qkv first mm / swiglu mul -> norm
+  std::unordered_map<const Tensor *, std::pair<const Tensor *, const Tensor *>> _rope_into_attn;  // attn -> q, k rope
   std::unordered_map<const Tensor *, bool> _skip;
 };

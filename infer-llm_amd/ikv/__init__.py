@@ -38,6 +38,12 @@ SIGNATURES = {
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
          _c_int, _c_int, _c_int, _c_int64, _c_float, _c_void_p, _c_size_t, _c_void_p],
     ),
+    "ikv_attn_decode_rope_f32": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int,
+         _c_int64, _c_float, _c_void_p, _c_void_p, _c_float, _c_void_p, _c_void_p, _c_void_p,
+         _c_int64, _c_void_p, _c_void_p, _c_size_t, _c_void_p],
+    ),
     "ikv_attn_prefill_f32": (
         _c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int,
@@ -62,10 +68,11 @@ SIGNATURES = {
     "ikv_gemv3_f32": (
         _c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
-         _c_int64, _c_int64, _c_int64, _c_int64, _c_void_p],
+         _c_int64, _c_int64, _c_int64, _c_int64, _c_void_p, _c_float, _c_void_p],
     ),
     "ikv_gemv_swiglu_f32": (
-        _c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int64, _c_int64, _c_void_p]),
+        _c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int64, _c_int64, _c_void_p, _c_float,
+                 _c_void_p]),
     "ikv_get_rows_f32": (
         _c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_int64, _c_int64, _c_int64, _c_void_p, _c_void_p]),
@@ -221,6 +228,27 @@ def attn_decode(q, k_cache, v_cache, n_kv: int, *, k_new=None, v_new=None, out=N
     return out
 
 
+def attn_decode_rope(q_raw, k_raw, v_new, k_cache, v_cache, n_kv: int, q_norm_w, k_norm_w,
+                     eps: float, pos, sin_tab, cos_tab, *, out=None, scale: float = 0.0,
+                     status=None, workspace=None, stream=None):
+    """Decode with qk-RMSNorm + RoPE folded in: q/k rotated at position pos[0],
+    k (rotated) and v_new appended at row n_kv-1, attention over [0, n_kv)."""
+    torch = _torch()
+    n_head, D = q_raw.shape[-2], q_raw.shape[-1]
+    n_head_kv = k_cache.shape[-2]
+    if out is None:
+        out = torch.empty((n_head, D), dtype=torch.float32, device=q_raw.device)
+    if workspace is None:
+        workspace = decode_workspace(n_head, n_head_kv, D, n_kv, device=q_raw.device)
+    rc = load().ikv_attn_decode_rope_f32(
+        _ptr(q_raw), _ptr(k_raw), _ptr(v_new), _ptr(k_cache), _ptr(v_cache), _ptr(out), n_head,
+        n_head_kv, D, n_kv, scale, _ptr(q_norm_w), _ptr(k_norm_w), eps, _ptr(pos), _ptr(sin_tab),
+        _ptr(cos_tab), sin_tab.shape[0], _ptr(status), _ptr(workspace), workspace.numel() * 4,
+        _stream(stream))
+    _check("ikv_attn_decode_rope_f32", rc)
+    return out
+
+
 def attn_prefill(q, k, v, n_past: int = 0, *, n_kv: Optional[int] = None, out=None,
                  scale: float = 0.0, stream=None):
     """Causal attention for q [n_q, n_head, D] over k, v [>= n_kv, n_head_kv, D]."""
@@ -314,23 +342,25 @@ def mul_mat(w, x, out=None, residual=None, stream=None):
     return out
 
 
-def gemv3(w0, w1, w2, x, stream=None):
+def gemv3(w0, w1, w2, x, norm_w=None, eps: float = 1e-6, stream=None):
+    """[w_i . x'] for i = 0, 1, 2; x' = rms_norm(x, norm_w, eps) when norm_w is given."""
     torch = _torch()
     k = x.numel()
     outs = [torch.empty(w.shape[0], device=x.device) for w in (w0, w1, w2)]
     _check("ikv_gemv3_f32", load().ikv_gemv3_f32(
         _ptr(w0), _ptr(w1), _ptr(w2), _ptr(x), _ptr(outs[0]), _ptr(outs[1]), _ptr(outs[2]),
-        w0.shape[0], w1.shape[0], w2.shape[0], k, _stream(stream)))
+        w0.shape[0], w1.shape[0], w2.shape[0], k, _ptr(norm_w), eps, _stream(stream)))
     return outs
 
 
-def gemv_swiglu(w_gate, w_up, x, out=None, stream=None):
+def gemv_swiglu(w_gate, w_up, x, out=None, norm_w=None, eps: float = 1e-6, stream=None):
     torch = _torch()
     n_out, k = w_gate.shape
     if out is None:
         out = torch.empty(n_out, device=x.device)
     _check("ikv_gemv_swiglu_f32", load().ikv_gemv_swiglu_f32(
-        _ptr(w_gate), _ptr(w_up), _ptr(x), _ptr(out), n_out, k, _stream(stream)))
+        _ptr(w_gate), _ptr(w_up), _ptr(x), _ptr(out), n_out, k, _ptr(norm_w), eps,
+        _stream(stream)))
     return out
 
 

@@ -159,11 +159,14 @@ def test_small_model_greedy_tokens_match_oracle(dev, oracle_pool):
     stats = eng.last_stats()
     ref = oracle.Qwen3Oracle(SMALL, w, 128).generate(prompt, 48)
     assert toks == ref
-    # a decode step took every fusion: per layer qk-norm+RoPE x2, append+decode,
-    # q/k/v, SwiGLU, o_proj+residual and down+residual
+    # a decode step took every fusion: per layer attn_norm + q/k/v, qk-norm +
+    # RoPE + append + decode, o_proj + residual, ffn_norm + SwiGLU, down +
+    # residual: 5 launches per layer
     L = SMALL.n_layer
-    assert stats["fused_norm_rope"] == 2 * L and stats["fused_append_decode"] == L
+    assert stats["fused_rope_decode"] == L and stats["fused_append_decode"] == L
     assert stats["fused_qkv"] == L and stats["fused_swiglu"] == L and stats["fused_residual"] == 2 * L
+    assert stats["fused_norm_mm"] == 2 * L and stats["fused_norm_rope"] == 0
+    assert stats["launches"] == 5 * L + 3  # + embedding, final norm, logits
     assert t.ttft_s > 0 and t.tpot_s > 0
     # unfused graph (every node its own kernel) gives the same tokens
     eng.set_fusion(False)
@@ -194,3 +197,82 @@ def test_qwen3_06b_config0_greedy_tokens_match_oracle(dev, oracle_pool):
     eng.close()
     ref = oracle.Qwen3Oracle(cfg, w, 160).generate(prompt, 128)
     assert toks == ref
+
+
+# ---------------------------------------------------------------------------
+# folded forms equal the separate ops bit for bit
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("k", [1024, 4096])
+def test_norm_folded_into_gemv_equals_separate_norm(dev, k):
+    x = synth.normal(20 + k, (k,)) * 2
+    nw = 1 + 0.2 * synth.normal(21, (k,))
+    ws = [synth.normal(22 + i, (n, k), 0.02) for i, n in enumerate((512, 256, 256))]
+    xd, nwd = dev_t(x, dev), dev_t(nw, dev)
+    normed = ikv.rms_norm(xd[None], nwd, 1e-6)[0]
+    sep = [host(o) for o in ikv.gemv3(*[dev_t(w, dev) for w in ws], normed)]
+    fused = [host(o) for o in ikv.gemv3(*[dev_t(w, dev) for w in ws], xd, norm_w=nwd, eps=1e-6)]
+    for a, b in zip(sep, fused):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    wg, wu = dev_t(ws[1], dev), dev_t(ws[2], dev)
+    sep = host(ikv.gemv_swiglu(wg, wu, normed))
+    fused = host(ikv.gemv_swiglu(wg, wu, xd, norm_w=nwd, eps=1e-6))
+    assert np.array_equal(sep.view(np.uint32), fused.view(np.uint32))
+    # and the model-width norm itself matches the reference's float result on these rows
+    ref = oracle.rms_norm(x[None], nw, 1e-6)[0]
+    assert np.array_equal(host(normed).view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("Hq,Hkv,ctx", [(16, 8, 0), (16, 8, 37), (16, 8, 4096), (32, 8, 1000),
+                                        (8, 8, 300), (64, 8, 129)])
+def test_decode_with_qk_rope_equals_separate_ops(dev, oracle_pool, Hq, Hkv, ctx):
+    import torch
+    D = 128
+    th = oracle.rope_theta_table(1e6, D, 8192)
+    s, c = ikv.rope_sincos_table(th)
+    sd, cd = dev_t(s, dev), dev_t(c, dev)
+    qn_w = 1 + 0.3 * synth.normal(30, (D,))
+    kn_w = 1 + 0.3 * synth.normal(31, (D,))
+    q_raw = synth.normal(32 + ctx, (Hq, D)) * 2
+    k_raw = synth.normal(33 + ctx, (Hkv, D)) * 2
+    v_new = synth.normal(34 + ctx, (Hkv, D))
+    hist_k = synth.normal(35 + ctx, (ctx + 1, Hkv, D))
+    hist_v = synth.normal(36 + ctx, (ctx + 1, Hkv, D))
+    pos = torch.tensor([ctx], dtype=torch.int32, device=dev)
+    # separate: qk-norm+rope, then decode with fused append
+    q_rot = ikv.qk_norm_rope(dev_t(q_raw[None], dev), dev_t(qn_w, dev), pos, 1e-6, sd, cd)[0]
+    k_rot = ikv.qk_norm_rope(dev_t(k_raw[None], dev), dev_t(kn_w, dev), pos, 1e-6, sd, cd)[0]
+    kc1, vc1 = dev_t(hist_k, dev), dev_t(hist_v, dev)
+    out1 = ikv.attn_decode(q_rot, kc1, vc1, ctx + 1, k_new=k_rot, v_new=dev_t(v_new, dev))
+    # folded
+    kc2, vc2 = dev_t(hist_k, dev), dev_t(hist_v, dev)
+    out2 = ikv.attn_decode_rope(dev_t(q_raw, dev), dev_t(k_raw, dev), dev_t(v_new, dev), kc2, vc2,
+                                ctx + 1, dev_t(qn_w, dev), dev_t(kn_w, dev), 1e-6, pos, sd, cd)
+    assert np.array_equal(host(kc1).view(np.uint32), host(kc2).view(np.uint32))
+    assert np.array_equal(host(vc1).view(np.uint32), host(vc2).view(np.uint32))
+    assert np.array_equal(host(out1).view(np.uint32), host(out2).view(np.uint32))
+    # and against the oracle chain
+    qo = oracle.rope_neox(oracle.rms_norm(q_raw[None], qn_w, 1e-6), np.array([ctx], np.int32), th)[0]
+    ko = oracle.rope_neox(oracle.rms_norm(k_raw[None], kn_w, 1e-6), np.array([ctx], np.int32), th)[0]
+    hk, hv = hist_k.copy(), hist_v.copy()
+    want = oracle.decode_append_attn(qo, ko, v_new, hk, hv, ctx)
+    assert np.array_equal(host(kc2).view(np.uint32), hk.view(np.uint32))
+    got = host(out2).astype(np.float64)
+    assert np.all(np.abs(got - want) <= 1e-5 + 1e-4 * np.abs(want))
+
+
+def test_decode_with_qk_rope_bad_position_is_flagged(dev):
+    import torch
+    D = 128
+    th = oracle.rope_theta_table(1e6, D, 64)
+    s, c = ikv.rope_sincos_table(th)
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
+    kc = torch.zeros((11, 8, D), device=dev)
+    vc = torch.zeros((11, 8, D), device=dev)
+    pos = torch.tensor([64], dtype=torch.int32, device=dev)     # outside the 64-row table
+    ones = torch.ones(D, device=dev)
+    ikv.attn_decode_rope(torch.ones((16, D), device=dev), torch.ones((8, D), device=dev),
+                         torch.ones((8, D), device=dev), kc, vc, 11, ones, ones, 1e-6, pos,
+                         dev_t(s, dev), dev_t(c, dev), status=status)
+    assert int(host(status)[0]) == 1
+    assert not host(kc)[10].any()       # the appended key row is zeros, not garbage
