@@ -11,10 +11,6 @@ namespace {
 
 size_t align256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
 
-double seconds(std::chrono::steady_clock::time_point a, std::chrono::steady_clock::time_point b) {
-  return std::chrono::duration<double>(b - a).count();
-}
-
 bool is_norm(const std::string &name) { return name.find("norm") != std::string::npos; }
 
 }  // namespace
@@ -171,9 +167,14 @@ Qwen3Runner::Qwen3Runner(Qwen3Model &model, HIPBackend &backend, size_t capacity
     : _model(model), _backend(backend), _capacity(capacity) {}
 
 Qwen3Runner::~Qwen3Runner() {
+  (void)_backend.synchronize();
   if (_ctx) (void)_ctx->release_kv_access();
   if (_kv && _seq != kInvalidSequenceId) (void)_kv->release_sequence(_seq);
+  for (hipEvent_t &e : _ready)
+    if (e) (void)hipEventDestroy(e);
   if (_token_dev) (void)hipFree(_token_dev);
+  if (_positions_dev) (void)hipFree(_positions_dev);
+  if (_token_host) (void)hipHostFree(_token_host);
 }
 
 infer::expected<void, std::error_code> Qwen3Runner::init() {
@@ -194,73 +195,87 @@ infer::expected<void, std::error_code> Qwen3Runner::init() {
   _ctx = std::make_unique<GraphContext>(nullptr);
   _tokens = _ctx->make_tensor("inp_tokens", GGML_TYPE_I32, {1});
   _pos = _ctx->make_tensor("inp_pos", GGML_TYPE_I32, {1});
-  for (Tensor *t : {_tokens, _pos}) {
-    t->device = DeviceType::CPU;
-    t->tensorRole = TensorRole::TNESOR_ROLE_INPUT;
-  }
+  for (Tensor *t : {_tokens, _pos}) t->tensorRole = TensorRole::TNESOR_ROLE_INPUT;
   _ctx->set_input_tokens(_tokens);
   _ctx->set_input_pos(_pos);
-  if (hipMalloc(&_token_dev, sizeof(int32_t)) != hipSuccess) {
+  auto fail_alloc = [] {
     (void)hipGetLastError();
     return infer::fail(std::errc::not_enough_memory);
-  }
+  };
+  if (hipMalloc(&_token_dev, 2 * sizeof(int32_t)) != hipSuccess) return fail_alloc();
+  if (hipMalloc(&_positions_dev, _capacity * sizeof(int32_t)) != hipSuccess) return fail_alloc();
+  if (hipHostMalloc(&_token_host, 2 * sizeof(int32_t), hipHostMallocDefault) != hipSuccess)
+    return fail_alloc();
+  for (hipEvent_t &e : _ready)
+    if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) return fail_alloc();
+  std::vector<int32_t> iota(_capacity);
+  for (size_t i = 0; i < _capacity; ++i) iota[i] = int32_t(i);
+  if (hipMemcpy(_positions_dev, iota.data(), _capacity * sizeof(int32_t), hipMemcpyHostToDevice) !=
+      hipSuccess)
+    return infer::fail(std::errc::io_error);
   return {};
 }
 
-infer::expected<int32_t, std::error_code> Qwen3Runner::evaluate(const std::vector<int32_t> &input,
-                                                                bool sample,
-                                                                GenerationTiming &timing) {
+infer::expected<void, std::error_code> Qwen3Runner::enqueue_step(const int32_t *host_tokens,
+                                                                 int64_t n, int slot,
+                                                                 GenerationTiming &timing) {
   using Clock = std::chrono::steady_clock;
   const auto t0 = Clock::now();
   auto n_past = _kv->length(_seq);
   if (!n_past) return infer::unexpected(n_past.error());
-  if (auto r = _kv->reserve_append(_seq, input.size()); !r) return infer::unexpected(r.error());
-  _input = input;
-  _positions.resize(input.size());
-  for (size_t i = 0; i < input.size(); ++i) _positions[i] = int32_t(*n_past + i);
-  const int64_t n = int64_t(input.size());
+  if (auto r = _kv->reserve_append(_seq, size_t(n)); !r) return r;
   for (Tensor *t : {_tokens, _pos}) {
     t->dims = {n, 1, 1, 1};
     t->set_contiguous_strides();
   }
-  _tokens->data = _input.data();
-  _pos->data = _positions.data();
-
-  auto graph = _model.build_graph(*_ctx);
-  if (!graph) {
-    (void)_ctx->release_kv_access();
-    (void)_kv->abort_append(_seq);
-    return infer::unexpected(graph.error());
+  if (host_tokens) {  // the prompt: a host input the scheduler stages
+    _input.assign(host_tokens, host_tokens + n);
+    _tokens->data = _input.data();
+    _tokens->device = DeviceType::CPU;
+    _tokens->backend = nullptr;
+  } else {  // the previous step's greedy token, already on the device
+    _tokens->data = _token_dev + (slot ^ 1);
+    _tokens->device = DeviceType::HIP;
+    _tokens->backend = &_backend;
   }
-  const auto t1 = Clock::now();
-  auto fail = [&](std::error_code e) -> infer::expected<int32_t, std::error_code> {
+  _pos->data = _positions_dev + *n_past;
+  _pos->device = DeviceType::HIP;
+  _pos->backend = &_backend;
+
+  auto abort = [&](std::error_code e) -> infer::expected<void, std::error_code> {
     (void)_backend.synchronize();
     (void)_ctx->release_kv_access();
     (void)_kv->abort_append(_seq);
     return infer::unexpected(e);
   };
-  if (auto r = _sched->execute(*graph); !r) return fail(r.error());
+  auto graph = _model.build_graph(*_ctx);
+  if (!graph) return abort(graph.error());
+  const auto t1 = Clock::now();
+  if (auto r = _sched->execute(*graph); !r) return abort(r.error());
+  const Tensor *logits = graph->outputs().front();
+  const int64_t vocab = logits->dims[0];
+  const float *row = static_cast<const float *>(logits->data) + (n - 1) * vocab;
+  hipStream_t s = _backend.stream();
+  if (ikv_argmax_f32(row, vocab, _token_dev + slot, s) != 0 ||
+      hipMemcpyAsync(_token_host + slot, _token_dev + slot, sizeof(int32_t), hipMemcpyDeviceToHost,
+                     s) != hipSuccess ||
+      hipEventRecord(_ready[slot], s) != hipSuccess)
+    return abort(std::make_error_code(std::errc::io_error));
+  // The kernels of this step hold no host-side state: hand the layer
+  // accesses back and commit the appended range now.
+  if (auto r = _ctx->release_kv_access(); !r) return r;
+  if (auto r = _kv->commit_append(_seq); !r) return r;
   const auto t2 = Clock::now();
-  int32_t token = -1;
-  if (sample) {
-    const Tensor *logits = graph->outputs().front();
-    const int64_t vocab = logits->dims[0];
-    const float *row = static_cast<const float *>(logits->data) + (n - 1) * vocab;
-    if (int rc = ikv_argmax_f32(row, vocab, _token_dev, _backend.stream()); rc != 0)
-      return fail(std::make_error_code(std::errc::io_error));
-    if (hipMemcpyAsync(&token, _token_dev, sizeof(int32_t), hipMemcpyDeviceToHost,
-                       _backend.stream()) != hipSuccess)
-      return fail(std::make_error_code(std::errc::io_error));
-  }
-  if (auto r = _backend.synchronize(); !r) return fail(r.error());
-  const auto t3 = Clock::now();
-  if (sample && token < 0) return fail(std::make_error_code(std::errc::invalid_argument));
-  if (auto r = _ctx->release_kv_access(); !r) return infer::unexpected(r.error());
-  if (auto r = _kv->commit_append(_seq); !r) return infer::unexpected(r.error());
-  timing.build_s += seconds(t0, t1);
-  timing.execute_s += seconds(t1, t2);
-  timing.sample_s += seconds(t2, t3);
-  return token;
+  timing.build_s += std::chrono::duration<double>(t1 - t0).count();
+  timing.execute_s += std::chrono::duration<double>(t2 - t1).count();
+  return {};
+}
+
+infer::expected<int32_t, std::error_code> Qwen3Runner::collect(int slot) {
+  if (hipEventSynchronize(_ready[slot]) != hipSuccess) return infer::fail(std::errc::io_error);
+  const int32_t tok = _token_host[slot];
+  if (tok < 0) return infer::fail(std::errc::invalid_argument);  // NaN / +inf logits
+  return tok;
 }
 
 infer::expected<void, std::error_code> Qwen3Runner::generate(const std::vector<int32_t> &prompt,
@@ -277,28 +292,38 @@ infer::expected<void, std::error_code> Qwen3Runner::generate(const std::vector<i
   if (auto r = _ctx->set_kv_cache(_kv.get(), _seq); !r) return r;
   timing = GenerationTiming{};
   tokens_out.clear();
+  auto finish = [&](infer::expected<void, std::error_code> r) {
+    const auto sync = _backend.synchronize();
+    (void)_ctx->release_kv_access();
+    (void)_ctx->set_kv_cache(nullptr, kInvalidSequenceId);
+    (void)_kv->release_sequence(_seq);
+    _seq = kInvalidSequenceId;
+    if (r && !sync) return sync;
+    return r;
+  };
   const auto start = Clock::now();
   Clock::time_point first{}, last{};
-  std::vector<int32_t> ids = prompt;
-  for (size_t i = 0; i < n_gen; ++i) {
-    auto tok = evaluate(ids, true, timing);
-    if (!tok) {
-      (void)_ctx->set_kv_cache(nullptr, kInvalidSequenceId);
-      (void)_kv->release_sequence(_seq);
-      _seq = kInvalidSequenceId;
-      return infer::unexpected(tok.error());
-    }
+  auto take = [&](int slot, size_t i) -> infer::expected<void, std::error_code> {
+    const auto t0 = Clock::now();
+    auto tok = collect(slot);
+    if (!tok) return infer::unexpected(tok.error());
     const auto ready = Clock::now();
+    timing.sample_s += std::chrono::duration<double>(ready - t0).count();
     if (i == 0) first = ready;
     last = ready;
     tokens_out.push_back(*tok);
-    ids.assign(1, *tok);
+    return {};
+  };
+  // step i writes token slot i % 2 and reads slot (i - 1) % 2
+  if (auto r = enqueue_step(prompt.data(), int64_t(prompt.size()), 0, timing); !r) return finish(r);
+  for (size_t i = 1; i < n_gen; ++i) {
+    if (auto r = enqueue_step(nullptr, 1, int(i & 1), timing); !r) return finish(r);
+    if (auto r = take(int((i - 1) & 1), i - 1); !r) return finish(r);
   }
-  timing.wall_s = seconds(start, Clock::now());
-  timing.ttft_s = seconds(start, first);
-  timing.tpot_s = n_gen > 1 ? seconds(first, last) / double(n_gen - 1) : 0.0;
-  (void)_ctx->set_kv_cache(nullptr, kInvalidSequenceId);
-  if (auto r = _kv->release_sequence(_seq); !r) return r;
-  _seq = kInvalidSequenceId;
-  return {};
+  if (auto r = take(int((n_gen - 1) & 1), n_gen - 1); !r) return finish(r);
+  timing.wall_s = std::chrono::duration<double>(Clock::now() - start).count();
+  timing.ttft_s = std::chrono::duration<double>(first - start).count();
+  timing.tpot_s =
+      n_gen > 1 ? std::chrono::duration<double>(last - first).count() / double(n_gen - 1) : 0.0;
+  return finish({});
 }

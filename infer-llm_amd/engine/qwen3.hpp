@@ -12,8 +12,13 @@
 //
 // Qwen3Runner restates the benchmark Runner (benchmarks/cpu/bench.cpp:
 // 130-219): per step reserve -> build graph -> execute -> sample -> commit,
-// with greedy sampling on the device (ikv_argmax_f32) and the reference's
-// TTFT / TPOT definitions (benchmarks/cpu/bench.cpp:239-281).
+// with the reference's TTFT / TPOT definitions (benchmarks/cpu/bench.cpp:
+// 239-281). Sampling is greedy on the device (ikv_argmax_f32) into a device
+// token slot that the next step's embedding reads directly, and positions
+// come from a resident device table, so no step waits for the previous one
+// on the host: the host builds and enqueues step i+1 while the GPU runs step
+// i, then reads back token i (pinned memory, one event per slot). A token is
+// "ready" when the host has it, as in the reference's loop.
 #pragma once
 
 #include <chrono>
@@ -107,8 +112,11 @@ class Qwen3Runner {
                                                   GenerationTiming &timing);
 
  private:
-  infer::expected<int32_t, std::error_code> evaluate(const std::vector<int32_t> &input, bool sample,
-                                                     GenerationTiming &timing);
+  // Enqueues one step; its greedy token lands in token slot `slot` (device)
+  // and, once event `slot` has fired, in _token_host[slot].
+  infer::expected<void, std::error_code> enqueue_step(const int32_t *host_tokens, int64_t n,
+                                                      int slot, GenerationTiming &timing);
+  infer::expected<int32_t, std::error_code> collect(int slot);
 
   Qwen3Model &_model;
   HIPBackend &_backend;
@@ -118,6 +126,9 @@ class Qwen3Runner {
   std::unique_ptr<GraphContext> _ctx;
   SequenceId _seq = kInvalidSequenceId;
   Tensor *_tokens = nullptr, *_pos = nullptr;
-  std::vector<int32_t> _input, _positions;
-  int32_t *_token_dev = nullptr;
+  std::vector<int32_t> _input;
+  int32_t *_token_dev = nullptr;    // [2] sampled-token slots
+  int32_t *_token_host = nullptr;   // [2] pinned read-back slots
+  int32_t *_positions_dev = nullptr;  // [capacity]: 0, 1, 2, ...
+  hipEvent_t _ready[2] = {nullptr, nullptr};
 };
