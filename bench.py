@@ -15,6 +15,15 @@ Algorithmic bytes per launch (Qwen3-0.6B):  8192*L + 32768
 value = total algorithmic bytes / timed wall time (GB/s); roofline.achieved =
 the same bytes / mean launch duration; peak = 8 TB/s.
 
+Model level (extra.model): the whole Qwen3 graph on the HIP backend with
+random-init weights (N(0, 0.02^2), norms 1.0) and uniform synthetic prompt
+ids, greedy, no EOS stop — BASELINE configs 0 (Qwen3-0.6B, P=32, 128 tokens),
+3 (Qwen3-0.6B, P=2048, 512 tokens) and 4 (Qwen3-8B, P=4096, 256 tokens) —
+reporting TTFT and TPOT as benchmarks/cpu/bench.cpp:239-281 defines them and
+the token checksum of that harness (c = c*131 + token). The CPU leg runs the
+oracle (restated reference CPU backend) on config 0's weights and prompt for a
+few tokens: its TPOT, and whether its tokens equal the GPU's.
+
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
 Prints ONE JSON line on stdout; progress goes to stderr.
 """
@@ -258,6 +267,85 @@ def traffic_summary(fetch_dir, write_dir, cal_fetch_dir, cal_write_dir, ctx):
     }
 
 
+MODEL_CONFIGS = {  # (architecture, prompt, generated tokens)
+    0: ("QWEN3_0_6B", 32, 128),
+    3: ("QWEN3_0_6B", 2048, 512),
+    4: ("QWEN3_8B", 4096, 256),
+}
+
+
+def token_checksum(tokens):
+    c = 0
+    for t in tokens:
+        c = (c * 131 + (t & 0xFFFFFFFF)) & 0xFFFFFFFFFFFFFFFF
+    return c
+
+
+def model_bench(configs, cpu_tokens):
+    """TTFT / TPOT of the whole model on the GPU per config, and the oracle's
+    TPOT on config 0 (cpu_tokens greedy tokens) with a token-equality check."""
+    from ikv import qwen3, synth
+
+    res = {}
+    gpu_tokens0 = None
+    for c in configs:
+        arch, P, N = MODEL_CONFIGS[c]
+        cfg = getattr(qwen3, arch)
+        t0 = time.perf_counter()
+        eng = qwen3.Qwen3Engine(cfg, P + N)
+        eng.init_synthetic(synth.config_seed(c, 1), threads=16)
+        init_s = time.perf_counter() - t0
+        prompt = synth.uniform_ints(synth.config_seed(c, 0), P, cfg.n_vocab)
+        eng.generate(prompt[:8], 4)  # warm-up: arena, rocBLAS handle, sin/cos tables
+        toks, t = eng.generate(prompt, N)
+        st = eng.last_stats()
+        eng.close()
+        if c == 0:
+            gpu_tokens0 = toks
+        res[f"config{c}"] = {
+            "model": arch.lower().replace("_", "-").replace("-0-6b", "-0.6b"),
+            "prompt": P, "generated": N, "ttft_ms": round(t.ttft_s * 1e3, 3),
+            "tpot_ms": round(t.tpot_s * 1e3, 4), "decode_tok_s": round(1 / t.tpot_s, 1),
+            "host_build_ms_per_step": round(t.build_s / N * 1e3, 4),
+            "host_enqueue_ms_per_step": round(t.execute_s / N * 1e3, 4),
+            "launches_per_decode_step": st["launches"], "token_checksum": str(token_checksum(toks)),
+            "weights_gib": round(sum(int(__import__("numpy").prod(sh))
+                                     for _, sh in qwen3.tensor_layout(cfg)) * 4 / 2**30, 2),
+            "init_s": round(init_s, 1),
+        }
+        log(f"[bench] model config {c} ({arch}, P={P}, N={N}): TTFT {t.ttft_s * 1e3:.2f} ms, "
+            f"TPOT {t.tpot_s * 1e3:.3f} ms")
+    if cpu_tokens and 0 in configs:
+        import oracle
+
+        arch, P, _ = MODEL_CONFIGS[0]
+        cfg = getattr(qwen3, arch)
+        workers = min(oracle.default_workers(), 15)
+        threads = oracle.set_workers(workers)
+        w = qwen3.synthetic_weights(cfg, synth.config_seed(0, 1), threads=16)
+        orc = oracle.Qwen3Oracle(cfg, w, P + cpu_tokens)
+        prompt = synth.uniform_ints(synth.config_seed(0, 0), P, cfg.n_vocab)
+        ids, n_past, times, toks = list(prompt), 0, [], []
+        start = time.perf_counter()
+        for _ in range(cpu_tokens):
+            logits = orc.step(ids, n_past)
+            tok = oracle.sample_greedy(logits[-1])
+            times.append(time.perf_counter())
+            toks.append(tok)
+            n_past += len(ids)
+            ids = [tok]
+        res["cpu_config0"] = {
+            "kind": "port", "threads": threads, "tokens": cpu_tokens,
+            "ttft_ms": round((times[0] - start) * 1e3, 1),
+            "tpot_ms": round((times[-1] - times[0]) / (cpu_tokens - 1) * 1e3, 2),
+            "tokens_equal_gpu_prefix": gpu_tokens0 is not None and toks == gpu_tokens0[:cpu_tokens],
+        }
+        log(f"[bench] cpu config 0: TPOT {res['cpu_config0']['tpot_ms']} ms on {threads} threads, "
+            f"tokens equal GPU: {res['cpu_config0']['tokens_equal_gpu_prefix']}")
+        del w, orc
+    return res
+
+
 def cpu_baseline(ctx, seconds):
     """The oracle (restated reference CPU backend) on this host: the same
     decode step (append + attention) of one layer, rotated over 8 layers."""
@@ -307,6 +395,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the ctx sweep and prefill")
     ap.add_argument("--eager", action="store_true", help="launch without HIP-graph capture")
+    ap.add_argument("--model-configs", default="0,3,4",
+                    help="BASELINE configs run at model level ('' for none)")
+    ap.add_argument("--cpu-model-tokens", type=int, default=6,
+                    help="greedy tokens the oracle generates on config 0 (0: skip)")
     ap.add_argument("--traffic-from", nargs=4, metavar=("FETCH", "WRITE", "CAL_FETCH", "CAL_WRITE"),
                     help="summarise four rocprofv3 --pmc output folders into the traffic file "
                          "(no GPU needed)")
@@ -362,7 +454,7 @@ def main():
             traffic = t.get("hbm_bytes_per_launch")
 
     extra = {"eager_gbs": None, "ctx_sweep_gbs": {}, "mall_hot_gbs": None, "prefill": {},
-             "hbm_probes": None}
+             "hbm_probes": None, "model": None}
     if not args.no_extra:
         rig.graph = None
         es = rig.time(max(args.steps // 2, 5), 2)
@@ -392,6 +484,11 @@ def main():
             extra["prefill"][str(p)] = {"us": round(t * 1e6, 2), "tflops": round(tf, 2),
                                         "mfma_frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)}
             log(f"[bench] prefill P={p}: {t * 1e6:.1f} us, {tf:.2f} TFLOP/s")
+
+    configs = [int(c) for c in args.model_configs.split(",") if c.strip()]
+    if configs and not args.no_extra:
+        torch.cuda.empty_cache()
+        extra["model"] = model_bench(configs, 0 if args.no_cpu else args.cpu_model_tokens)
 
     cpu = None
     if not args.no_cpu:
