@@ -95,12 +95,19 @@ struct Prologue {
   int *status = nullptr;
 };
 
+#ifndef IKV_DECODE_MIN_SPLIT_TOKENS
+#define IKV_DECODE_MIN_SPLIT_TOKENS 64
+#endif
+
 Plan plan_for(int n_head, int n_head_kv, int64_t n_kv) {
-  // Whole tiles per split; at most `target` splits per KV head, and at most
-  // kMergeCap / G so that the merge's weights fit in LDS.
+  // Whole tiles per split; at most `target` splits per KV head, at most
+  // kMergeCap / G so that the merge's weights fit in LDS, and at least
+  // IKV_DECODE_MIN_SPLIT_TOKENS tokens per split.
   const int G = n_head / n_head_kv;
   int64_t target = (IKV_DECODE_TARGET_WGS + n_head_kv - 1) / n_head_kv;
   if (target > kMergeCap / G) target = kMergeCap / G;
+  const int64_t by_min = (n_kv + IKV_DECODE_MIN_SPLIT_TOKENS - 1) / IKV_DECODE_MIN_SPLIT_TOKENS;
+  if (target > by_min) target = by_min;
   if (target < 1) target = 1;
   const int64_t n_tiles = (n_kv + TILE - 1) / TILE;
   const int64_t tiles_per_split = (n_tiles + target - 1) / target;
@@ -161,31 +168,31 @@ __device__ __forceinline__ float4 load4_agent(__amdgpu_buffer_rsrc_t r, unsigned
   return make_float4(v.x, v.y, v.z, v.w);
 }
 
-template <int G>
-__device__ __forceinline__ void load_rows(float4 (&kr)[R], float4 (&vr)[R], int base, int t_end,
+// Loads the K and V rows of tile `base` for this lane: row r of the lane is
+// token base + r*2*NWAVE + 2*wave + half. Rows past the split (t > t_last)
+// are clamped to t_last and scored -inf by the caller, so every lane issues
+// the same unconditional loads (no branch between a load and its use, which
+// keeps the next tile's loads in flight while this one is scored). The new
+// token's row comes from k_new / v_new.
+__device__ __forceinline__ void load_tile(float4 (&kr)[R], float4 (&vr)[R], int base, int t_last,
                                           int wave, int half, int new_row, const float *kc,
                                           const float *vc, const float *k_new, const float *v_new,
                                           size_t tok_stride, size_t head_off) {
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int t = base + r * (NWAVE * 2) + wave * 2 + half;
-    if (t < t_end) {
-      const bool fresh = (t == new_row);
-      const float *kp = fresh ? k_new + head_off : kc + static_cast<size_t>(t) * tok_stride + head_off;
-      const float *vp = fresh ? v_new + head_off : vc + static_cast<size_t>(t) * tok_stride + head_off;
+    const int t = min(base + r * (NWAVE * 2) + wave * 2 + half, t_last);
+    const bool fresh = (t == new_row);
+    const float *kp = fresh ? k_new + head_off : kc + static_cast<size_t>(t) * tok_stride + head_off;
+    const float *vp = fresh ? v_new + head_off : vc + static_cast<size_t>(t) * tok_stride + head_off;
 #if IKV_DECODE_NT
-      const f4v a = __builtin_nontemporal_load(reinterpret_cast<const f4v *>(kp));
-      const f4v b = __builtin_nontemporal_load(reinterpret_cast<const f4v *>(vp));
-      kr[r] = make_float4(a.x, a.y, a.z, a.w);
-      vr[r] = make_float4(b.x, b.y, b.z, b.w);
+    const f4v ka = __builtin_nontemporal_load(reinterpret_cast<const f4v *>(kp));
+    const f4v va = __builtin_nontemporal_load(reinterpret_cast<const f4v *>(vp));
+    kr[r] = make_float4(ka.x, ka.y, ka.z, ka.w);
+    vr[r] = make_float4(va.x, va.y, va.z, va.w);
 #else
-      kr[r] = *reinterpret_cast<const float4 *>(kp);
-      vr[r] = *reinterpret_cast<const float4 *>(vp);
+    kr[r] = *reinterpret_cast<const float4 *>(kp);
+    vr[r] = *reinterpret_cast<const float4 *>(vp);
 #endif
-    } else {
-      kr[r] = make_float4(0.f, 0.f, 0.f, 0.f);
-      vr[r] = make_float4(0.f, 0.f, 0.f, 0.f);
-    }
   }
 }
 
@@ -396,9 +403,11 @@ __global__ __launch_bounds__(WG, G <= 4 ? 4 : 2) void decode_kernel(
   const size_t tok_stride = static_cast<size_t>(n_head_kv) * D;
   const size_t head_off = static_cast<size_t>(g) * D + 4 * sub;
 
-  float4 kr[R], vr[R];
-  load_rows<G>(kr, vr, t_begin, t_end, wave, half, new_row, kc, vc, k_new, v_new, tok_stride,
-               head_off);
+  // Two register buffers of K/V rows: tile t+1 loads into one while tile t
+  // is scored from the other.
+  float4 ka[R], va[R], kb[R], vb[R];
+  load_tile(ka, va, t_begin, t_end - 1, wave, half, new_row, kc, vc, k_new, v_new, tok_stride,
+            head_off);
 
   float4 qv[G];
   float4 knew_rot = make_float4(0.f, 0.f, 0.f, 0.f);  // this lane's piece of rope(norm(k_new))
@@ -424,23 +433,18 @@ __global__ __launch_bounds__(WG, G <= 4 ? 4 : 2) void decode_kernel(
     acc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
 
-  for (int base = t_begin; base < t_end; base += TILE) {
-    float4 kn[R], vn[R];
-    const bool more = base + TILE < t_end;
-    if (more)
-      load_rows<G>(kn, vn, base + TILE, t_end, wave, half, new_row, kc, vc, k_new, v_new,
-                   tok_stride, head_off);
-
-    if (new_row >= base && new_row < base + TILE) {
+  // Scores and accumulates one tile. Branch-free: masked rows are -inf
+  // scores, and with the folded RoPE the new token's key is swapped for the
+  // rotated one by a select.
+  auto process = [&](float4 (&kr)[R], const float4 (&vr)[R], int base) {
+    if constexpr (PRO) {
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const int t = base + r * (NWAVE * 2) + wave * 2 + half;
-        if (t == new_row) {
-          if constexpr (PRO) kr[r] = knew_rot;  // the appended key is the rotated one
-          const size_t off = static_cast<size_t>(new_row) * tok_stride + head_off;
-          *reinterpret_cast<float4 *>(kc + off) = kr[r];
-          *reinterpret_cast<float4 *>(vc + off) = vr[r];
-        }
+        const bool fresh = base + r * (NWAVE * 2) + wave * 2 + half == new_row;
+        kr[r].x = fresh ? knew_rot.x : kr[r].x;
+        kr[r].y = fresh ? knew_rot.y : kr[r].y;
+        kr[r].z = fresh ? knew_rot.z : kr[r].z;
+        kr[r].w = fresh ? knew_rot.w : kr[r].w;
       }
     }
 #pragma unroll
@@ -455,26 +459,54 @@ __global__ __launch_bounds__(WG, G <= 4 ? 4 : 2) void decode_kernel(
       float mx = m[h];
 #pragma unroll
       for (int r = 0; r < R; ++r) mx = fmaxf(mx, sc[r]);
-      if (mx != -INFINITY) {
-        const float alpha = ikv::fast_exp2(m[h] - mx);
-        l[h] *= alpha;
-        acc[h] = ikv::scale4(alpha, acc[h]);
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-          const float p = ikv::fast_exp2(sc[r] - mx);
-          l[h] += p;
-          acc[h] = ikv::fma4(p, vr[r], acc[h]);
-        }
-        m[h] = mx;
-      }
-    }
-    if (more) {
+      // No branch on mx: with every score so far masked (mx = -inf) the
+      // reference point is 0, so alpha and every p are exactly 0.
+      const float ref = (mx == -INFINITY) ? 0.f : mx;
+      const float alpha = ikv::fast_exp2(m[h] - ref);
+      l[h] *= alpha;
+      acc[h] = ikv::scale4(alpha, acc[h]);
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        kr[r] = kn[r];
-        vr[r] = vn[r];
+        const float p = ikv::fast_exp2(sc[r] - ref);
+        l[h] += p;
+        acc[h] = ikv::fma4(p, vr[r], acc[h]);
       }
+      m[h] = mx;
     }
+  };
+  // Ping-pong over the split's tiles. The tail cases get their own calls so
+  // that on every path the next tile's loads are issued unconditionally
+  // before the current tile is scored: the compiler's wait then covers only
+  // the current tile's loads.
+  for (int base = t_begin;; base += 2 * TILE) {
+    if (base + TILE >= t_end) {
+      process(ka, va, base);
+      break;
+    }
+    load_tile(kb, vb, base + TILE, t_end - 1, wave, half, new_row, kc, vc, k_new, v_new,
+              tok_stride, head_off);
+    process(ka, va, base);
+    if (base + 2 * TILE >= t_end) {
+      process(kb, vb, base + TILE);
+      break;
+    }
+    load_tile(ka, va, base + 2 * TILE, t_end - 1, wave, half, new_row, kc, vc, k_new, v_new,
+              tok_stride, head_off);
+    process(kb, vb, base + TILE);
+  }
+
+  // The append: the split holding the new token writes its K (rotated when
+  // RoPE is folded in) and V rows into the caches, 16 bytes per lane of the
+  // first half-wave.
+  if (new_row >= t_begin && new_row < t_end && wave == 0 && half == 0) {
+    const size_t off = static_cast<size_t>(new_row) * tok_stride + head_off;
+    float4 kw;
+    if constexpr (PRO)
+      kw = knew_rot;
+    else
+      kw = *reinterpret_cast<const float4 *>(k_new + head_off);
+    *reinterpret_cast<float4 *>(kc + off) = kw;
+    *reinterpret_cast<float4 *>(vc + off) = *reinterpret_cast<const float4 *>(v_new + head_off);
   }
 
   // Merge the two half-waves (they saw different tokens).

@@ -341,7 +341,11 @@ static void gpu_tests() {
     auto sy = hip->synchronize();
     CHECK(ex && sy, ("execute " + tag).c_str());
     const auto &stt = hip->last_stats();
-    CHECK(stt.fused_norm_rope == 2 * L && stt.fused_append_decode == (step == 0 ? 0 : L),
+    // prefill: qk-norm + RoPE fused per q and k; decode: qk-norm + RoPE and
+    // the append folded into the decode launch
+    CHECK(step == 0 ? stt.fused_norm_rope == 2 * L && stt.fused_append_decode == 0
+                    : stt.fused_norm_rope == 0 && stt.fused_append_decode == L &&
+                          stt.fused_rope_decode == L,
           ("fusions " + tag).c_str());
 
     for (int l = 0; l < L; ++l) {
