@@ -399,6 +399,8 @@ def main():
                     help="BASELINE configs run at model level ('' for none)")
     ap.add_argument("--cpu-model-tokens", type=int, default=6,
                     help="greedy tokens the oracle generates on config 0 (0: skip)")
+    ap.add_argument("--model-only", action="store_true",
+                    help="only the model-level runs (--model-configs); prints their JSON")
     ap.add_argument("--traffic-from", nargs=4, metavar=("FETCH", "WRITE", "CAL_FETCH", "CAL_WRITE"),
                     help="summarise four rocprofv3 --pmc output folders into the traffic file "
                          "(no GPU needed)")
@@ -433,6 +435,11 @@ def main():
                           "bytes_written": n, "dispatches": 3}), flush=True)
         return
     log(f"[bench] {ikv.version()} on {torch.cuda.get_device_name(0)}")
+    if args.model_only:
+        configs = [int(c) for c in args.model_configs.split(",") if c.strip()]
+        print(json.dumps({"model": model_bench(configs, 0 if args.no_cpu else args.cpu_model_tokens)}),
+              flush=True)
+        return
 
     rig = DecodeRig(torch, ikv, args.ctx)
     if not args.eager:
