@@ -62,8 +62,9 @@ def prefill_flops(p, n_head=N_HEAD, d=D):
 class DecodeRig:
     """28 layers of KV cache at one context length, launched through the C-ABI."""
 
-    def __init__(self, torch, ikv, ctx, n_layer=N_LAYER, seed=0x1F0000 + 1000 + 2):
+    def __init__(self, torch, ikv, ctx, n_layer=N_LAYER, seed=0x1F0000 + 1000 + 2, n_head=N_HEAD):
         self.torch, self.ikv, self.ctx, self.n_layer = torch, ikv, ctx, n_layer
+        self.n_head = n_head
         dev = torch.device("cuda:0")
         g = torch.Generator(device=dev)
         g.manual_seed(seed)
@@ -75,11 +76,11 @@ class DecodeRig:
             vc.normal_(generator=g)
             self.layers.append(dict(
                 kc=kc, vc=vc,
-                q=torch.randn((N_HEAD, D), generator=g, device=dev),
+                q=torch.randn((n_head, D), generator=g, device=dev),
                 kn=torch.randn((N_HEAD_KV, D), generator=g, device=dev),
                 vn=torch.randn((N_HEAD_KV, D), generator=g, device=dev),
-                out=torch.empty((N_HEAD, D), device=dev)))
-        self.ws = ikv.decode_workspace(N_HEAD, N_HEAD_KV, D, ctx + 1, device=dev)
+                out=torch.empty((n_head, D), device=dev)))
+        self.ws = ikv.decode_workspace(n_head, N_HEAD_KV, D, ctx + 1, device=dev)
         self.ws_bytes = self.ws.numel() * 4
         self.lib = ikv.load()
         self.graph = None
@@ -90,7 +91,7 @@ class DecodeRig:
         n_kv = self.ctx + 1
         for L in self.layers:
             rc = f(L["q"].data_ptr(), L["kc"].data_ptr(), L["vc"].data_ptr(), L["kn"].data_ptr(),
-                   L["vn"].data_ptr(), L["out"].data_ptr(), N_HEAD, N_HEAD_KV, D, n_kv, 0.0,
+                   L["vn"].data_ptr(), L["out"].data_ptr(), self.n_head, N_HEAD_KV, D, n_kv, 0.0,
                    self.ws.data_ptr(), self.ws_bytes, s)
             if rc != 0:
                 raise RuntimeError(f"ikv_attn_decode_f32 returned {rc}")
@@ -460,8 +461,8 @@ def main():
         if t.get("ctx") == args.ctx:
             traffic = t.get("hbm_bytes_per_launch")
 
-    extra = {"eager_gbs": None, "ctx_sweep_gbs": {}, "mall_hot_gbs": None, "prefill": {},
-             "hbm_probes": None, "model": None}
+    extra = {"eager_gbs": None, "ctx_sweep_gbs": {}, "short_ctx_us": {}, "g4_ctx4096": None,
+             "mall_hot_gbs": None, "prefill": {}, "hbm_probes": None, "model": None}
     if not args.no_extra:
         rig.graph = None
         es = rig.time(max(args.steps // 2, 5), 2)
@@ -477,6 +478,23 @@ def main():
             log(f"[bench] sweep ctx {ctx}: {extra['ctx_sweep_gbs'][str(ctx)]} GB/s")
             del r
             torch.cuda.empty_cache()
+        for ctx in (32, 96, 160, 512):  # the contexts of model config 0's decode steps
+            r = DecodeRig(torch, ikv, ctx)
+            r.capture()
+            s = r.time(50, 3)
+            extra["short_ctx_us"][str(ctx)] = round(s / 50 / N_LAYER * 1e6, 2)
+            del r
+        log(f"[bench] short contexts, us per layer: {extra['short_ctx_us']}")
+        # Qwen3-8B layer shape (32 query heads over 8 KV heads, G = 4), 36 layers.
+        r = DecodeRig(torch, ikv, 4096, n_layer=36, n_head=32)
+        r.capture()
+        s = r.time(20, 3)
+        b = decode_bytes(4096, n_head=32)
+        extra["g4_ctx4096"] = {"us": round(s / 20 / 36 * 1e6, 2),
+                               "gbs": round(b * 20 * 36 / s / 1e9, 1)}
+        log(f"[bench] G=4 ctx 4096: {extra['g4_ctx4096']}")
+        del r
+        torch.cuda.empty_cache()
         hot = DecodeRig(torch, ikv, args.ctx, n_layer=1)
         hot.layers = hot.layers * N_LAYER  # the same cache 28 times: MALL-resident
         hot.capture()

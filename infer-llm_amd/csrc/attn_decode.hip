@@ -80,6 +80,16 @@ constexpr int kMergeChunk = 16;
 // Arrival counters: one int per KV head, kCounterStride ints apart.
 constexpr int kCounterStride = 64;
 
+// MI355X compute units.
+constexpr int kCUs = 256;
+
+// Waves per SIMD that decode_kernel<G> is built for (the second launch
+// bound): 4 caps it at 128 VGPRs, which fits G <= 2; wider query groups need
+// more registers (G = 4: ~172), so they get 2 (256 VGPRs) instead of spilling.
+constexpr int waves_per_simd(int G) { return G <= 2 ? 4 : 2; }
+// 8-wave workgroups resident per CU (4 SIMDs) at that bound.
+constexpr int resident_wgs(int G) { return waves_per_simd(G) * 4 / NWAVE; }
+
 struct Plan {
   int n_splits;
   int tokens_per_split;
@@ -104,7 +114,10 @@ Plan plan_for(int n_head, int n_head_kv, int64_t n_kv) {
   // kMergeCap / G so that the merge's weights fit in LDS, and at least
   // IKV_DECODE_MIN_SPLIT_TOKENS tokens per split.
   const int G = n_head / n_head_kv;
-  int64_t target = (IKV_DECODE_TARGET_WGS + n_head_kv - 1) / n_head_kv;
+  // With one resident workgroup per CU, the workgroups past 256 would run as
+  // a second wave behind the first: stay at one per CU.
+  const int target_wgs = resident_wgs(G) >= 2 ? IKV_DECODE_TARGET_WGS : kCUs;
+  int64_t target = (target_wgs + n_head_kv - 1) / n_head_kv;
   if (target > kMergeCap / G) target = kMergeCap / G;
   const int64_t by_min = (n_kv + IKV_DECODE_MIN_SPLIT_TOKENS - 1) / IKV_DECODE_MIN_SPLIT_TOKENS;
   if (target > by_min) target = by_min;
@@ -380,7 +393,7 @@ __device__ __forceinline__ void merge_splits(const float *part_ml, const float *
 }
 
 template <int G, bool PRO>
-__global__ __launch_bounds__(WG, G <= 4 ? 4 : 2) void decode_kernel(
+__global__ __launch_bounds__(WG, waves_per_simd(G)) void decode_kernel(
     const float *__restrict__ q, float *kc, float *vc, const float *k_new, const float *v_new,
     float *__restrict__ out, int *counters, float *part_ml, float *part_o, int n_head_kv, int n_kv,
     int tokens_per_split, int n_splits, float scale_log2, Prologue pro) {
