@@ -113,6 +113,58 @@ int ikv_attn_prefill_f32(const float *q, const float *k, const float *v, float *
                          float scale, void *stream);
 
 /* ---------------------------------------------------------------------
+ * Paged KV cache. The reference's KVCacheConfig::block_tokens > 0
+ * (include/kvcache/kvutil.hpp:43) asks for a cache cut into blocks, with a
+ * sequence's tokens spread over several storage slices
+ * (src/kvcache/kvstrategy.cpp:83-158) and an attention kernel that follows
+ * them (the TODO at include/op_factory.hpp:38). Here one layer's K (and V)
+ * cache is a pool of n_pool_blocks blocks of block_tokens token rows,
+ * [n_pool_blocks * block_tokens][n_head_kv][head_dim], and logical token t of
+ * a sequence lives in pool row
+ *     block_table[t / block_tokens] * block_tokens + t % block_tokens.
+ * block_tokens must be a positive multiple of 64 (a tile of the kernels never
+ * straddles two blocks). block_table is device memory with an entry for every
+ * block the call touches; an entry outside [0, n_pool_blocks) does not fault:
+ * block 0 is read (or written) instead and *status (device int, if non-NULL)
+ * is set to 1.
+ * ------------------------------------------------------------------- */
+typedef struct ikv_kv_pages {
+    const int32_t *block_table;
+    int64_t block_tokens;
+    int64_t n_pool_blocks;
+    int32_t *status;
+} ikv_kv_pages;
+
+/* Writes n_rows token rows (row_bytes each, one token's K or V for all KV
+ * heads) from src_rows to logical tokens [first_token, first_token + n_rows)
+ * of the paged pool. Byte-exact; nothing else is written. row_bytes must be a
+ * multiple of 16. */
+int ikv_append_paged_f32(void *pool, const void *src_rows, const ikv_kv_pages *pages,
+                         int64_t first_token, size_t n_rows, size_t row_bytes, void *stream);
+
+/* ikv_attn_decode_f32 / ikv_attn_decode_rope_f32 / ikv_attn_prefill_f32 over
+ * a paged cache: k_pool / v_pool are the pools, tokens [0, n_kv) are read
+ * through `pages`, and the fused append writes logical row n_kv - 1. Same
+ * splits, same arithmetic: the results are bit-identical to the contiguous
+ * entry points' on the same logical cache. Workspaces as for those. */
+int ikv_attn_decode_paged_f32(const float *q, float *k_pool, float *v_pool,
+                              const ikv_kv_pages *pages, const float *k_new, const float *v_new,
+                              float *out, int n_head, int n_head_kv, int head_dim, int64_t n_kv,
+                              float scale, void *workspace, size_t workspace_bytes, void *stream);
+int ikv_attn_decode_rope_paged_f32(const float *q_raw, const float *k_raw, const float *v_new,
+                                   float *k_pool, float *v_pool, const ikv_kv_pages *pages,
+                                   float *out, int n_head, int n_head_kv, int head_dim,
+                                   int64_t n_kv, float scale, const float *q_norm_w,
+                                   const float *k_norm_w, float eps, const int32_t *pos,
+                                   const float *sin_tab, const float *cos_tab, int64_t n_ctx,
+                                   int *status, void *workspace, size_t workspace_bytes,
+                                   void *stream);
+int ikv_attn_prefill_paged_f32(const float *q, const float *k_pool, const float *v_pool,
+                               const ikv_kv_pages *pages, float *out, int n_head, int n_head_kv,
+                               int head_dim, int64_t n_q, int64_t n_kv, int64_t n_past,
+                               float scale, void *stream);
+
+/* ---------------------------------------------------------------------
  * RMS norm over rows of `dim` floats: out = (x * s) * w with
  * s = float(1 / sqrt(sum_d double(x_d*x_d) / dim + eps)) — the arithmetic of
  * CPUBackend::compute_rms_norm (src/backends/cpu_backend.cpp:335-382).

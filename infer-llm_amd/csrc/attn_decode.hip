@@ -186,17 +186,20 @@ __device__ __forceinline__ float4 load4_agent(__amdgpu_buffer_rsrc_t r, unsigned
 // are clamped to t_last and scored -inf by the caller, so every lane issues
 // the same unconditional loads (no branch between a load and its use, which
 // keeps the next tile's loads in flight while this one is scored). The new
-// token's row comes from k_new / v_new.
+// token's row comes from k_new / v_new. Token t is read from cache row
+// t + shift (shift = 0 for a contiguous cache; a paged cache's block offset,
+// the same for the whole tile).
 __device__ __forceinline__ void load_tile(float4 (&kr)[R], float4 (&vr)[R], int base, int t_last,
                                           int wave, int half, int new_row, const float *kc,
                                           const float *vc, const float *k_new, const float *v_new,
-                                          size_t tok_stride, size_t head_off) {
+                                          size_t tok_stride, size_t head_off, int64_t shift) {
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int t = min(base + r * (NWAVE * 2) + wave * 2 + half, t_last);
     const bool fresh = (t == new_row);
-    const float *kp = fresh ? k_new + head_off : kc + static_cast<size_t>(t) * tok_stride + head_off;
-    const float *vp = fresh ? v_new + head_off : vc + static_cast<size_t>(t) * tok_stride + head_off;
+    const size_t row = static_cast<size_t>(t + shift) * tok_stride + head_off;
+    const float *kp = fresh ? k_new + head_off : kc + row;
+    const float *vp = fresh ? v_new + head_off : vc + row;
 #if IKV_DECODE_NT
     const f4v ka = __builtin_nontemporal_load(reinterpret_cast<const f4v *>(kp));
     const f4v va = __builtin_nontemporal_load(reinterpret_cast<const f4v *>(vp));
@@ -392,11 +395,11 @@ __device__ __forceinline__ void merge_splits(const float *part_ml, const float *
   }
 }
 
-template <int G, bool PRO>
+template <int G, bool PRO, bool PAGED>
 __global__ __launch_bounds__(WG, waves_per_simd(G)) void decode_kernel(
     const float *__restrict__ q, float *kc, float *vc, const float *k_new, const float *v_new,
     float *__restrict__ out, int *counters, float *part_ml, float *part_o, int n_head_kv, int n_kv,
-    int tokens_per_split, int n_splits, float scale_log2, Prologue pro) {
+    int tokens_per_split, int n_splits, float scale_log2, Prologue pro, ikv::Pages pages) {
   __shared__ float s_acc[NWAVE][G][D];
   __shared__ float s_m[NWAVE][G];
   __shared__ float s_l[NWAVE][G];
@@ -416,11 +419,21 @@ __global__ __launch_bounds__(WG, waves_per_simd(G)) void decode_kernel(
   const size_t tok_stride = static_cast<size_t>(n_head_kv) * D;
   const size_t head_off = static_cast<size_t>(g) * D + 4 * sub;
 
+  // Cache row offset of the tile at token `base`: tiles start at multiples
+  // of TILE from a split start (itself a multiple of TILE), so a paged
+  // cache's block (a multiple of 64 tokens) holds each tile whole.
+  auto shift_of = [&](int base) -> int64_t {
+    if constexpr (PAGED)
+      return ikv::page_shift(pages, base);
+    else
+      return 0;
+  };
+
   // Two register buffers of K/V rows: tile t+1 loads into one while tile t
   // is scored from the other.
   float4 ka[R], va[R], kb[R], vb[R];
   load_tile(ka, va, t_begin, t_end - 1, wave, half, new_row, kc, vc, k_new, v_new, tok_stride,
-            head_off);
+            head_off, shift_of(t_begin));
 
   float4 qv[G];
   float4 knew_rot = make_float4(0.f, 0.f, 0.f, 0.f);  // this lane's piece of rope(norm(k_new))
@@ -497,14 +510,14 @@ __global__ __launch_bounds__(WG, waves_per_simd(G)) void decode_kernel(
       break;
     }
     load_tile(kb, vb, base + TILE, t_end - 1, wave, half, new_row, kc, vc, k_new, v_new,
-              tok_stride, head_off);
+              tok_stride, head_off, shift_of(base + TILE));
     process(ka, va, base);
     if (base + 2 * TILE >= t_end) {
       process(kb, vb, base + TILE);
       break;
     }
     load_tile(ka, va, base + 2 * TILE, t_end - 1, wave, half, new_row, kc, vc, k_new, v_new,
-              tok_stride, head_off);
+              tok_stride, head_off, shift_of(base + 2 * TILE));
     process(kb, vb, base + TILE);
   }
 
@@ -512,7 +525,7 @@ __global__ __launch_bounds__(WG, waves_per_simd(G)) void decode_kernel(
   // RoPE is folded in) and V rows into the caches, 16 bytes per lane of the
   // first half-wave.
   if (new_row >= t_begin && new_row < t_end && wave == 0 && half == 0) {
-    const size_t off = static_cast<size_t>(new_row) * tok_stride + head_off;
+    const size_t off = static_cast<size_t>(new_row + shift_of(new_row)) * tok_stride + head_off;
     float4 kw;
     if constexpr (PRO)
       kw = knew_rot;
@@ -591,25 +604,45 @@ __global__ __launch_bounds__(WG, waves_per_simd(G)) void decode_kernel(
 
 bool supported_group(int G) { return G == 1 || G == 2 || G == 4 || G == 8; }
 
+template <int G, bool PRO, bool PAGED>
+void launch_one(const float *q, float *kc, float *vc, const float *kn, const float *vn, float *out,
+                int *counters, float *part_ml, float *part_o, int n_head_kv, int n_kv,
+                const Plan &p, float scale_log2, const Prologue &pro, const ikv::Pages &pg,
+                hipStream_t s) {
+  decode_kernel<G, PRO, PAGED><<<n_head_kv * p.n_splits, WG, 0, s>>>(
+      q, kc, vc, kn, vn, out, counters, part_ml, part_o, n_head_kv, n_kv, p.tokens_per_split,
+      p.n_splits, scale_log2, pro, pg);
+}
+
 template <int G>
 void launch(const float *q, float *kc, float *vc, const float *kn, const float *vn, float *out,
             int *counters, float *part_ml, float *part_o, int n_head_kv, int n_kv, const Plan &p,
-            float scale_log2, const Prologue *pro, hipStream_t s) {
-  if (pro)
-    decode_kernel<G, true><<<n_head_kv * p.n_splits, WG, 0, s>>>(
-        q, kc, vc, kn, vn, out, counters, part_ml, part_o, n_head_kv, n_kv, p.tokens_per_split,
-        p.n_splits, scale_log2, *pro);
+            float scale_log2, const Prologue *pro, const ikv::Pages *pg, hipStream_t s) {
+  const Prologue none{};
+  const ikv::Pages flat{};
+  if (pro && pg)
+    launch_one<G, true, true>(q, kc, vc, kn, vn, out, counters, part_ml, part_o, n_head_kv, n_kv,
+                              p, scale_log2, *pro, *pg, s);
+  else if (pro)
+    launch_one<G, true, false>(q, kc, vc, kn, vn, out, counters, part_ml, part_o, n_head_kv,
+                               n_kv, p, scale_log2, *pro, flat, s);
+  else if (pg)
+    launch_one<G, false, true>(q, kc, vc, kn, vn, out, counters, part_ml, part_o, n_head_kv,
+                               n_kv, p, scale_log2, none, *pg, s);
   else
-    decode_kernel<G, false><<<n_head_kv * p.n_splits, WG, 0, s>>>(
-        q, kc, vc, kn, vn, out, counters, part_ml, part_o, n_head_kv, n_kv, p.tokens_per_split,
-        p.n_splits, scale_log2, Prologue{});
+    launch_one<G, false, false>(q, kc, vc, kn, vn, out, counters, part_ml, part_o, n_head_kv,
+                                n_kv, p, scale_log2, none, flat, s);
 }
 
 int decode_common(const float *q, float *k_cache, float *v_cache, const float *k_new,
                   const float *v_new, float *out, int n_head, int n_head_kv, int head_dim,
                   int64_t n_kv, float scale, void *workspace, size_t workspace_bytes,
-                  const Prologue *pro, void *stream) {
+                  const Prologue *pro, const ikv_kv_pages *pages, void *stream) {
   if (!q || !k_cache || !v_cache || !out) return -EINVAL;
+  ikv::Pages pg;
+  if (pages) {
+    if (const int rc = ikv::pages_arg(pages, pg)) return rc;
+  }
   if ((k_new == nullptr) != (v_new == nullptr)) return -EINVAL;
   if (n_head <= 0 || n_head_kv <= 0 || n_head % n_head_kv != 0) return -EINVAL;
   if (n_kv <= 0) return -EINVAL;
@@ -636,10 +669,10 @@ int decode_common(const float *q, float *k_cache, float *v_cache, const float *k
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int nk = static_cast<int>(n_kv);
   switch (G) {
-    case 1: launch<1>(q, k_cache, v_cache, k_new, v_new, out, counters, part_ml, part_o, n_head_kv, nk, p, sl2, pro, s); break;
-    case 2: launch<2>(q, k_cache, v_cache, k_new, v_new, out, counters, part_ml, part_o, n_head_kv, nk, p, sl2, pro, s); break;
-    case 4: launch<4>(q, k_cache, v_cache, k_new, v_new, out, counters, part_ml, part_o, n_head_kv, nk, p, sl2, pro, s); break;
-    default: launch<8>(q, k_cache, v_cache, k_new, v_new, out, counters, part_ml, part_o, n_head_kv, nk, p, sl2, pro, s); break;
+    case 1: launch<1>(q, k_cache, v_cache, k_new, v_new, out, counters, part_ml, part_o, n_head_kv, nk, p, sl2, pro, pages ? &pg : nullptr, s); break;
+    case 2: launch<2>(q, k_cache, v_cache, k_new, v_new, out, counters, part_ml, part_o, n_head_kv, nk, p, sl2, pro, pages ? &pg : nullptr, s); break;
+    case 4: launch<4>(q, k_cache, v_cache, k_new, v_new, out, counters, part_ml, part_o, n_head_kv, nk, p, sl2, pro, pages ? &pg : nullptr, s); break;
+    default: launch<8>(q, k_cache, v_cache, k_new, v_new, out, counters, part_ml, part_o, n_head_kv, nk, p, sl2, pro, pages ? &pg : nullptr, s); break;
   }
   return ikv::launch_status();
 }
@@ -660,16 +693,28 @@ extern "C" int ikv_attn_decode_f32(const float *q, float *k_cache, float *v_cach
                                    int n_head_kv, int head_dim, int64_t n_kv, float scale,
                                    void *workspace, size_t workspace_bytes, void *stream) {
   return decode_common(q, k_cache, v_cache, k_new, v_new, out, n_head, n_head_kv, head_dim, n_kv,
-                       scale, workspace, workspace_bytes, nullptr, stream);
+                       scale, workspace, workspace_bytes, nullptr, nullptr, stream);
 }
 
-extern "C" int ikv_attn_decode_rope_f32(const float *q_raw, const float *k_raw, const float *v_new,
-                                        float *k_cache, float *v_cache, float *out, int n_head,
-                                        int n_head_kv, int head_dim, int64_t n_kv, float scale,
-                                        const float *q_norm_w, const float *k_norm_w, float eps,
-                                        const int32_t *pos, const float *sin_tab,
-                                        const float *cos_tab, int64_t n_ctx, int *status,
-                                        void *workspace, size_t workspace_bytes, void *stream) {
+extern "C" int ikv_attn_decode_paged_f32(const float *q, float *k_pool, float *v_pool,
+                                         const ikv_kv_pages *pages, const float *k_new,
+                                         const float *v_new, float *out, int n_head,
+                                         int n_head_kv, int head_dim, int64_t n_kv, float scale,
+                                         void *workspace, size_t workspace_bytes, void *stream) {
+  if (!pages) return -EINVAL;
+  return decode_common(q, k_pool, v_pool, k_new, v_new, out, n_head, n_head_kv, head_dim, n_kv,
+                       scale, workspace, workspace_bytes, nullptr, pages, stream);
+}
+
+namespace {
+
+int decode_rope_common(const float *q_raw, const float *k_raw, const float *v_new, float *k_cache,
+                       float *v_cache, const ikv_kv_pages *pages, float *out, int n_head,
+                       int n_head_kv, int head_dim, int64_t n_kv, float scale,
+                       const float *q_norm_w, const float *k_norm_w, float eps,
+                       const int32_t *pos, const float *sin_tab, const float *cos_tab,
+                       int64_t n_ctx, int *status, void *workspace, size_t workspace_bytes,
+                       void *stream) {
   if (!k_raw || !v_new || !q_norm_w || !k_norm_w || !pos || !sin_tab || !cos_tab || n_ctx <= 0)
     return -EINVAL;
   Prologue pro;
@@ -682,5 +727,31 @@ extern "C" int ikv_attn_decode_rope_f32(const float *q_raw, const float *k_raw, 
   pro.n_ctx = n_ctx;
   pro.status = status;
   return decode_common(q_raw, k_cache, v_cache, k_raw, v_new, out, n_head, n_head_kv, head_dim,
-                       n_kv, scale, workspace, workspace_bytes, &pro, stream);
+                       n_kv, scale, workspace, workspace_bytes, &pro, pages, stream);
+}
+
+}  // namespace
+
+extern "C" int ikv_attn_decode_rope_f32(const float *q_raw, const float *k_raw, const float *v_new,
+                                        float *k_cache, float *v_cache, float *out, int n_head,
+                                        int n_head_kv, int head_dim, int64_t n_kv, float scale,
+                                        const float *q_norm_w, const float *k_norm_w, float eps,
+                                        const int32_t *pos, const float *sin_tab,
+                                        const float *cos_tab, int64_t n_ctx, int *status,
+                                        void *workspace, size_t workspace_bytes, void *stream) {
+  return decode_rope_common(q_raw, k_raw, v_new, k_cache, v_cache, nullptr, out, n_head,
+                            n_head_kv, head_dim, n_kv, scale, q_norm_w, k_norm_w, eps, pos,
+                            sin_tab, cos_tab, n_ctx, status, workspace, workspace_bytes, stream);
+}
+
+extern "C" int ikv_attn_decode_rope_paged_f32(
+    const float *q_raw, const float *k_raw, const float *v_new, float *k_pool, float *v_pool,
+    const ikv_kv_pages *pages, float *out, int n_head, int n_head_kv, int head_dim, int64_t n_kv,
+    float scale, const float *q_norm_w, const float *k_norm_w, float eps, const int32_t *pos,
+    const float *sin_tab, const float *cos_tab, int64_t n_ctx, int *status, void *workspace,
+    size_t workspace_bytes, void *stream) {
+  if (!pages) return -EINVAL;
+  return decode_rope_common(q_raw, k_raw, v_new, k_pool, v_pool, pages, out, n_head, n_head_kv,
+                            head_dim, n_kv, scale, q_norm_w, k_norm_w, eps, pos, sin_tab, cos_tab,
+                            n_ctx, status, workspace, workspace_bytes, stream);
 }

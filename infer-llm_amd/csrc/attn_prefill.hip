@@ -76,14 +76,14 @@ __device__ __forceinline__ float row_sum4(float x) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-template <int G, int NW>
+template <int G, int NW, bool PAGED>
 __global__ __launch_bounds__(NW * 64) void prefill_kernel(const float *__restrict__ q,
                                                           const float *__restrict__ k,
                                                           const float *__restrict__ v,
                                                           float *__restrict__ out, int n_head_kv,
                                                           int n_q, int n_kv, int n_past,
                                                           int n_blocks, int paired,
-                                                          float scale_log2) {
+                                                          float scale_log2, ikv::Pages pages) {
   constexpr int BQ = NW * 16 / G;
   // [buffer][K | V]; K rows hold 16-byte chunk c at slot c ^ (key & 15)
   __shared__ __attribute__((aligned(16))) float s_buf0[2 * TILE];
@@ -98,15 +98,19 @@ __global__ __launch_bounds__(NW * 64) void prefill_kernel(const float *__restric
   const int row = wave * 16 + j;
   const int n_head = n_head_kv * G;
 
-  // this wave's share of one tile: chunks c = wave + NW*i, 1 KB (2 keys) each
+  // this wave's share of one tile: chunks c = wave + NW*i, 1 KB (2 keys) each.
+  // A paged cache's block (a multiple of 64 keys) holds every tile whole, so
+  // one block offset serves the tile.
   auto issue = [&](float *buf, int tile) {
+    int64_t shift = 0;
+    if constexpr (PAGED) shift = ikv::page_shift(pages, tile * BN);
 #pragma unroll
     for (int i = 0; i < 16 / NW; ++i) {
       const int c = wave + NW * i;
       const int key = 2 * c + (lane >> 5);
       const int slot = lane & 31;
       const int kg = min(tile * BN + key, n_kv - 1);
-      const size_t rowoff = (static_cast<size_t>(kg) * n_head_kv + g) * D;
+      const size_t rowoff = (static_cast<size_t>(kg + shift) * n_head_kv + g) * D;
       __builtin_amdgcn_global_load_lds(k + rowoff + 4 * (slot ^ (key & 15)),
                                        (lds_ptr)(buf + c * 256), 16, 0, 0);
       __builtin_amdgcn_global_load_lds(v + rowoff + 4 * slot, (lds_ptr)(buf + TILE + c * 256),
@@ -272,12 +276,17 @@ __global__ __launch_bounds__(NW * 64) void prefill_kernel(const float *__restric
 
 template <int G, int NW>
 void launch_nw(const float *q, const float *k, const float *v, float *out, int n_head_kv, int n_q,
-               int n_kv, int n_past, float scale_log2, int paired, hipStream_t s) {
+               int n_kv, int n_past, float scale_log2, int paired, const ikv::Pages *pg,
+               hipStream_t s) {
   constexpr int BQ = NW * 16 / G;
   const int n_blocks = (n_q + BQ - 1) / BQ;
   const int items = paired ? (n_blocks + 1) / 2 : n_blocks;
-  prefill_kernel<G, NW><<<n_head_kv * items, NW * 64, 0, s>>>(
-      q, k, v, out, n_head_kv, n_q, n_kv, n_past, n_blocks, paired, scale_log2);
+  if (pg)
+    prefill_kernel<G, NW, true><<<n_head_kv * items, NW * 64, 0, s>>>(
+        q, k, v, out, n_head_kv, n_q, n_kv, n_past, n_blocks, paired, scale_log2, *pg);
+  else
+    prefill_kernel<G, NW, false><<<n_head_kv * items, NW * 64, 0, s>>>(
+        q, k, v, out, n_head_kv, n_q, n_kv, n_past, n_blocks, paired, scale_log2, ikv::Pages{});
 }
 
 // Shape choice: 4-wave blocks (64 rows) share each staged K/V tile among the
@@ -286,25 +295,33 @@ void launch_nw(const float *q, const float *k, const float *v, float *out, int n
 // is used only when the paired grid still gives every CU a workgroup.
 template <int G>
 void launch(const float *q, const float *k, const float *v, float *out, int n_head_kv, int n_q,
-            int n_kv, int n_past, float scale_log2, hipStream_t s) {
+            int n_kv, int n_past, float scale_log2, const ikv::Pages *pg, hipStream_t s) {
   int nw = IKV_PREFILL_NW;
   auto blocks = [&](int w) { return (n_q + w * 16 / G - 1) / (w * 16 / G); };
   if (nw == 0) nw = blocks(4) * n_head_kv >= IKV_PREFILL_PAIR_MIN_WGS ? 4 : 2;
   const int nb = blocks(nw);
   const int paired = (nb >= 2 && (nb + 1) / 2 * n_head_kv >= IKV_PREFILL_PAIR_MIN_WGS) ? 1 : 0;
   if (nw == 4)
-    launch_nw<G, 4>(q, k, v, out, n_head_kv, n_q, n_kv, n_past, scale_log2, paired, s);
+    launch_nw<G, 4>(q, k, v, out, n_head_kv, n_q, n_kv, n_past, scale_log2, paired, pg, s);
   else
-    launch_nw<G, 2>(q, k, v, out, n_head_kv, n_q, n_kv, n_past, scale_log2, paired, s);
+    launch_nw<G, 2>(q, k, v, out, n_head_kv, n_q, n_kv, n_past, scale_log2, paired, pg, s);
 }
 
 }  // namespace
 
-extern "C" int ikv_attn_prefill_f32(const float *q, const float *k, const float *v, float *out,
-                                    int n_head, int n_head_kv, int head_dim, int64_t n_q,
-                                    int64_t n_kv, int64_t n_past, float scale, void *stream) {
+namespace {
+
+int prefill_common(const float *q, const float *k, const float *v, const ikv_kv_pages *pages,
+                   float *out, int n_head, int n_head_kv, int head_dim, int64_t n_q,
+                   int64_t n_kv, int64_t n_past, float scale, void *stream) {
   if (n_q == 0) return 0;
   if (!q || !k || !v || !out) return -EINVAL;
+  ikv::Pages pgv;
+  const ikv::Pages *pg = nullptr;
+  if (pages) {
+    if (const int rc = ikv::pages_arg(pages, pgv)) return rc;
+    pg = &pgv;
+  }
   if (n_head <= 0 || n_head_kv <= 0 || n_head % n_head_kv != 0) return -EINVAL;
   if (n_q < 0 || n_kv <= 0 || n_past < 0) return -EINVAL;
   if (head_dim != D) return -ENOTSUP;
@@ -318,10 +335,29 @@ extern "C" int ikv_attn_prefill_f32(const float *q, const float *k, const float 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int nq = static_cast<int>(n_q), nk = static_cast<int>(n_kv), np = static_cast<int>(n_past);
   switch (G) {
-    case 1: launch<1>(q, k, v, out, n_head_kv, nq, nk, np, sl2, s); break;
-    case 2: launch<2>(q, k, v, out, n_head_kv, nq, nk, np, sl2, s); break;
-    case 4: launch<4>(q, k, v, out, n_head_kv, nq, nk, np, sl2, s); break;
-    default: launch<8>(q, k, v, out, n_head_kv, nq, nk, np, sl2, s); break;
+    case 1: launch<1>(q, k, v, out, n_head_kv, nq, nk, np, sl2, pg, s); break;
+    case 2: launch<2>(q, k, v, out, n_head_kv, nq, nk, np, sl2, pg, s); break;
+    case 4: launch<4>(q, k, v, out, n_head_kv, nq, nk, np, sl2, pg, s); break;
+    default: launch<8>(q, k, v, out, n_head_kv, nq, nk, np, sl2, pg, s); break;
   }
   return ikv::launch_status();
+}
+
+}  // namespace
+
+extern "C" int ikv_attn_prefill_f32(const float *q, const float *k, const float *v, float *out,
+                                    int n_head, int n_head_kv, int head_dim, int64_t n_q,
+                                    int64_t n_kv, int64_t n_past, float scale, void *stream) {
+  return prefill_common(q, k, v, nullptr, out, n_head, n_head_kv, head_dim, n_q, n_kv, n_past,
+                        scale, stream);
+}
+
+extern "C" int ikv_attn_prefill_paged_f32(const float *q, const float *k_pool,
+                                          const float *v_pool, const ikv_kv_pages *pages,
+                                          float *out, int n_head, int n_head_kv, int head_dim,
+                                          int64_t n_q, int64_t n_kv, int64_t n_past, float scale,
+                                          void *stream) {
+  if (!pages) return -EINVAL;
+  return prefill_common(q, k_pool, v_pool, pages, out, n_head, n_head_kv, head_dim, n_q, n_kv,
+                        n_past, scale, stream);
 }

@@ -8,7 +8,10 @@
 #include <cerrno>
 #include <cmath>
 #include <cstddef>
+#include <climits>
 #include <cstdint>
+
+#include "../../include/ikv.h"
 
 namespace ikv {
 
@@ -93,6 +96,43 @@ __device__ __forceinline__ float rms_scale_strided(const float4 *row, int dim, f
   }
   for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
   return static_cast<float>(1.0 / sqrt(s / static_cast<double>(dim) + static_cast<double>(eps)));
+}
+
+// A paged KV cache as the kernels see it: logical token t lives in pool row
+// table[t / bt] * bt + t % bt (bt a multiple of 64).
+struct Pages {
+  const int32_t *table = nullptr;
+  int bt = 0;
+  int n_blocks = 0;
+  int *status = nullptr;
+};
+
+// Offset that takes logical token t to its pool row (t + shift), shared by
+// every token of t's block. A table entry outside [0, n_blocks) maps to block
+// 0 and raises *status. t is uniform across the wave, so the entry is one
+// scalar load.
+__device__ __forceinline__ int64_t page_shift(const Pages &pg, int t) {
+  const int b = t / pg.bt;
+  int blk = pg.table[b];
+  if (static_cast<unsigned>(blk) >= static_cast<unsigned>(pg.n_blocks)) {
+    if (pg.status) *pg.status = 1;
+    blk = 0;
+  }
+  return static_cast<int64_t>(blk - b) * pg.bt;
+}
+
+// Host check of a paged-cache descriptor: a table, blocks of a positive
+// multiple of 64 tokens, pool rows that index in int.
+inline int pages_arg(const ikv_kv_pages *p, Pages &out) {
+  if (!p || !p->block_table || p->block_tokens <= 0 || p->block_tokens % 64 != 0 ||
+      p->n_pool_blocks <= 0)
+    return -EINVAL;
+  if (p->block_tokens > INT_MAX / p->n_pool_blocks) return -EOVERFLOW;
+  out.table = p->block_table;
+  out.bt = static_cast<int>(p->block_tokens);
+  out.n_blocks = static_cast<int>(p->n_pool_blocks);
+  out.status = p->status;
+  return 0;
 }
 
 }  // namespace ikv

@@ -28,6 +28,15 @@ _c_int = ctypes.c_int
 _c_int64 = ctypes.c_int64
 _c_float = ctypes.c_float
 
+
+class KvPages(ctypes.Structure):
+    """ikv_kv_pages (include/ikv.h): a paged KV pool's block table."""
+    _fields_ = [("block_table", ctypes.c_void_p), ("block_tokens", ctypes.c_int64),
+                ("n_pool_blocks", ctypes.c_int64), ("status", ctypes.c_void_p)]
+
+
+_c_pages = ctypes.POINTER(KvPages)
+
 # name -> (restype, argtypes); include/ikv.h, then include/ikv_probe.h
 SIGNATURES = {
     "ikv_version": (ctypes.c_char_p, []),
@@ -47,6 +56,24 @@ SIGNATURES = {
     "ikv_attn_prefill_f32": (
         _c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int,
+         _c_int64, _c_int64, _c_int64, _c_float, _c_void_p],
+    ),
+    "ikv_append_paged_f32": (
+        _c_int, [_c_void_p, _c_void_p, _c_pages, _c_int64, _c_size_t, _c_size_t, _c_void_p]),
+    "ikv_attn_decode_paged_f32": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_pages, _c_void_p, _c_void_p, _c_void_p,
+         _c_int, _c_int, _c_int, _c_int64, _c_float, _c_void_p, _c_size_t, _c_void_p],
+    ),
+    "ikv_attn_decode_rope_paged_f32": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_pages, _c_void_p, _c_int,
+         _c_int, _c_int, _c_int64, _c_float, _c_void_p, _c_void_p, _c_float, _c_void_p,
+         _c_void_p, _c_void_p, _c_int64, _c_void_p, _c_void_p, _c_size_t, _c_void_p],
+    ),
+    "ikv_attn_prefill_paged_f32": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_pages, _c_void_p, _c_int, _c_int, _c_int,
          _c_int64, _c_int64, _c_int64, _c_float, _c_void_p],
     ),
     "ikv_rms_norm_f32": (
@@ -265,6 +292,99 @@ def attn_prefill(q, k, v, n_past: int = 0, *, n_kv: Optional[int] = None, out=No
     rc = load().ikv_attn_prefill_f32(_ptr(q), _ptr(k), _ptr(v), _ptr(out), n_head, n_head_kv, D,
                                      n_q, n_kv, n_past, scale, _stream(stream))
     _check("ikv_attn_prefill_f32", rc)
+    return out
+
+
+# ----------------------------------------------------------------------------
+# paged KV pool: [n_blocks * block_tokens, n_head_kv, D] per K and V; logical
+# token t in pool row table[t // block_tokens] * block_tokens + t % block_tokens
+# ----------------------------------------------------------------------------
+
+def kv_pages(table, block_tokens: int, pool, status=None) -> KvPages:
+    """The ikv_kv_pages descriptor of a device int32 block table over `pool`."""
+    torch = _torch()
+    if table.dtype != torch.int32 or not table.is_cuda or not table.is_contiguous():
+        raise ValueError("block table must be a contiguous device int32 tensor")
+    if pool.shape[0] % block_tokens:
+        raise ValueError("pool rows must be whole blocks")
+    return KvPages(table.data_ptr(), block_tokens, pool.shape[0] // block_tokens, _ptr(status))
+
+
+def append_paged(pool, src_rows, table, block_tokens: int, first_token: int, status=None,
+                 stream=None) -> None:
+    """Writes src_rows [n, n_head_kv, D] to logical tokens first_token.. of the pool."""
+    _need_f32_dev("pool", pool)
+    _need_f32_dev("src_rows", src_rows)
+    n_rows = src_rows.shape[0]
+    row_bytes = src_rows[0].numel() * 4 if n_rows else 0
+    pg = kv_pages(table, block_tokens, pool, status)
+    _check("ikv_append_paged_f32",
+           load().ikv_append_paged_f32(_ptr(pool), _ptr(src_rows), ctypes.byref(pg), first_token,
+                                       n_rows, row_bytes, _stream(stream)))
+
+
+def attn_decode_paged(q, k_pool, v_pool, table, block_tokens: int, n_kv: int, *, k_new=None,
+                      v_new=None, out=None, scale: float = 0.0, status=None, workspace=None,
+                      stream=None):
+    """attn_decode over a paged pool (logical rows [0, n_kv) through `table`)."""
+    torch = _torch()
+    for name, t in (("q", q), ("k_pool", k_pool), ("v_pool", v_pool)):
+        _need_f32_dev(name, t)
+    n_head, D = q.shape[-2], q.shape[-1]
+    n_head_kv = k_pool.shape[-2]
+    if out is None:
+        out = torch.empty((n_head, D), dtype=torch.float32, device=q.device)
+    if workspace is None:
+        workspace = decode_workspace(n_head, n_head_kv, D, n_kv, device=q.device)
+    pg = kv_pages(table, block_tokens, k_pool, status)
+    rc = load().ikv_attn_decode_paged_f32(
+        _ptr(q), _ptr(k_pool), _ptr(v_pool), ctypes.byref(pg), _ptr(k_new), _ptr(v_new),
+        _ptr(out), n_head, n_head_kv, D, n_kv, scale, _ptr(workspace), workspace.numel() * 4,
+        _stream(stream))
+    _check("ikv_attn_decode_paged_f32", rc)
+    return out
+
+
+def attn_decode_rope_paged(q_raw, k_raw, v_new, k_pool, v_pool, table, block_tokens: int,
+                           n_kv: int, q_norm_w, k_norm_w, eps: float, pos, sin_tab, cos_tab, *,
+                           out=None, scale: float = 0.0, status=None, page_status=None,
+                           workspace=None, stream=None):
+    """attn_decode_rope over a paged pool."""
+    torch = _torch()
+    n_head, D = q_raw.shape[-2], q_raw.shape[-1]
+    n_head_kv = k_pool.shape[-2]
+    if out is None:
+        out = torch.empty((n_head, D), dtype=torch.float32, device=q_raw.device)
+    if workspace is None:
+        workspace = decode_workspace(n_head, n_head_kv, D, n_kv, device=q_raw.device)
+    pg = kv_pages(table, block_tokens, k_pool, page_status)
+    rc = load().ikv_attn_decode_rope_paged_f32(
+        _ptr(q_raw), _ptr(k_raw), _ptr(v_new), _ptr(k_pool), _ptr(v_pool), ctypes.byref(pg),
+        _ptr(out), n_head, n_head_kv, D, n_kv, scale, _ptr(q_norm_w), _ptr(k_norm_w), eps,
+        _ptr(pos), _ptr(sin_tab), _ptr(cos_tab), sin_tab.shape[0], _ptr(status), _ptr(workspace),
+        workspace.numel() * 4, _stream(stream))
+    _check("ikv_attn_decode_rope_paged_f32", rc)
+    return out
+
+
+def attn_prefill_paged(q, k_pool, v_pool, table, block_tokens: int, n_past: int = 0, *,
+                       n_kv: Optional[int] = None, out=None, scale: float = 0.0, status=None,
+                       stream=None):
+    """attn_prefill over a paged pool."""
+    torch = _torch()
+    for name, t in (("q", q), ("k_pool", k_pool), ("v_pool", v_pool)):
+        _need_f32_dev(name, t)
+    n_q, n_head, D = q.shape
+    n_head_kv = k_pool.shape[1]
+    if n_kv is None:
+        n_kv = n_past + n_q
+    if out is None:
+        out = torch.empty_like(q)
+    pg = kv_pages(table, block_tokens, k_pool, status)
+    rc = load().ikv_attn_prefill_paged_f32(_ptr(q), _ptr(k_pool), _ptr(v_pool), ctypes.byref(pg),
+                                           _ptr(out), n_head, n_head_kv, D, n_q, n_kv, n_past,
+                                           scale, _stream(stream))
+    _check("ikv_attn_prefill_paged_f32", rc)
     return out
 
 

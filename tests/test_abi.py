@@ -98,3 +98,29 @@ def test_sincos_table_is_bitwise_glibc():
     sin_ref = r[:, np.arange(64), np.arange(64) + 64]
     assert np.array_equal(c.view(np.uint32), cos_ref.view(np.uint32))
     assert np.array_equal(s.view(np.uint32), sin_ref.view(np.uint32))
+
+
+def test_paged_entry_points_reject_bad_descriptors():
+    P = 64
+    good = ikv.KvPages(P, 64, 10, None)
+    bad_bt = ikv.KvPages(P, 48, 10, None)          # not a multiple of 64
+    no_table = ikv.KvPages(None, 64, 10, None)
+    huge = ikv.KvPages(P, 2**30, 2**20, None)     # pool rows beyond int
+    ref = ctypes.byref
+
+    def dec(pg):
+        return _rc("ikv_attn_decode_paged_f32", P, P, P, pg, None, None, P, 16, 8, 128, 60, 0.0,
+                   None, 0, None)
+
+    assert dec(None) == -errno.EINVAL
+    assert dec(ref(bad_bt)) == -errno.EINVAL
+    assert dec(ref(no_table)) == -errno.EINVAL
+    assert dec(ref(huge)) == -errno.EOVERFLOW
+    assert _rc("ikv_attn_prefill_paged_f32", P, P, P, None, P, 16, 8, 128, 4, 10, 0, 0.0,
+               None) == -errno.EINVAL
+    assert _rc("ikv_attn_prefill_paged_f32", P, P, P, ref(bad_bt), P, 16, 8, 128, 4, 10, 0, 0.0,
+               None) == -errno.EINVAL
+    assert _rc("ikv_append_paged_f32", P, P, ref(good), 0, 0, 4096, None) == 0  # nothing to do
+    assert _rc("ikv_append_paged_f32", P, P, ref(good), -1, 1, 4096, None) == -errno.EINVAL
+    assert _rc("ikv_append_paged_f32", P, P, ref(good), 0, 1, 4100, None) == -errno.EINVAL
+    assert _rc("ikv_append_paged_f32", P, P, None, 0, 1, 4096, None) == -errno.EINVAL
