@@ -45,6 +45,13 @@ typedef struct ikv_qwen3 ikv_qwen3;
 /* Creates the model on HIP device `device` with weights allocated (not yet
  * initialised) and a KV cache of max_ctx tokens per layer. */
 int ikv_qwen3_create(const ikv_qwen3_config *cfg, int device, int64_t max_ctx, ikv_qwen3 **out);
+/* The same with a paged KV cache (KVCacheConfig::block_tokens > 0,
+ * include/kvcache/kvutil.hpp:43 of the reference): per layer a pool of
+ * pool_blocks blocks of block_tokens tokens (a positive multiple of 64;
+ * pool_blocks 0 = enough for one max_ctx sequence), blocks taken as a
+ * sequence grows and returned when the next generate() starts a new one. */
+int ikv_qwen3_create_paged(const ikv_qwen3_config *cfg, int device, int64_t max_ctx,
+                           int64_t block_tokens, int64_t pool_blocks, ikv_qwen3 **out);
 
 /* Weight tensors by GGUF name (ModelBase::load_weight, src/model.cpp:
  * 164-311): "token_embd.weight", "blk.<i>.attn_q.weight", ...,

@@ -26,9 +26,13 @@ HIPBackend *hip(ikv_qwen3 *m) { return static_cast<HIPBackend *>(m->backend.get(
 
 }  // namespace
 
-extern "C" int ikv_qwen3_create(const ikv_qwen3_config *cfg, int device, int64_t max_ctx,
-                                ikv_qwen3 **out) {
+namespace {
+
+int create(const ikv_qwen3_config *cfg, int device, int64_t max_ctx, int64_t block_tokens,
+           int64_t pool_blocks, ikv_qwen3 **out) {
   if (!cfg || !out || max_ctx <= 0 || device < 0) return -EINVAL;
+  if (block_tokens < 0 || pool_blocks < 0 || (block_tokens > 0 && block_tokens % 64 != 0))
+    return -EINVAL;
   *out = nullptr;
   if (cfg->n_layer == 0 || cfg->n_embd == 0 || cfg->n_head == 0 || cfg->n_head_kv == 0 ||
       cfg->head_dim == 0 || cfg->n_ff == 0 || cfg->n_vocab == 0 ||
@@ -56,11 +60,25 @@ extern "C" int ikv_qwen3_create(const ikv_qwen3_config *cfg, int device, int64_t
   hp.rms_norm_eps = cfg->rms_norm_eps;
   m->model = std::make_unique<Qwen3Model>(hp);
   if (auto r = m->model->alloc_weights(m->backend.get()); !r) return to_errno(r.error());
-  m->runner = std::make_unique<Qwen3Runner>(*m->model, *hip(m.get()), size_t(max_ctx));
+  m->runner = std::make_unique<Qwen3Runner>(*m->model, *hip(m.get()), size_t(max_ctx),
+                                            size_t(block_tokens), size_t(pool_blocks));
   if (auto r = m->runner->init(); !r) return to_errno(r.error());
   m->names = m->model->tensor_names();
   *out = m.release();
   return 0;
+}
+
+}  // namespace
+
+extern "C" int ikv_qwen3_create(const ikv_qwen3_config *cfg, int device, int64_t max_ctx,
+                                ikv_qwen3 **out) {
+  return create(cfg, device, max_ctx, 0, 0, out);
+}
+
+extern "C" int ikv_qwen3_create_paged(const ikv_qwen3_config *cfg, int device, int64_t max_ctx,
+                                      int64_t block_tokens, int64_t pool_blocks, ikv_qwen3 **out) {
+  if (block_tokens <= 0) return -EINVAL;
+  return create(cfg, device, max_ctx, block_tokens, pool_blocks, out);
 }
 
 extern "C" int ikv_qwen3_tensor_count(const ikv_qwen3 *m) {

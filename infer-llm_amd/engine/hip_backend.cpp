@@ -30,6 +30,18 @@ bool contiguous_f32(const Tensor *t) {
   return t && t->data && t->dataType == GGML_TYPE_F32 && t->is_contiguous();
 }
 
+// A KV CPY or VIEW node of a paged layer (append_kv_paged): the block table
+// rides in src[1], (block_tokens, pool blocks, first token) in op_params.
+bool is_paged(const Tensor *t) {
+  return t && (t->op == OperationType::GGML_OP_CPY || t->op == OperationType::GGML_OP_VIEW) &&
+         t->src[1] && t->src[1]->dataType == GGML_TYPE_I32 && t->src[1]->data;
+}
+
+ikv_kv_pages pages_of(const Tensor *t, int *status) {
+  return ikv_kv_pages{static_cast<const int32_t *>(t->src[1]->data), t->op_params[0],
+                      t->op_params[1], status};
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------
@@ -351,10 +363,17 @@ infer::expected<void, std::error_code> HIPBackend::compute(Graph &graph) {
         AttnParams p;
         std::memcpy(&p, n->op_params, sizeof(p));
         const size_t row = static_cast<size_t>(kv->dims[0] * kv->dims[1]) * 4;
-        const bool last_row_k = kc->dims[2] == 1 && kc->dims[3] == 1 &&
-                                kc->data == static_cast<char *>(kv->data) + (n_kv - 1) * row;
-        const bool last_row_v = vc->dims[2] == 1 && vc->dims[3] == 1 &&
-                                vc->data == static_cast<char *>(vv->data) + (n_kv - 1) * row;
+        // the copies write exactly the last row the views read: by address
+        // for a contiguous cache, by logical token for a paged one
+        auto last_row = [&](const Tensor *c, const Tensor *view) {
+          if (c->dims[2] != 1 || c->dims[3] != 1 || is_paged(c) != is_paged(view)) return false;
+          if (is_paged(c))
+            return c->src[1] == view->src[1] && c->data == view->data &&
+                   int64_t(c->op_params[2]) == n_kv - 1;
+          return c->data == static_cast<char *>(view->data) + (n_kv - 1) * row;
+        };
+        const bool last_row_k = last_row(kc, kv);
+        const bool last_row_v = last_row(vc, vv);
         if (!last_row_k || !last_row_v || int64_t(p.n_ctx) + 1 != n_kv) continue;
         if (!contiguous_f32(kc->src[0]) || !contiguous_f32(vc->src[0])) continue;
         _append_into_attn[n] = {kc->src[0], vc->src[0]};
@@ -497,6 +516,12 @@ infer::expected<void, std::error_code> HIPBackend::dispatch(Tensor *node) {
       const size_t rows = static_cast<size_t>(node->dims[2] * node->dims[3]);
       const size_t row_bytes = static_cast<size_t>(node->dims[0] * node->dims[1]) * dataType_size(node->dataType);
       ++_stats.launches;
+      if (is_paged(node)) {
+        const ikv_kv_pages pg = pages_of(node, _status);
+        return check_ikv(ikv_append_paged_f32(node->data, src->data, &pg, node->op_params[2], rows,
+                                              row_bytes, s),
+                         "append_paged");
+      }
       return check_ikv(ikv_append_f32(node->data, src->data, rows, row_bytes, s), "append");
     }
 
@@ -580,6 +605,8 @@ infer::expected<void, std::error_code> HIPBackend::dispatch(Tensor *node) {
         }
         const size_t need = ikv_attn_decode_workspace_bytes(int(Hq), int(Hkv), int(D), nkv);
         if (auto r = ensure_workspace(need); !r) return r;
+        const bool paged = is_paged(k) && is_paged(v);
+        const ikv_kv_pages pg = paged ? pages_of(k, _status) : ikv_kv_pages{};
         if (const auto rf = _rope_into_attn.find(node); rf != _rope_into_attn.end()) {
           const Tensor *qr = rf->second.first, *kr = rf->second.second;
           const Tensor *qn = _norm_into_rope[qr], *kn = _norm_into_rope[kr];
@@ -591,6 +618,18 @@ infer::expected<void, std::error_code> HIPBackend::dispatch(Tensor *node) {
           float eps;
           std::memcpy(&eps, &qn->op_params[0], sizeof(eps));
           ++_stats.fused_rope_decode;
+          if (paged)
+            return check_ikv(ikv_attn_decode_rope_paged_f32(
+                                 static_cast<const float *>(qn->src[0]->data),
+                                 static_cast<const float *>(kn->src[0]->data),
+                                 static_cast<const float *>(vn), static_cast<float *>(k->data),
+                                 static_cast<float *>(v->data), &pg, static_cast<float *>(node->data),
+                                 int(Hq), int(Hkv), int(D), nkv, p.scale,
+                                 static_cast<const float *>(qn->src[1]->data),
+                                 static_cast<const float *>(kn->src[1]->data), eps,
+                                 static_cast<const int32_t *>(pos->data), (*tab)->sin, (*tab)->cos,
+                                 (*tab)->n_ctx, _status, _workspace, _workspace_bytes, s),
+                             "attn_decode_rope_paged");
           return check_ikv(ikv_attn_decode_rope_f32(
                                static_cast<const float *>(qn->src[0]->data),
                                static_cast<const float *>(kn->src[0]->data),
@@ -603,12 +642,29 @@ infer::expected<void, std::error_code> HIPBackend::dispatch(Tensor *node) {
                                (*tab)->n_ctx, _status, _workspace, _workspace_bytes, s),
                            "attn_decode_rope");
         }
+        if (paged)
+          return check_ikv(ikv_attn_decode_paged_f32(
+                               static_cast<const float *>(q->data), static_cast<float *>(k->data),
+                               static_cast<float *>(v->data), &pg, static_cast<const float *>(kn),
+                               static_cast<const float *>(vn), static_cast<float *>(node->data),
+                               int(Hq), int(Hkv), int(D), nkv, p.scale, _workspace,
+                               _workspace_bytes, s),
+                           "attn_decode_paged");
         return check_ikv(ikv_attn_decode_f32(static_cast<const float *>(q->data),
                                              static_cast<float *>(k->data), static_cast<float *>(v->data),
                                              static_cast<const float *>(kn), static_cast<const float *>(vn),
                                              static_cast<float *>(node->data), int(Hq), int(Hkv), int(D),
                                              nkv, p.scale, _workspace, _workspace_bytes, s),
                          "attn_decode");
+      }
+      if (is_paged(k) && is_paged(v)) {
+        const ikv_kv_pages pg = pages_of(k, _status);
+        return check_ikv(ikv_attn_prefill_paged_f32(static_cast<const float *>(q->data),
+                                                    static_cast<const float *>(k->data),
+                                                    static_cast<const float *>(v->data), &pg,
+                                                    static_cast<float *>(node->data), int(Hq),
+                                                    int(Hkv), int(D), nq, nkv, p.n_ctx, p.scale, s),
+                         "attn_prefill_paged");
       }
       return check_ikv(ikv_attn_prefill_f32(static_cast<const float *>(q->data),
                                             static_cast<const float *>(k->data),

@@ -103,3 +103,83 @@ void NaiveKVStorage::destroy_object(StorageId id) noexcept {
   Backend *backend = _backend_layer[it->second.layer];
   if (backend) backend->free(BufferKind::KVCACHE, it->second.object.k_base);
 }
+
+// ---------------------------------------------------------------------------
+
+BlockPoolKVStorage::~BlockPoolKVStorage() {
+  for (std::size_t l = 0; l < _pools.size(); ++l)
+    if (_pools[l].base && _backend_layer[l]) _backend_layer[l]->free(BufferKind::KVCACHE, _pools[l].base);
+}
+
+infer::expected<void, std::error_code> BlockPoolKVStorage::init(
+    std::span<const KVLayerSpec> layers, std::span<Backend *const> backend_layer) {
+  if (layers.size() != backend_layer.size() || !_pools.empty() || _blocks == 0 ||
+      _block_tokens == 0)
+    return infer::fail(std::errc::invalid_argument);
+  _layers.assign(layers.begin(), layers.end());
+  _backend_layer.assign(backend_layer.begin(), backend_layer.end());
+  _pools.resize(layers.size());
+  for (std::size_t l = 0; l < layers.size(); ++l) {
+    Backend *backend = _backend_layer[l];
+    if (!backend) return infer::fail(std::errc::invalid_argument);
+    const KVLayerSpec &sp = _layers[l];
+    const std::size_t k_row = sp.n_kv_heads * sp.k_head_dim * dataType_size(sp.k_type);
+    const std::size_t v_row = sp.n_kv_heads * sp.v_head_dim * dataType_size(sp.v_type);
+    const std::size_t rows = _blocks * _block_tokens;
+    if (rows / _blocks != _block_tokens || (k_row && rows > SIZE_MAX / 2 / k_row) ||
+        (v_row && rows > SIZE_MAX / 2 / v_row))
+      return infer::fail(std::errc::value_too_large);
+    Pool &p = _pools[l];
+    p.k_block_bytes = k_row * _block_tokens;
+    p.v_block_bytes = v_row * _block_tokens;
+    auto mem = backend->alloc(BufferKind::KVCACHE, (p.k_block_bytes + p.v_block_bytes) * _blocks);
+    if (!mem) return infer::unexpected(mem.error());
+    p.base = *mem;
+    p.k = p.base;
+    p.v = static_cast<std::byte *>(p.base) + p.k_block_bytes * _blocks;
+    p.free.resize(_blocks);
+    // handed out from the back: block 0 first
+    for (std::size_t b = 0; b < _blocks; ++b) p.free[b] = _blocks - 1 - b;
+  }
+  return {};
+}
+
+infer::expected<StorageId, std::error_code> BlockPoolKVStorage::alloc(std::size_t layer,
+                                                                     std::size_t capacity_tokens) {
+  if (layer >= _pools.size() || capacity_tokens != _block_tokens)
+    return infer::fail(std::errc::invalid_argument);
+  Pool &p = _pools[layer];
+  if (p.free.empty()) return infer::fail(std::errc::not_enough_memory);
+  const std::size_t b = p.free.back();
+  const StorageId id = _next_storage_id++;
+  KVStorageObject obj{.id = id,
+                      .backend = _backend_layer[layer],
+                      .capacity_tokens = _block_tokens,
+                      .k_base = static_cast<std::byte *>(p.k) + b * p.k_block_bytes,
+                      .v_base = static_cast<std::byte *>(p.v) + b * p.v_block_bytes};
+  if (!_states.try_emplace(id, StorageState{.object = obj, .layer = layer}).second)
+    return infer::fail(std::errc::file_exists);
+  p.free.pop_back();
+  _block.emplace(id, b);
+  return id;
+}
+
+int64_t BlockPoolKVStorage::block_of(StorageId id) const {
+  auto it = _block.find(id);
+  return it == _block.end() ? -1 : static_cast<int64_t>(it->second);
+}
+
+infer::expected<void, std::error_code> BlockPoolKVStorage::prepare_object(
+    const KVObjectAccessRequest &req) {
+  if (req.layer >= _pools.size() || !_states.contains(req.id))
+    return infer::fail(std::errc::invalid_argument);
+  return {};
+}
+
+void BlockPoolKVStorage::destroy_object(StorageId id) noexcept {
+  auto st = _states.find(id);
+  auto it = _block.find(id);
+  if (st == _states.end() || it == _block.end()) return;
+  _pools[st->second.layer].free.push_back(it->second);
+  _block.erase(it);
+}

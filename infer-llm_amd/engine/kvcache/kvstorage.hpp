@@ -92,3 +92,47 @@ class NaiveKVStorage : public KVStorage {
   infer::expected<void, std::error_code> prepare_object(const KVObjectAccessRequest &req) override;
   void destroy_object(StorageId id) noexcept override;
 };
+
+// Paged storage: per layer one backend allocation holding a K pool and a V
+// pool of `blocks_per_layer` blocks of `block_tokens` token rows each
+// ([blocks][block_tokens][n_kv_heads][head_dim] per pool), sized once for
+// the device (an MI355X holds 288 GB of HBM). alloc() hands out one block as
+// one storage object (capacity_tokens == block_tokens) from the layer's free
+// list; destroying the object returns the block. No backend call per block.
+class BlockPoolKVStorage : public KVStorage {
+ public:
+  BlockPoolKVStorage(std::size_t blocks_per_layer, std::size_t block_tokens) noexcept
+      : _blocks(blocks_per_layer), _block_tokens(block_tokens) {}
+  ~BlockPoolKVStorage() override;
+  infer::expected<void, std::error_code> init(std::span<const KVLayerSpec> layers,
+                                              std::span<Backend *const> backend_layer) override;
+  infer::expected<StorageId, std::error_code> alloc(std::size_t layer,
+                                                   std::size_t capacity_tokens) override;
+
+  std::size_t block_tokens() const { return _block_tokens; }
+  std::size_t blocks_per_layer() const { return _blocks; }
+  std::size_t free_blocks(std::size_t layer) const {
+    return layer < _pools.size() ? _pools[layer].free.size() : 0;
+  }
+  void *k_pool(std::size_t layer) const { return layer < _pools.size() ? _pools[layer].k : nullptr; }
+  void *v_pool(std::size_t layer) const { return layer < _pools.size() ? _pools[layer].v : nullptr; }
+  // Pool block of an object, or -1 for an unknown id.
+  int64_t block_of(StorageId id) const;
+
+ protected:
+  infer::expected<void, std::error_code> prepare_object(const KVObjectAccessRequest &req) override;
+  void destroy_object(StorageId id) noexcept override;
+
+ private:
+  struct Pool {
+    void *base = nullptr;  // the allocation: K pool, then V pool
+    void *k = nullptr;
+    void *v = nullptr;
+    std::size_t k_block_bytes = 0, v_block_bytes = 0;
+    std::vector<std::size_t> free;  // block indices, taken from the back
+  };
+  std::size_t _blocks, _block_tokens;
+  std::vector<Pool> _pools;
+  std::unordered_map<StorageId, std::size_t> _block;  // object -> pool block
+};
+

@@ -1,7 +1,10 @@
 #include "kvstrategy.hpp"
 
+#include <algorithm>
 #include <cstddef>
+#include <cstdint>
 #include <limits>
+#include <string>
 
 infer::expected<KVLayerAccess, std::error_code> KVStrategy::acquire_layer(SequenceId id,
                                                                           std::size_t layer,
@@ -35,6 +38,7 @@ infer::expected<KVLayerAccess, std::error_code> KVStrategy::acquire_layer(Sequen
   access.readable = std::move(*readable);
   access.writable = std::move(*writable);
   if (!objects.empty()) access.backend = objects.begin()->second.backend;
+  describe(access, id, layer);
   return access;
 }
 
@@ -50,6 +54,7 @@ infer::expected<void, std::error_code> KVStrategy::release_layer(KVLayerAccess &
   access.writable.v.clear();
   access.backend = nullptr;
   access.n_past = access.n_new = 0;
+  access.pages = KVPages{};
   return {};
 }
 
@@ -213,3 +218,191 @@ infer::expected<void, std::error_code> ContiguousKVStrategy::clear_sequence() {
   _sequences.clear();
   return {};
 }
+
+// ---------------------------------------------------------------------------
+// PagedKVStrategy
+
+PagedKVStrategy::PagedKVStrategy(std::unique_ptr<BlockPoolKVStorage> storage) noexcept
+    : KVStrategy(std::move(storage)) {
+  _pool = static_cast<BlockPoolKVStorage *>(_storage.get());
+}
+
+PagedKVStrategy::~PagedKVStrategy() {
+  for (auto &[id, layers] : _sequences) drop(layers);
+}
+
+void PagedKVStrategy::drop(std::vector<Layer> &layers) noexcept {
+  for (std::size_t l = 0; l < layers.size(); ++l) {
+    for (StorageId sid : layers[l].blocks) _storage->free(sid);
+    layers[l].blocks.clear();
+    if (layers[l].device_table && layers[l].device_table->data && l < _backend_layer.size())
+      _backend_layer[l]->free(BufferKind::KVCACHE, layers[l].device_table->data);
+    layers[l].device_table.reset();
+  }
+}
+
+infer::expected<void, std::error_code> PagedKVStrategy::init(std::span<const KVLayerSpec> layers,
+                                                            std::span<Backend *const> backend_layer,
+                                                            const KVCacheConfig &config) {
+  if (!_pool || layers.size() != backend_layer.size() || config.layers != layers.size() ||
+      config.block_tokens == 0 || config.block_tokens != _pool->block_tokens() ||
+      config.max_tokens_per_sequence == 0)
+    return infer::fail(std::errc::invalid_argument);
+  const std::size_t max_blocks =
+      (config.max_tokens_per_sequence + config.block_tokens - 1) / config.block_tokens;
+  if (max_blocks > static_cast<std::size_t>(INT32_MAX)) return infer::fail(std::errc::value_too_large);
+  auto r = _storage->init(layers, backend_layer);
+  if (!r) return infer::unexpected(r.error());
+  _layers.assign(layers.begin(), layers.end());
+  _backend_layer.assign(backend_layer.begin(), backend_layer.end());
+  _cfg = config;
+  _max_blocks = max_blocks;
+  return {};
+}
+
+infer::expected<void, std::error_code> PagedKVStrategy::create_sequence(SequenceId id) {
+  if (id == kInvalidSequenceId) return infer::fail(std::errc::invalid_argument);
+  if (_sequences.contains(id)) return infer::fail(std::errc::file_exists);
+  std::vector<Layer> layers(_cfg.layers);
+  for (std::size_t l = 0; l < _cfg.layers; ++l) {
+    Backend *backend = _backend_layer[l];
+    auto mem = backend->alloc(BufferKind::KVCACHE, _max_blocks * sizeof(int32_t));
+    if (!mem) {
+      drop(layers);
+      return infer::unexpected(mem.error());
+    }
+    auto t = std::make_unique<Tensor>("kv_block_table_" + std::to_string(l), GGML_TYPE_I32,
+                                      std::initializer_list<int64_t>{static_cast<int64_t>(_max_blocks)});
+    t->data = *mem;
+    t->backend = backend;
+    t->device = backend->device_type();
+    t->tensorRole = TensorRole::TENSOR_ROLE_KVCACHE;
+    layers[l].device_table = std::move(t);
+  }
+  _sequences.emplace(id, std::move(layers));
+  return {};
+}
+
+infer::expected<void, std::error_code> PagedKVStrategy::reserve_append(SequenceId id,
+                                                                      TokenRange range) {
+  auto it = _sequences.find(id);
+  if (id == kInvalidSequenceId || it == _sequences.end()) return infer::fail(std::errc::invalid_argument);
+  if (!fits(range)) return infer::fail(std::errc::not_enough_memory);
+  const std::size_t bt = _cfg.block_tokens;
+  const std::size_t need = (range.end() + bt - 1) / bt;
+  std::vector<Layer> &layers = it->second;
+  // Take every new block first, so that running out of pool leaves the
+  // sequence as it was.
+  std::vector<std::vector<StorageId>> fresh(layers.size());
+  auto undo = [&]() noexcept {
+    for (auto &v : fresh)
+      for (StorageId sid : v) _storage->free(sid);
+  };
+  for (std::size_t l = 0; l < layers.size(); ++l) {
+    for (std::size_t b = layers[l].blocks.size(); b < need; ++b) {
+      auto sid = _pool->alloc(l, bt);
+      if (!sid) {
+        undo();
+        return infer::unexpected(sid.error());
+      }
+      fresh[l].push_back(*sid);
+    }
+  }
+  for (std::size_t l = 0; l < layers.size(); ++l) {
+    if (fresh[l].empty()) continue;
+    Layer &L = layers[l];
+    const std::size_t first = L.blocks.size();
+    for (StorageId sid : fresh[l]) {
+      L.blocks.push_back(sid);
+      L.table.push_back(static_cast<int32_t>(_pool->block_of(sid)));
+    }
+    auto up = _backend_layer[l]->copy_tensor_set(L.device_table.get(), L.table.data() + first,
+                                                 first * sizeof(int32_t),
+                                                 fresh[l].size() * sizeof(int32_t));
+    if (!up) return infer::unexpected(up.error());
+  }
+  return {};
+}
+
+infer::expected<KVMapping, std::error_code> PagedKVStrategy::lookup(SequenceId id,
+                                                                   std::size_t layer,
+                                                                   TokenRange range) const {
+  if (id == kInvalidSequenceId) return infer::fail(std::errc::invalid_argument);
+  auto it = _sequences.find(id);
+  if (it == _sequences.end() || layer >= it->second.size())
+    return infer::fail(std::errc::invalid_argument);
+  if (!fits(range)) return infer::fail(std::errc::not_enough_memory);
+  KVMapping m;
+  if (range.empty()) return m;
+  const std::size_t bt = _cfg.block_tokens;
+  const auto &blocks = it->second[layer].blocks;
+  if ((range.end() + bt - 1) / bt > blocks.size()) return infer::fail(std::errc::invalid_argument);
+  for (std::size_t t = range.begin; t < range.end();) {
+    const std::size_t b = t / bt, off = t - b * bt;
+    const std::size_t n = std::min(bt - off, range.end() - t);
+    const KVSlice slice{.storage_id = blocks[b], .token_offset = off, .token_count = n};
+    m.k.push_back(slice);
+    m.v.push_back(slice);
+    t += n;
+  }
+  return m;
+}
+
+void PagedKVStrategy::describe(KVLayerAccess &access, SequenceId id, std::size_t layer) const {
+  auto it = _sequences.find(id);
+  if (it == _sequences.end() || layer >= it->second.size()) return;
+  access.pages = KVPages{.block_table = it->second[layer].device_table.get(),
+                         .block_tokens = _cfg.block_tokens,
+                         .pool_blocks = _pool->blocks_per_layer(),
+                         .k_pool = _pool->k_pool(layer),
+                         .v_pool = _pool->v_pool(layer)};
+}
+
+infer::expected<void, std::error_code> PagedKVStrategy::commit_append(SequenceId id,
+                                                                     TokenRange range) {
+  if (!_sequences.contains(id)) return infer::fail(std::errc::invalid_argument);
+  if (!fits(range)) return infer::fail(std::errc::not_enough_memory);
+  return {};
+}
+
+infer::expected<void, std::error_code> PagedKVStrategy::abort_append(SequenceId id,
+                                                                    TokenRange range) {
+  auto it = _sequences.find(id);
+  if (it == _sequences.end()) return infer::fail(std::errc::invalid_argument);
+  if (!fits(range)) return infer::fail(std::errc::not_enough_memory);
+  // Blocks past the one holding the last committed token go back to the pool
+  // (an object still in use is returned by its last release).
+  const std::size_t bt = _cfg.block_tokens;
+  const std::size_t keep = (range.begin + bt - 1) / bt;
+  for (Layer &L : it->second) {
+    while (L.blocks.size() > keep) {
+      _storage->free(L.blocks.back());
+      L.blocks.pop_back();
+      L.table.pop_back();
+    }
+  }
+  return {};
+}
+
+infer::expected<void, std::error_code> PagedKVStrategy::release_sequence(SequenceId id) {
+  auto it = _sequences.find(id);
+  if (it == _sequences.end()) return infer::fail(std::errc::invalid_argument);
+  drop(it->second);
+  _sequences.erase(it);
+  return {};
+}
+
+infer::expected<void, std::error_code> PagedKVStrategy::clear_sequence() {
+  for (auto &[id, layers] : _sequences) drop(layers);
+  _sequences.clear();
+  return {};
+}
+
+std::vector<int64_t> PagedKVStrategy::blocks(SequenceId id, std::size_t layer) const {
+  std::vector<int64_t> out;
+  auto it = _sequences.find(id);
+  if (it == _sequences.end() || layer >= it->second.size()) return out;
+  for (StorageId sid : it->second[layer].blocks) out.push_back(_pool->block_of(sid));
+  return out;
+}
+

@@ -45,6 +45,10 @@ class KVStrategy {
   KVStorage *storage() const { return _storage.get(); }
 
  protected:
+  // Lets a strategy attach what its kernels need beyond the views (a paged
+  // strategy's block table) to an access it has built.
+  virtual void describe(KVLayerAccess &, SequenceId, std::size_t) const {}
+
   virtual infer::expected<KVMapping, std::error_code> lookup(SequenceId id, std::size_t layer,
                                                              TokenRange range) const = 0;
   infer::expected<KVRangeAccess, std::error_code> make_KVRangeAccess(
@@ -84,3 +88,52 @@ class ContiguousKVStrategy : public KVStrategy {
   }
   std::unordered_map<SequenceId, std::vector<StorageId>> _sequences;  // index = layer
 };
+
+// Paged strategy (KVCacheConfig::block_tokens > 0) over a BlockPoolKVStorage:
+// a sequence's layer is a list of pool blocks, grown by reserve_append,
+// trimmed by abort_append to the blocks that hold committed tokens, and
+// returned by release_sequence. lookup() yields one slice per block touched,
+// and every access carries the sequence's device block table (one int32 per
+// block, kept on the layer's backend and updated only when blocks are added),
+// so the attention kernels follow the blocks without a per-step upload.
+class PagedKVStrategy : public KVStrategy {
+ public:
+  explicit PagedKVStrategy(std::unique_ptr<BlockPoolKVStorage> storage) noexcept;
+  ~PagedKVStrategy() override;
+
+  infer::expected<void, std::error_code> init(std::span<const KVLayerSpec> layers,
+                                              std::span<Backend *const> backend_layer,
+                                              const KVCacheConfig &config) override;
+  infer::expected<void, std::error_code> create_sequence(SequenceId id) override;
+  infer::expected<void, std::error_code> reserve_append(SequenceId id, TokenRange range) override;
+  infer::expected<void, std::error_code> commit_append(SequenceId id, TokenRange range) override;
+  infer::expected<void, std::error_code> abort_append(SequenceId id, TokenRange range) override;
+  infer::expected<void, std::error_code> release_sequence(SequenceId id) override;
+  infer::expected<void, std::error_code> clear_sequence() override;
+
+  // Pool blocks of (sequence, layer), in token order (tests, tools).
+  std::vector<int64_t> blocks(SequenceId id, std::size_t layer) const;
+
+ protected:
+  infer::expected<KVMapping, std::error_code> lookup(SequenceId id, std::size_t layer,
+                                                     TokenRange range) const override;
+  void describe(KVLayerAccess &access, SequenceId id, std::size_t layer) const override;
+
+ private:
+  struct Layer {
+    std::vector<StorageId> blocks;
+    std::vector<int32_t> table;            // host mirror of the device table
+    std::unique_ptr<Tensor> device_table;  // I32 [max_blocks] on the layer's backend
+  };
+  bool fits(TokenRange r) const {
+    const auto cap = _cfg.max_tokens_per_sequence;
+    return r.begin <= cap && r.count <= cap - r.begin;
+  }
+  void drop(std::vector<Layer> &layers) noexcept;
+
+  BlockPoolKVStorage *_pool;
+  std::vector<Backend *> _backend_layer;
+  std::size_t _max_blocks = 0;
+  std::unordered_map<SequenceId, std::vector<Layer>> _sequences;
+};
+

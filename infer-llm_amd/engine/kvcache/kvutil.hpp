@@ -61,6 +61,20 @@ struct KVSegmentView {
   std::size_t token_count = 0;
 };
 
+// A paged layer as one kernel sees it: the layer's K and V block pools
+// ([pool_blocks * block_tokens][n_kv_heads][head_dim] each) and the
+// sequence's device block table (entry i = pool block of tokens
+// [i * block_tokens, (i + 1) * block_tokens)). The readable and writable
+// segments of the access are the same rows, one segment per block.
+struct KVPages {
+  Tensor *block_table = nullptr;  // I32 [entries], device; owned by the strategy
+  std::size_t block_tokens = 0;
+  std::size_t pool_blocks = 0;
+  void *k_pool = nullptr;
+  void *v_pool = nullptr;
+  explicit operator bool() const noexcept { return block_table != nullptr; }
+};
+
 struct KVRangeAccess {
   std::vector<KVSegmentView> k;
   std::vector<KVSegmentView> v;
@@ -86,7 +100,8 @@ struct KVLayerAccess {
         n_past(std::exchange(o.n_past, 0)),
         n_new(std::exchange(o.n_new, 0)),
         readable(std::move(o.readable)),
-        writable(std::move(o.writable)) {
+        writable(std::move(o.writable)),
+        pages(std::exchange(o.pages, KVPages{})) {
     o._storage_ids.clear();
     o.readable.k.clear();
     o.readable.v.clear();
@@ -103,4 +118,6 @@ struct KVLayerAccess {
   std::size_t n_new = 0;
   KVRangeAccess readable;
   KVRangeAccess writable;
+  // Set by a paged strategy (block_tokens > 0); empty for contiguous storage.
+  KVPages pages;
 };

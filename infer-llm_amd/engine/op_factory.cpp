@@ -118,6 +118,42 @@ Tensor *append_kv(Graph &g, Tensor *current, const Tensor &writable, const Tenso
   return g.add_node(std::move(full));
 }
 
+Tensor *append_kv_paged(Graph &g, Tensor *current, const KVPages &pages, void *pool,
+                        const Tensor &readable, std::size_t n_past) {
+  // CPY: the step's rows into their pool blocks (first logical token n_past);
+  // VIEW: logical rows [0, n_kv) of the pool. Both carry the block table as
+  // src[1] and (block_tokens, pool blocks, first token) in op_params.
+  auto tag = [&](Tensor &t) {
+    t.data = pool;
+    t.offset = 0;
+    t.layer = readable.layer;
+    t.backend = readable.backend;
+    t.device = readable.device;
+    t.tensorRole = TensorRole::TENSOR_ROLE_KVCACHE;
+    t.pinned = true;
+    t.op_params[0] = static_cast<int32_t>(pages.block_tokens);
+    t.op_params[1] = static_cast<int32_t>(pages.pool_blocks);
+    t.op_params[2] = static_cast<int32_t>(n_past);
+  };
+  auto write = std::make_unique<Tensor>(current->name + "_cache_write", current->dataType,
+                                        std::initializer_list<int64_t>{current->dims[0], current->dims[1],
+                                                                       current->dims[2], 1});
+  write->op = OperationType::GGML_OP_CPY;
+  tag(*write);
+  write->src[0] = current;
+  write->src[1] = pages.block_table;
+  Tensor *write_node = g.add_node(std::move(write));
+
+  auto full = std::make_unique<Tensor>(current->name + "_cache_full", readable.dataType,
+                                       std::initializer_list<int64_t>{readable.dims[0], readable.dims[1],
+                                                                      readable.dims[2], 1});
+  full->op = OperationType::GGML_OP_VIEW;
+  tag(*full);
+  full->src[0] = write_node;
+  full->src[1] = pages.block_table;
+  return g.add_node(std::move(full));
+}
+
 infer::expected<Tensor *, std::error_code> build_attention_slice(
     Graph &g, GraphContext &ctx, Tensor *q_proj, Tensor *k_proj, Tensor *v_proj, Tensor *q_norm_w,
     Tensor *k_norm_w, std::size_t layer, const AttentionSliceParams &p) {
@@ -151,7 +187,18 @@ infer::expected<Tensor *, std::error_code> build_attention_slice(
   ap.n_ctx = static_cast<uint32_t>(a.n_past);
   ap.sliding_window = 0;
 
-  Tensor *k_cached = append_kv(g, kr, a.writable.k.front().view, a.readable.k.front().view);
-  Tensor *v_cached = append_kv(g, v, a.writable.v.front().view, a.readable.v.front().view);
+  Tensor *k_cached, *v_cached;
+  if (a.pages) {
+    // Paged cache: the views span several blocks, so the append and the
+    // attention read the pools through the sequence's block table. The
+    // logical view keeps the dims [head_dim, n_kv_heads, n_kv, 1].
+    Tensor rk = a.readable.k.front().view, rv = a.readable.v.front().view;
+    rk.dims[2] = rv.dims[2] = static_cast<int64_t>(a.n_past + a.n_new);
+    k_cached = append_kv_paged(g, kr, a.pages, a.pages.k_pool, rk, a.n_past);
+    v_cached = append_kv_paged(g, v, a.pages, a.pages.v_pool, rv, a.n_past);
+  } else {
+    k_cached = append_kv(g, kr, a.writable.k.front().view, a.readable.k.front().view);
+    v_cached = append_kv(g, v, a.writable.v.front().view, a.readable.v.front().view);
+  }
   return OpFactory::flash_attn(g, qr, k_cached, v_cached, ap, "flash_attn_" + l);
 }

@@ -43,6 +43,12 @@ struct OpFactory {
 // then a VIEW node of the readable view [0, n_past + n_new) whose src[0] is
 // the CPY, so consumers of the view run after the append.
 Tensor *append_kv(Graph &g, Tensor *current, const Tensor &writable, const Tensor &readable);
+// The same pair for a paged layer: a CPY of `current` into its pool blocks
+// and a VIEW of logical rows [0, readable.dims[2]) of the pool, each with the
+// block table as src[1] and (block_tokens, pool blocks, first token) in
+// op_params[0..2].
+Tensor *append_kv_paged(Graph &g, Tensor *current, const KVPages &pages, void *pool,
+                        const Tensor &readable, std::size_t n_past);
 
 struct AttentionSliceParams {
   uint32_t n_head = 16;

@@ -163,8 +163,13 @@ infer::expected<Graph, std::error_code> Qwen3Model::build_graph(GraphContext &ct
 // ---------------------------------------------------------------------------
 // runner
 
-Qwen3Runner::Qwen3Runner(Qwen3Model &model, HIPBackend &backend, size_t capacity)
-    : _model(model), _backend(backend), _capacity(capacity) {}
+Qwen3Runner::Qwen3Runner(Qwen3Model &model, HIPBackend &backend, size_t capacity,
+                         size_t block_tokens, size_t pool_blocks)
+    : _model(model),
+      _backend(backend),
+      _capacity(capacity),
+      _block_tokens(block_tokens),
+      _pool_blocks(pool_blocks) {}
 
 Qwen3Runner::~Qwen3Runner() {
   (void)_backend.synchronize();
@@ -181,12 +186,18 @@ infer::expected<void, std::error_code> Qwen3Runner::init() {
   const Qwen3Hparams &hp = _model.hparams();
   std::vector<KVLayerSpec> specs(hp.n_layer, KVLayerSpec{hp.n_head_kv, hp.head_dim, hp.head_dim});
   std::vector<Backend *> place(hp.n_layer, &_backend);
-  _kv = std::make_unique<KVCacheManager>(
-      std::make_unique<ContiguousKVStrategy>(std::make_unique<NaiveKVStorage>()));
-  if (auto r = _kv->init(specs, place,
-                         KVCacheConfig{.layers = hp.n_layer, .max_tokens_per_sequence = _capacity});
-      !r)
-    return r;
+  KVCacheConfig cfg{.layers = hp.n_layer, .max_tokens_per_sequence = _capacity};
+  if (_block_tokens > 0) {
+    const size_t blocks =
+        _pool_blocks ? _pool_blocks : (_capacity + _block_tokens - 1) / _block_tokens;
+    cfg.block_tokens = _block_tokens;
+    _kv = std::make_unique<KVCacheManager>(std::make_unique<PagedKVStrategy>(
+        std::make_unique<BlockPoolKVStorage>(blocks, _block_tokens)));
+  } else {
+    _kv = std::make_unique<KVCacheManager>(
+        std::make_unique<ContiguousKVStrategy>(std::make_unique<NaiveKVStorage>()));
+  }
+  if (auto r = _kv->init(specs, place, cfg); !r) return r;
   if (auto r = _backend.reserve_decode_workspace(int(hp.n_head), int(hp.n_head_kv), int(hp.head_dim),
                                                  int64_t(_capacity));
       !r)

@@ -102,7 +102,11 @@ struct GenerationTiming {
 
 class Qwen3Runner {
  public:
-  Qwen3Runner(Qwen3Model &model, HIPBackend &backend, size_t capacity);
+  // block_tokens > 0 keeps the KV cache paged (PagedKVStrategy over a
+  // BlockPoolKVStorage of pool_blocks blocks per layer; 0 = enough for one
+  // sequence of `capacity` tokens); 0 keeps one contiguous cache per layer.
+  Qwen3Runner(Qwen3Model &model, HIPBackend &backend, size_t capacity, size_t block_tokens = 0,
+              size_t pool_blocks = 0);
   ~Qwen3Runner();
   infer::expected<void, std::error_code> init();
   // prompt, then n_gen greedy tokens (the first from the prompt's last
@@ -121,6 +125,7 @@ class Qwen3Runner {
   Qwen3Model &_model;
   HIPBackend &_backend;
   size_t _capacity;
+  size_t _block_tokens, _pool_blocks;
   std::unique_ptr<KVCacheManager> _kv;
   std::unique_ptr<Scheduler> _sched;
   std::unique_ptr<GraphContext> _ctx;

@@ -54,6 +54,8 @@ _P = ctypes.c_void_p
 ENGINE_SIGNATURES = {
     "ikv_qwen3_create": (ctypes.c_int, [ctypes.POINTER(_Config), ctypes.c_int, ctypes.c_int64,
                                         ctypes.POINTER(_P)]),
+    "ikv_qwen3_create_paged": (ctypes.c_int, [ctypes.POINTER(_Config), ctypes.c_int, ctypes.c_int64,
+                                              ctypes.c_int64, ctypes.c_int64, ctypes.POINTER(_P)]),
     "ikv_qwen3_tensor_count": (ctypes.c_int, [_P]),
     "ikv_qwen3_tensor_name": (ctypes.c_char_p, [_P, ctypes.c_int]),
     "ikv_qwen3_tensor_size": (ctypes.c_size_t, [_P, ctypes.c_char_p]),
@@ -111,14 +113,22 @@ def synthetic_weights(cfg: Qwen3Config, seed: int, std: float = 0.02, threads: i
 
 
 class Qwen3Engine:
-    """A Qwen3 model on HIP device `device` with a KV cache of max_ctx tokens."""
+    """A Qwen3 model on HIP device `device` with a KV cache of max_ctx tokens:
+    one contiguous cache per layer, or with block_tokens > 0 a paged cache
+    (pool_blocks blocks of block_tokens tokens per layer; 0 = max_ctx worth)."""
 
-    def __init__(self, cfg: Qwen3Config, max_ctx: int, device: int = 0):
+    def __init__(self, cfg: Qwen3Config, max_ctx: int, device: int = 0, block_tokens: int = 0,
+                 pool_blocks: int = 0):
         self.cfg = cfg
         c = _Config(*(getattr(cfg, f) for f, _ in _Config._fields_))
         h = _P()
-        _check("ikv_qwen3_create", _lib().ikv_qwen3_create(ctypes.byref(c), device, max_ctx,
-                                                           ctypes.byref(h)))
+        if block_tokens:
+            _check("ikv_qwen3_create_paged",
+                   _lib().ikv_qwen3_create_paged(ctypes.byref(c), device, max_ctx, block_tokens,
+                                                 pool_blocks, ctypes.byref(h)))
+        else:
+            _check("ikv_qwen3_create", _lib().ikv_qwen3_create(ctypes.byref(c), device, max_ctx,
+                                                               ctypes.byref(h)))
         self._h = h
 
     def close(self):

@@ -100,6 +100,8 @@ struct Rng {
 // ---------------------------------------------------------------------------
 // CPU checks
 
+static void paged_cpu_tests();
+
 static void cpu_tests() {
   {
     infer::expected<int, std::error_code> a = 5;
@@ -230,6 +232,91 @@ static void cpu_tests() {
               g.nodes()[1]->data == cache_w.data && view->data == cache_r.data && g.leafs().size() == 2,
           "graph topo order; append_kv = CPY then VIEW over the cache");
   }
+  paged_cpu_tests();
+}
+
+// Paged strategy over a block pool (KVCacheConfig::block_tokens > 0): block
+// lists, slices per block, the device block table, pool exhaustion with
+// rollback, abort trimming, reuse of returned blocks.
+static void paged_cpu_tests() {
+  HostBackend be;
+  const size_t L = 2, bt = 64, nb = 6, row = 8 * 128 * 4;
+  std::vector<KVLayerSpec> specs(L, KVLayerSpec{8, 128, 128, GGML_TYPE_F32, GGML_TYPE_F32});
+  std::vector<Backend *> place(L, &be);
+  {
+    auto bad = KVCacheManager(std::make_unique<PagedKVStrategy>(std::make_unique<BlockPoolKVStorage>(nb, bt)))
+                   .init(specs, place, KVCacheConfig{.layers = L, .max_tokens_per_sequence = 320, .block_tokens = 32});
+    CHECK(!bad && is_err(bad.error(), std::errc::invalid_argument), "paged init: block size must match the pool");
+  }
+  auto pool_owner = std::make_unique<BlockPoolKVStorage>(nb, bt);
+  BlockPoolKVStorage *pool = pool_owner.get();
+  auto strat_owner = std::make_unique<PagedKVStrategy>(std::move(pool_owner));
+  PagedKVStrategy *strat = strat_owner.get();
+  KVCacheManager kv(std::move(strat_owner));
+  const int allocs0 = be.allocs;
+  CHECK(kv.init(specs, place, KVCacheConfig{.layers = L, .max_tokens_per_sequence = 320, .block_tokens = bt}) &&
+            be.allocs == allocs0 + int(L) && pool->free_blocks(0) == nb && pool->k_pool(1) != nullptr,
+        "paged init: one pool allocation per layer");
+  auto a = kv.create_sequence();
+  CHECK(a && pool->free_blocks(0) == nb, "create_sequence takes no block");
+  CHECK(kv.reserve_append(*a, 100) && strat->blocks(*a, 0) == std::vector<int64_t>({0, 1}) &&
+            strat->blocks(*a, 1) == std::vector<int64_t>({0, 1}) && pool->free_blocks(0) == nb - 2,
+        "reserve 100 tokens: two blocks per layer");
+  {
+    auto acc = kv.acquire_layer(*a, 0);
+    bool ok = bool(acc) && acc->readable.k.size() == 2 && acc->writable.k.size() == 2 && acc->pages;
+    if (ok) {
+      const auto &r = acc->readable.k;
+      const char *kp = static_cast<const char *>(acc->pages.k_pool);
+      ok = r[0].token_begin == 0 && r[0].token_count == 64 && r[1].token_begin == 64 &&
+           r[1].token_count == 36 && r[0].view.data == kp && r[1].view.data == kp + bt * row &&
+           acc->pages.block_tokens == bt && acc->pages.pool_blocks == nb &&
+           static_cast<const int32_t *>(acc->pages.block_table->data)[1] == 1;
+      CHECK(ok, "paged access: one segment per block, pool addresses, device table");
+      (void)kv.release_layer(*acc);
+    } else {
+      CHECK(false, "paged access: one segment per block, pool addresses, device table");
+    }
+  }
+  CHECK(kv.commit_append(*a) && kv.reserve_append(*a, 1) && strat->blocks(*a, 0).size() == 2, "decode step within a block");
+  {
+    auto acc = kv.acquire_layer(*a, 1);
+    CHECK(acc && acc->writable.k.size() == 1 && acc->writable.k[0].token_begin == 100 &&
+              acc->writable.k[0].view.data == static_cast<char *>(acc->pages.k_pool) + (bt + 36) * row,
+          "decode write slice lands at block 1 offset 36");
+    if (acc) (void)kv.release_layer(*acc);
+  }
+  CHECK(kv.commit_append(*a), "commit");
+  auto b = kv.create_sequence();
+  CHECK(b && kv.reserve_append(*b, 200) && strat->blocks(*b, 0) == std::vector<int64_t>({2, 3, 4, 5}) &&
+            pool->free_blocks(0) == 0,
+        "second sequence takes the remaining four blocks");
+  auto exhausted = kv.reserve_append(*a, 100);
+  CHECK(!exhausted && is_err(exhausted.error(), std::errc::not_enough_memory), "pool exhausted: reserve fails");
+  CHECK(strat->blocks(*a, 0).size() == 2 && strat->blocks(*a, 1).size() == 2 && pool->free_blocks(1) == 0,
+        "failed reserve leaves the sequence and the pool as they were");
+  CHECK(kv.abort_append(*b) && pool->free_blocks(0) == 4 && strat->blocks(*b, 0).empty(),
+        "abort returns the blocks that hold no committed token");
+  CHECK(kv.reserve_append(*a, 100) && strat->blocks(*a, 0) == std::vector<int64_t>({0, 1, 2, 3}),
+        "returned blocks are reused");
+  {
+    auto acc = kv.acquire_layer(*a, 0);
+    const int32_t *tab = acc ? static_cast<const int32_t *>(acc->pages.block_table->data) : nullptr;
+    CHECK(acc && tab && tab[0] == 0 && tab[1] == 1 && tab[2] == 2 && tab[3] == 3 && acc->writable.k.size() == 3 &&
+              acc->writable.k[0].token_count == 27 && acc->writable.k[2].token_count == 9,
+          "device table updated for the new blocks; tokens 101..200 span three blocks");
+    if (acc) (void)kv.release_layer(*acc);
+  }
+  CHECK(kv.commit_append(*a) && kv.release_sequence(*a) && pool->free_blocks(0) == nb, "release returns every block");
+  auto c = kv.create_sequence();
+  CHECK(c && kv.reserve_append(*c, 128) && strat->blocks(*c, 0) == std::vector<int64_t>({3, 2}),
+        "a new sequence gets the last returned blocks first (non-identity table)");
+  auto over = kv.reserve_append(*c, 321);
+  CHECK(!over && is_err(over.error(), std::errc::device_or_resource_busy), "one pending append per sequence");
+  CHECK(kv.abort_append(*c) && pool->free_blocks(0) == 6, "abort at length 0 frees all");
+  auto big = kv.reserve_append(*c, 321);
+  CHECK(!big && is_err(big.error(), std::errc::not_enough_memory), "beyond max_tokens_per_sequence");
+  CHECK(kv.clear_sequence() && pool->free_blocks(0) == nb && pool->free_blocks(1) == nb, "clear returns all blocks");
 }
 
 // ---------------------------------------------------------------------------

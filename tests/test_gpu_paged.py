@@ -189,3 +189,47 @@ def test_bad_block_entry_is_flagged_not_faulted(dev):
     ikv.attn_decode_paged(q, kp, vp, good, bt, n_kv, status=status)
     torch.cuda.synchronize()
     assert int(status.cpu()[0]) == 0
+
+
+# ---------------------------------------------------------------------------
+# the whole model on a paged cache
+# ---------------------------------------------------------------------------
+
+def test_paged_engine_matches_contiguous_and_oracle(dev, oracle_pool):
+    from ikv import qwen3
+    cfg = qwen3.Qwen3Config(n_layer=3, n_vocab=8192, n_ctx_train=4096)
+    w = qwen3.synthetic_weights(cfg, synth.config_seed(0, 20))
+    p1 = synth.uniform_ints(synth.config_seed(0, 21), 100, cfg.n_vocab)  # prefill over two blocks
+    p2 = synth.uniform_ints(synth.config_seed(0, 22), 7, cfg.n_vocab)
+    flat = qwen3.Qwen3Engine(cfg, 256)
+    flat.set_weights(w)
+    paged = qwen3.Qwen3Engine(cfg, 256, block_tokens=64)
+    paged.set_weights(w)
+    a1 = flat.generate(p1, 60)[0]
+    b1 = paged.generate(p1, 60)[0]          # 159 tokens: three blocks per layer
+    st = paged.last_stats()
+    assert b1 == a1
+    assert st["fused_rope_decode"] == cfg.n_layer and st["fused_append_decode"] == cfg.n_layer
+    # the next sequence gets the returned blocks in reverse order: a
+    # non-identity block table, same tokens
+    a2 = flat.generate(p2, 150)[0]
+    b2 = paged.generate(p2, 150)[0]
+    assert b2 == a2
+    assert a2 == oracle.Qwen3Oracle(cfg, w, 256).generate(p2, 150)
+    # every node on its own (unfused paged append, paged decode, paged prefill)
+    paged.set_fusion(False)
+    assert paged.generate(p1, 60)[0] == a1
+    flat.close()
+    paged.close()
+
+
+def test_paged_engine_pool_too_small_fails_cleanly(dev):
+    from ikv import qwen3
+    cfg = qwen3.Qwen3Config(n_layer=2, n_vocab=4096, n_ctx_train=4096)
+    eng = qwen3.Qwen3Engine(cfg, 512, block_tokens=64, pool_blocks=2)  # 128 tokens per layer
+    eng.init_synthetic(3)
+    assert len(eng.generate(list(range(1, 60)), 40)[0]) == 40       # 98 tokens fit
+    with pytest.raises(ikv.IkvError):
+        eng.generate(list(range(1, 100)), 40)                        # 138 do not
+    assert len(eng.generate(list(range(1, 60)), 40)[0]) == 40       # blocks came back
+    eng.close()
