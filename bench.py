@@ -62,9 +62,11 @@ def prefill_flops(p, n_head=N_HEAD, d=D):
 class DecodeRig:
     """28 layers of KV cache at one context length, launched through the C-ABI."""
 
-    def __init__(self, torch, ikv, ctx, n_layer=N_LAYER, seed=0x1F0000 + 1000 + 2, n_head=N_HEAD):
+    def __init__(self, torch, ikv, ctx, n_layer=N_LAYER, seed=0x1F0000 + 1000 + 2, n_head=N_HEAD,
+                 block_tokens=0):
         self.torch, self.ikv, self.ctx, self.n_layer = torch, ikv, ctx, n_layer
         self.n_head = n_head
+        self.block_tokens = block_tokens  # > 0: paged pools with a shuffled block table
         dev = torch.device("cuda:0")
         g = torch.Generator(device=dev)
         g.manual_seed(seed)
@@ -80,6 +82,22 @@ class DecodeRig:
                 kn=torch.randn((N_HEAD_KV, D), generator=g, device=dev),
                 vn=torch.randn((N_HEAD_KV, D), generator=g, device=dev),
                 out=torch.empty((n_head, D), device=dev)))
+        if block_tokens:
+            import numpy as np
+            n_blocks = (ctx + 1 + block_tokens - 1) // block_tokens
+            rng = np.random.default_rng(seed)
+            for L in self.layers:
+                pool_blocks = n_blocks + 4
+                table = rng.permutation(pool_blocks)[:n_blocks].astype(np.int32)
+                L["table"] = torch.tensor(table, device=dev)
+                for name in ("kc", "vc"):
+                    pool = torch.empty((pool_blocks * block_tokens, N_HEAD_KV, D), device=dev)
+                    for b, blk in enumerate(table):
+                        n = min(block_tokens, ctx + 1 - b * block_tokens)
+                        pool[blk * block_tokens:blk * block_tokens + n] = \
+                            L[name][b * block_tokens:b * block_tokens + n]
+                    L[name] = pool
+                L["pages"] = ikv.kv_pages(L["table"], block_tokens, L["kc"])
         self.ws = ikv.decode_workspace(n_head, N_HEAD_KV, D, ctx + 1, device=dev)
         self.ws_bytes = self.ws.numel() * 4
         self.lib = ikv.load()
@@ -87,14 +105,22 @@ class DecodeRig:
 
     def step(self):
         s = self.torch.cuda.current_stream().cuda_stream
-        f = self.lib.ikv_attn_decode_f32
         n_kv = self.ctx + 1
         for L in self.layers:
-            rc = f(L["q"].data_ptr(), L["kc"].data_ptr(), L["vc"].data_ptr(), L["kn"].data_ptr(),
-                   L["vn"].data_ptr(), L["out"].data_ptr(), self.n_head, N_HEAD_KV, D, n_kv, 0.0,
-                   self.ws.data_ptr(), self.ws_bytes, s)
+            if self.block_tokens:
+                import ctypes
+                rc = self.lib.ikv_attn_decode_paged_f32(
+                    L["q"].data_ptr(), L["kc"].data_ptr(), L["vc"].data_ptr(),
+                    ctypes.byref(L["pages"]), L["kn"].data_ptr(), L["vn"].data_ptr(),
+                    L["out"].data_ptr(), self.n_head, N_HEAD_KV, D, n_kv, 0.0, self.ws.data_ptr(),
+                    self.ws_bytes, s)
+            else:
+                rc = self.lib.ikv_attn_decode_f32(
+                    L["q"].data_ptr(), L["kc"].data_ptr(), L["vc"].data_ptr(), L["kn"].data_ptr(),
+                    L["vn"].data_ptr(), L["out"].data_ptr(), self.n_head, N_HEAD_KV, D, n_kv, 0.0,
+                    self.ws.data_ptr(), self.ws_bytes, s)
             if rc != 0:
-                raise RuntimeError(f"ikv_attn_decode_f32 returned {rc}")
+                raise RuntimeError(f"decode returned {rc}")
 
     def capture(self):
         torch = self.torch
@@ -289,11 +315,14 @@ def model_bench(configs, cpu_tokens):
 
     res = {}
     gpu_tokens0 = None
-    for c in configs:
+    runs = [(c, 0) for c in configs]
+    if 3 in configs:
+        runs.append((3, 256))  # config 3 again on a paged cache of 256-token blocks
+    for c, bt in runs:
         arch, P, N = MODEL_CONFIGS[c]
         cfg = getattr(qwen3, arch)
         t0 = time.perf_counter()
-        eng = qwen3.Qwen3Engine(cfg, P + N)
+        eng = qwen3.Qwen3Engine(cfg, P + N, block_tokens=bt)
         eng.init_synthetic(synth.config_seed(c, 1), threads=16)
         init_s = time.perf_counter() - t0
         prompt = synth.uniform_ints(synth.config_seed(c, 0), P, cfg.n_vocab)
@@ -303,7 +332,7 @@ def model_bench(configs, cpu_tokens):
         eng.close()
         if c == 0:
             gpu_tokens0 = toks
-        res[f"config{c}"] = {
+        res[f"config{c}" + (f"_paged{bt}" if bt else "")] = {
             "model": arch.lower().replace("_", "-").replace("-0-6b", "-0.6b"),
             "prompt": P, "generated": N, "ttft_ms": round(t.ttft_s * 1e3, 3),
             "tpot_ms": round(t.tpot_s * 1e3, 4), "decode_tok_s": round(1 / t.tpot_s, 1),
@@ -314,8 +343,8 @@ def model_bench(configs, cpu_tokens):
                                      for _, sh in qwen3.tensor_layout(cfg)) * 4 / 2**30, 2),
             "init_s": round(init_s, 1),
         }
-        log(f"[bench] model config {c} ({arch}, P={P}, N={N}): TTFT {t.ttft_s * 1e3:.2f} ms, "
-            f"TPOT {t.tpot_s * 1e3:.3f} ms")
+        log(f"[bench] model config {c}{f' paged {bt}' if bt else ''} ({arch}, P={P}, N={N}): "
+            f"TTFT {t.ttft_s * 1e3:.2f} ms, TPOT {t.tpot_s * 1e3:.3f} ms")
     if cpu_tokens and 0 in configs:
         import oracle
 
@@ -462,6 +491,7 @@ def main():
             traffic = t.get("hbm_bytes_per_launch")
 
     extra = {"eager_gbs": None, "ctx_sweep_gbs": {}, "short_ctx_us": {}, "g4_ctx4096": None,
+             "paged_ctx4096_gbs": {},
              "mall_hot_gbs": None, "prefill": {}, "hbm_probes": None, "model": None}
     if not args.no_extra:
         rig.graph = None
@@ -485,6 +515,14 @@ def main():
             extra["short_ctx_us"][str(ctx)] = round(s / 50 / N_LAYER * 1e6, 2)
             del r
         log(f"[bench] short contexts, us per layer: {extra['short_ctx_us']}")
+        # the same workload on a paged cache (shuffled block tables)
+        for bt in (64, 256):
+            r = DecodeRig(torch, ikv, args.ctx, block_tokens=bt)
+            r.capture()
+            s = r.time(args.steps, 3)
+            extra["paged_ctx4096_gbs"][str(bt)] = round(bpl * args.steps * N_LAYER / s / 1e9, 1)
+            del r
+        log(f"[bench] paged ctx {args.ctx}, GB/s by block size: {extra['paged_ctx4096_gbs']}")
         # Qwen3-8B layer shape (32 query heads over 8 KV heads, G = 4), 36 layers.
         r = DecodeRig(torch, ikv, 4096, n_layer=36, n_head=32)
         r.capture()

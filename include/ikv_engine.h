@@ -52,6 +52,21 @@ int ikv_qwen3_create(const ikv_qwen3_config *cfg, int device, int64_t max_ctx, i
  * sequence grows and returned when the next generate() starts a new one. */
 int ikv_qwen3_create_paged(const ikv_qwen3_config *cfg, int device, int64_t max_ctx,
                            int64_t block_tokens, int64_t pool_blocks, ikv_qwen3 **out);
+/* The same with the KV cache in the HBM <-> host offload tier (the
+ * reference's OffloadKVStorage, include/kvcache/KVStorages/
+ * offloadKVStorage.hpp): every layer's cache has a pinned host copy, and at
+ * most hbm_bytes of them are resident in HBM; a layer is uploaded when a step
+ * acquires it, and the least recently used layer is written back and
+ * dropped to make room. Tokens are those of the all-HBM cache. */
+int ikv_qwen3_create_offload(const ikv_qwen3_config *cfg, int device, int64_t max_ctx,
+                             uint64_t hbm_bytes, ikv_qwen3 **out);
+
+/* Page-ins (host -> HBM), page-outs (write-backs), evictions and bytes moved
+ * by an offloaded cache since creation (zeros for the other caches). */
+typedef struct ikv_qwen3_kv_counters {
+    uint64_t page_ins, page_outs, evictions, bytes_in, bytes_out;
+} ikv_qwen3_kv_counters;
+int ikv_qwen3_kv_stats(const ikv_qwen3 *m, ikv_qwen3_kv_counters *out);
 
 /* Weight tensors by GGUF name (ModelBase::load_weight, src/model.cpp:
  * 164-311): "token_embd.weight", "blk.<i>.attn_q.weight", ...,

@@ -76,9 +76,12 @@ int ikv_silu_f32(const float *x, float *out, int64_t n, void *stream);
  * *token = the index of the largest of logits[0, n); ties go to the lowest
  * index. A NaN or +inf logit, or all logits -inf, writes *token = -1 (the
  * reference returns invalid_argument). n must be in [1, 2^31). token is a
- * device int32.
+ * device int32; token_mirror, if not NULL, receives the same value and may
+ * be pinned host memory (hipHostMalloc), so that the host reads the token
+ * once the stream has passed this launch, with no copy of its own.
  * ------------------------------------------------------------------- */
-int ikv_argmax_f32(const float *logits, int64_t n, int32_t *token, void *stream);
+int ikv_argmax_f32(const float *logits, int64_t n, int32_t *token, int32_t *token_mirror,
+                   void *stream);
 
 /* ---------------------------------------------------------------------
  * Host helper: the benchmarks' synthetic weights. out_host[i] =

@@ -8,9 +8,10 @@
 //             status flag instead of reading outside the table.
 //   add/mul/silu  src/backends/cpu_backend.cpp:636-703: grid-stride float4.
 //   argmax    sample_greedy (src/sampler.cpp:42-65): one workgroup of 1024
-//             threads scans the logits (16-byte loads), keeps (max, lowest
-//             index) per lane, and reduces through DPP shuffles and LDS;
-//             NaN or +inf anywhere, or no finite maximum, gives -1.
+//             threads scans the logits (16-byte loads, 8 in flight per
+//             lane), keeps (max, lowest index) per lane, and reduces through
+//             shuffles and LDS; NaN or +inf anywhere, or no finite maximum,
+//             gives -1.
 #include <climits>
 
 #include "ikv_common.hpp"
@@ -83,6 +84,7 @@ int launch_ew(const float *a, const float *b, float *out, int64_t n, void *strea
 }
 
 constexpr int kArgThreads = 1024;
+constexpr int kArgBatch = 8;  // float4 loads in flight per lane
 
 // (value, index) pair order of the greedy sampler: larger value wins, equal
 // values go to the lower index.
@@ -102,7 +104,8 @@ __device__ __forceinline__ void visit(float x, int idx, float &best, int &bi, in
 }
 
 __global__ __launch_bounds__(kArgThreads) void argmax_kernel(const float *__restrict__ logits,
-                                                             int n, int32_t *token, int vec) {
+                                                             int n, int32_t *token,
+                                                             int32_t *mirror, int vec) {
   __shared__ float s_v[kArgThreads / 64];
   __shared__ int s_i[kArgThreads / 64];
   __shared__ int s_bad;
@@ -112,14 +115,25 @@ __global__ __launch_bounds__(kArgThreads) void argmax_kernel(const float *__rest
   int bi = INT_MAX;
   int bad = 0;
   if (vec) {
-    // Lane t reads float4 t, t + 1024, ...: its indices increase.
+    // Lane t reads float4 t, t + 1024, ...: its indices increase. Batches of
+    // kArgBatch loads are issued together, then visited in index order.
     const int n4 = n / 4;
-    for (int j = tid; j < n4; j += kArgThreads) {
-      const float4 v = reinterpret_cast<const float4 *>(logits)[j];
-      visit(v.x, 4 * j, best, bi, bad);
-      visit(v.y, 4 * j + 1, best, bi, bad);
-      visit(v.z, 4 * j + 2, best, bi, bad);
-      visit(v.w, 4 * j + 3, best, bi, bad);
+    for (int j0 = tid; j0 < n4; j0 += kArgBatch * kArgThreads) {
+      float4 v[kArgBatch];
+#pragma unroll
+      for (int u = 0; u < kArgBatch; ++u) {
+        const int j = j0 + u * kArgThreads;
+        v[u] = j < n4 ? reinterpret_cast<const float4 *>(logits)[j]
+                      : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+      }
+#pragma unroll
+      for (int u = 0; u < kArgBatch; ++u) {
+        const int j = j0 + u * kArgThreads;
+        visit(v[u].x, 4 * j, best, bi, bad);
+        visit(v[u].y, 4 * j + 1, best, bi, bad);
+        visit(v[u].z, 4 * j + 2, best, bi, bad);
+        visit(v[u].w, 4 * j + 3, best, bi, bad);
+      }
     }
     for (int j = 4 * n4 + tid; j < n; j += kArgThreads) visit(logits[j], j, best, bi, bad);
   } else {
@@ -141,7 +155,9 @@ __global__ __launch_bounds__(kArgThreads) void argmax_kernel(const float *__rest
     float v = s_v[0];
     int i = s_i[0];
     for (int w = 1; w < kArgThreads / 64; ++w) better(v, i, s_v[w], s_i[w]);
-    *token = (s_bad || v == -INFINITY || i == INT_MAX) ? -1 : i;
+    const int32_t t = (s_bad || v == -INFINITY || i == INT_MAX) ? -1 : i;
+    *token = t;
+    if (mirror) *mirror = t;
   }
 }
 
@@ -171,11 +187,12 @@ extern "C" int ikv_silu_f32(const float *x, float *out, int64_t n, void *stream)
   return launch_ew<Ew::kSilu>(x, nullptr, out, n, stream);
 }
 
-extern "C" int ikv_argmax_f32(const float *logits, int64_t n, int32_t *token, void *stream) {
+extern "C" int ikv_argmax_f32(const float *logits, int64_t n, int32_t *token,
+                              int32_t *token_mirror, void *stream) {
   if (!logits || !token) return -EINVAL;
   if (n < 1) return -EINVAL;
-  if (n > INT_MAX) return -EOVERFLOW;
+  if (n > INT_MAX - kArgBatch * kArgThreads * 4) return -EOVERFLOW;
   argmax_kernel<<<1, kArgThreads, 0, static_cast<hipStream_t>(stream)>>>(
-      logits, static_cast<int>(n), token, ikv::aligned16(logits) ? 1 : 0);
+      logits, static_cast<int>(n), token, token_mirror, ikv::aligned16(logits) ? 1 : 0);
   return ikv::launch_status();
 }

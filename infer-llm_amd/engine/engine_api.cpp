@@ -28,11 +28,10 @@ HIPBackend *hip(ikv_qwen3 *m) { return static_cast<HIPBackend *>(m->backend.get(
 
 namespace {
 
-int create(const ikv_qwen3_config *cfg, int device, int64_t max_ctx, int64_t block_tokens,
-           int64_t pool_blocks, ikv_qwen3 **out) {
+int create(const ikv_qwen3_config *cfg, int device, int64_t max_ctx, const KVOptions &kv,
+           ikv_qwen3 **out) {
   if (!cfg || !out || max_ctx <= 0 || device < 0) return -EINVAL;
-  if (block_tokens < 0 || pool_blocks < 0 || (block_tokens > 0 && block_tokens % 64 != 0))
-    return -EINVAL;
+  if (kv.block_tokens % 64 != 0) return -EINVAL;
   *out = nullptr;
   if (cfg->n_layer == 0 || cfg->n_embd == 0 || cfg->n_head == 0 || cfg->n_head_kv == 0 ||
       cfg->head_dim == 0 || cfg->n_ff == 0 || cfg->n_vocab == 0 ||
@@ -60,8 +59,7 @@ int create(const ikv_qwen3_config *cfg, int device, int64_t max_ctx, int64_t blo
   hp.rms_norm_eps = cfg->rms_norm_eps;
   m->model = std::make_unique<Qwen3Model>(hp);
   if (auto r = m->model->alloc_weights(m->backend.get()); !r) return to_errno(r.error());
-  m->runner = std::make_unique<Qwen3Runner>(*m->model, *hip(m.get()), size_t(max_ctx),
-                                            size_t(block_tokens), size_t(pool_blocks));
+  m->runner = std::make_unique<Qwen3Runner>(*m->model, *hip(m.get()), size_t(max_ctx), kv);
   if (auto r = m->runner->init(); !r) return to_errno(r.error());
   m->names = m->model->tensor_names();
   *out = m.release();
@@ -72,13 +70,27 @@ int create(const ikv_qwen3_config *cfg, int device, int64_t max_ctx, int64_t blo
 
 extern "C" int ikv_qwen3_create(const ikv_qwen3_config *cfg, int device, int64_t max_ctx,
                                 ikv_qwen3 **out) {
-  return create(cfg, device, max_ctx, 0, 0, out);
+  return create(cfg, device, max_ctx, KVOptions{}, out);
 }
 
 extern "C" int ikv_qwen3_create_paged(const ikv_qwen3_config *cfg, int device, int64_t max_ctx,
                                       int64_t block_tokens, int64_t pool_blocks, ikv_qwen3 **out) {
-  if (block_tokens <= 0) return -EINVAL;
-  return create(cfg, device, max_ctx, block_tokens, pool_blocks, out);
+  if (block_tokens <= 0 || pool_blocks < 0) return -EINVAL;
+  return create(cfg, device, max_ctx,
+                KVOptions{.block_tokens = size_t(block_tokens), .pool_blocks = size_t(pool_blocks)}, out);
+}
+
+extern "C" int ikv_qwen3_create_offload(const ikv_qwen3_config *cfg, int device, int64_t max_ctx,
+                                        uint64_t hbm_bytes, ikv_qwen3 **out) {
+  if (hbm_bytes == 0) return -EINVAL;
+  return create(cfg, device, max_ctx, KVOptions{.offload_bytes = size_t(hbm_bytes)}, out);
+}
+
+extern "C" int ikv_qwen3_kv_stats(const ikv_qwen3 *m, ikv_qwen3_kv_counters *out) {
+  if (!m || !out) return -EINVAL;
+  const OffloadStats s = m->runner->offload_stats();
+  *out = {s.page_ins, s.page_outs, s.evictions, s.bytes_in, s.bytes_out};
+  return 0;
 }
 
 extern "C" int ikv_qwen3_tensor_count(const ikv_qwen3 *m) {

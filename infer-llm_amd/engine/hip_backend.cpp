@@ -61,6 +61,42 @@ void HIPPhysicalAllocator::raw_free(void *ptr) {
   if (ptr) (void)hipFree(ptr);
 }
 
+infer::expected<void *, std::error_code> PinnedHostAllocator::raw_alloc(size_t bytes) {
+  if (bytes == 0) return static_cast<void *>(nullptr);
+  void *p = nullptr;
+  if (hipHostMalloc(&p, bytes, hipHostMallocDefault) != hipSuccess || !p) {
+    (void)hipGetLastError();
+    return infer::fail(std::errc::not_enough_memory);
+  }
+  return p;
+}
+
+void PinnedHostAllocator::raw_free(void *ptr) {
+  if (ptr) (void)hipHostFree(ptr);
+}
+
+// ---------------------------------------------------------------------------
+// pinned host backend: the host tier of OffloadKVStorage
+
+PinnedHostBackend::PinnedHostBackend(int device_id)
+    : Backend(device_id, {"host:" + std::to_string(device_id), DeviceType::CPU, 0}, {}) {
+  init_pools(std::make_unique<PinnedHostAllocator>());
+}
+
+infer::expected<void, std::error_code> PinnedHostBackend::copy_tensor_set(Tensor *t, const void *d,
+                                                                          size_t off, size_t n) {
+  if (!t || !t->data || !d || off + n > t->byte_size()) return infer::fail(std::errc::invalid_argument);
+  std::memcpy(static_cast<char *>(t->data) + off, d, n);
+  return {};
+}
+
+infer::expected<void, std::error_code> PinnedHostBackend::copy_tensor_get(const Tensor *t, void *d,
+                                                                          size_t off, size_t n) {
+  if (!t || !t->data || !d || off + n > t->byte_size()) return infer::fail(std::errc::invalid_argument);
+  std::memcpy(d, static_cast<const char *>(t->data) + off, n);
+  return {};
+}
+
 // ---------------------------------------------------------------------------
 // registration
 

@@ -103,3 +103,26 @@ class HIPBackend : public Backend {
   std::unordered_map<const Tensor *, std::pair<const Tensor *, const Tensor *>> _rope_into_attn;  // attn -> q, k rope
   std::unordered_map<const Tensor *, bool> _skip;
 };
+
+// Host memory as a backend: pinned (hipHostMalloc) pools, memcpy copies, no
+// compute. The host tier of OffloadKVStorage, so that its page-in and
+// write-back copies are DMA transfers from page-locked memory.
+class PinnedHostBackend final : public Backend {
+ public:
+  explicit PinnedHostBackend(int device_id = 0);
+  DeviceType device_type() const override { return DeviceType::CPU; }
+  std::string device_name() const override { return "PINNED_HOST"; }
+  bool supports_op(OperationType, const Tensor &) const override { return false; }
+  bool is_host() const override { return true; }
+  infer::expected<void, std::error_code> copy_tensor_set(Tensor *t, const void *d, size_t off,
+                                                         size_t n) override;
+  infer::expected<void, std::error_code> copy_tensor_get(const Tensor *t, void *d, size_t off,
+                                                         size_t n) override;
+  infer::expected<bool, std::error_code> copy_tensor_high(const Tensor *, Tensor *) const override {
+    return false;
+  }
+  infer::expected<void, std::error_code> compute(Graph &) override {
+    return infer::fail(std::errc::not_supported);
+  }
+};
+

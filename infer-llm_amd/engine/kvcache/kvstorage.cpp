@@ -34,6 +34,7 @@ infer::expected<KVStorageObject, std::error_code> KVStorage::acquire(StorageId i
       !obj.k_base || !obj.v_base)
     return infer::fail(std::errc::invalid_argument);
   ++st.active_users;
+  record_access(id);
   return obj;
 }
 

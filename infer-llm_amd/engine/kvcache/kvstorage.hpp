@@ -70,6 +70,8 @@ class KVStorage {
   virtual infer::expected<void, std::error_code> prepare_object(const KVObjectAccessRequest &req) = 0;
   // Called only with active_users == 0; the base erases the entry after it.
   virtual void destroy_object(StorageId id) noexcept = 0;
+  // Called on every successful acquire (recency for eviction policies).
+  virtual void record_access(StorageId) noexcept {}
 
   std::unordered_map<StorageId, StorageState> _states;
   std::vector<KVLayerSpec> _layers;

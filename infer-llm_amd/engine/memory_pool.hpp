@@ -37,6 +37,14 @@ class HIPPhysicalAllocator : public PhysicalAllocator {
   void raw_free(void *ptr) override;
 };
 
+// hipHostMalloc-backed pinned host memory: the host tier of the KV offload
+// storage, which the DMA engines copy to and from HBM directly.
+class PinnedHostAllocator : public PhysicalAllocator {
+ public:
+  infer::expected<void *, std::error_code> raw_alloc(size_t bytes) override;
+  void raw_free(void *ptr) override;
+};
+
 class MemoryPool {
  public:
   explicit MemoryPool(PhysicalAllocator &a) : _phys_allocator(&a) {}

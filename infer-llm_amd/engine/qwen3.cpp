@@ -163,13 +163,8 @@ infer::expected<Graph, std::error_code> Qwen3Model::build_graph(GraphContext &ct
 // ---------------------------------------------------------------------------
 // runner
 
-Qwen3Runner::Qwen3Runner(Qwen3Model &model, HIPBackend &backend, size_t capacity,
-                         size_t block_tokens, size_t pool_blocks)
-    : _model(model),
-      _backend(backend),
-      _capacity(capacity),
-      _block_tokens(block_tokens),
-      _pool_blocks(pool_blocks) {}
+Qwen3Runner::Qwen3Runner(Qwen3Model &model, HIPBackend &backend, size_t capacity, KVOptions kv)
+    : _model(model), _backend(backend), _capacity(capacity), _kv_opt(kv) {}
 
 Qwen3Runner::~Qwen3Runner() {
   (void)_backend.synchronize();
@@ -187,12 +182,22 @@ infer::expected<void, std::error_code> Qwen3Runner::init() {
   std::vector<KVLayerSpec> specs(hp.n_layer, KVLayerSpec{hp.n_head_kv, hp.head_dim, hp.head_dim});
   std::vector<Backend *> place(hp.n_layer, &_backend);
   KVCacheConfig cfg{.layers = hp.n_layer, .max_tokens_per_sequence = _capacity};
-  if (_block_tokens > 0) {
-    const size_t blocks =
-        _pool_blocks ? _pool_blocks : (_capacity + _block_tokens - 1) / _block_tokens;
-    cfg.block_tokens = _block_tokens;
+  if (_kv_opt.block_tokens > 0 && _kv_opt.offload_bytes > 0) return infer::fail(std::errc::invalid_argument);
+  if (_kv_opt.block_tokens > 0) {
+    const size_t bt = _kv_opt.block_tokens;
+    const size_t blocks = _kv_opt.pool_blocks ? _kv_opt.pool_blocks : (_capacity + bt - 1) / bt;
+    cfg.block_tokens = bt;
     _kv = std::make_unique<KVCacheManager>(std::make_unique<PagedKVStrategy>(
-        std::make_unique<BlockPoolKVStorage>(blocks, _block_tokens)));
+        std::make_unique<BlockPoolKVStorage>(blocks, bt)));
+  } else if (_kv_opt.offload_bytes > 0) {
+    _host = std::make_unique<PinnedHostBackend>(0);
+    OffloadKVStorageConfig oc;
+    oc.host_backend = _host.get();
+    oc.device_budgets.push_back({.backend = &_backend, .resident_bytes = _kv_opt.offload_bytes,
+                                 .prefetch_bytes = _kv_opt.offload_bytes});
+    _kv = std::make_unique<KVCacheManager>(std::make_unique<ContiguousKVStrategy>(
+        std::make_unique<OffloadKVStorage>(std::move(oc), std::make_unique<LRUKVEvictionPolicy>(),
+                                           std::make_unique<NextAccessKVPrefetchPolicy>(2))));
   } else {
     _kv = std::make_unique<KVCacheManager>(
         std::make_unique<ContiguousKVStrategy>(std::make_unique<NaiveKVStorage>()));
@@ -215,7 +220,11 @@ infer::expected<void, std::error_code> Qwen3Runner::init() {
   };
   if (hipMalloc(&_token_dev, 2 * sizeof(int32_t)) != hipSuccess) return fail_alloc();
   if (hipMalloc(&_positions_dev, _capacity * sizeof(int32_t)) != hipSuccess) return fail_alloc();
-  if (hipHostMalloc(&_token_host, 2 * sizeof(int32_t), hipHostMallocDefault) != hipSuccess)
+  // Mapped and coherent: the sampler's store reaches host memory directly.
+  if (hipHostMalloc(&_token_host, 2 * sizeof(int32_t), hipHostMallocMapped | hipHostMallocCoherent) !=
+          hipSuccess ||
+      hipHostGetDevicePointer(reinterpret_cast<void **>(&_token_host_dev), _token_host, 0) !=
+          hipSuccess)
     return fail_alloc();
   for (hipEvent_t &e : _ready)
     if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) return fail_alloc();
@@ -267,9 +276,9 @@ infer::expected<void, std::error_code> Qwen3Runner::enqueue_step(const int32_t *
   const int64_t vocab = logits->dims[0];
   const float *row = static_cast<const float *>(logits->data) + (n - 1) * vocab;
   hipStream_t s = _backend.stream();
-  if (ikv_argmax_f32(row, vocab, _token_dev + slot, s) != 0 ||
-      hipMemcpyAsync(_token_host + slot, _token_dev + slot, sizeof(int32_t), hipMemcpyDeviceToHost,
-                     s) != hipSuccess ||
+  // The sampler writes the token to the device slot the next step embeds
+  // and to the pinned host slot the host reads once the event has fired.
+  if (ikv_argmax_f32(row, vocab, _token_dev + slot, _token_host_dev + slot, s) != 0 ||
       hipEventRecord(_ready[slot], s) != hipSuccess)
     return abort(std::make_error_code(std::errc::io_error));
   // The kernels of this step hold no host-side state: hand the layer
@@ -338,3 +347,10 @@ infer::expected<void, std::error_code> Qwen3Runner::generate(const std::vector<i
       n_gen > 1 ? std::chrono::duration<double>(last - first).count() / double(n_gen - 1) : 0.0;
   return finish({});
 }
+
+OffloadStats Qwen3Runner::offload_stats() const {
+  if (!_kv) return {};
+  if (const auto *o = dynamic_cast<const OffloadKVStorage *>(_kv->strategy()->storage())) return o->stats();
+  return {};
+}
+

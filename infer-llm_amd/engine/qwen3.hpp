@@ -17,8 +17,9 @@
 // token slot that the next step's embedding reads directly, and positions
 // come from a resident device table, so no step waits for the previous one
 // on the host: the host builds and enqueues step i+1 while the GPU runs step
-// i, then reads back token i (pinned memory, one event per slot). A token is
-// "ready" when the host has it, as in the reference's loop.
+// i, then reads back token i, which the sampler also writes to pinned host
+// memory (one event per slot). A token is "ready" when the host has it, as
+// in the reference's loop.
 #pragma once
 
 #include <chrono>
@@ -33,6 +34,7 @@
 #include "graph.hpp"
 #include "hip_backend.hpp"
 #include "kvcache/kvcache_manager.hpp"
+#include "kvcache/offload_storage.hpp"
 #include "scheduler.hpp"
 
 struct Qwen3Hparams {
@@ -91,6 +93,20 @@ class Qwen3Model {
   std::vector<Qwen3LayerWeights> _layers;
 };
 
+// How the runner keeps its KV cache.
+//   default            one contiguous HBM cache per layer (ContiguousKVStrategy
+//                      over NaiveKVStorage)
+//   block_tokens > 0   paged: PagedKVStrategy over a BlockPoolKVStorage of
+//                      pool_blocks blocks per layer (0 = one sequence's worth)
+//   offload_bytes > 0  contiguous caches in an OffloadKVStorage: pinned host
+//                      copies, at most offload_bytes of them resident in HBM
+//                      (LRU eviction with write-back)
+struct KVOptions {
+  size_t block_tokens = 0;
+  size_t pool_blocks = 0;
+  size_t offload_bytes = 0;
+};
+
 struct GenerationTiming {
   double ttft_s = 0;      // first sampled token - start
   double tpot_s = 0;      // (last - first) / (n_gen - 1)
@@ -102,11 +118,7 @@ struct GenerationTiming {
 
 class Qwen3Runner {
  public:
-  // block_tokens > 0 keeps the KV cache paged (PagedKVStrategy over a
-  // BlockPoolKVStorage of pool_blocks blocks per layer; 0 = enough for one
-  // sequence of `capacity` tokens); 0 keeps one contiguous cache per layer.
-  Qwen3Runner(Qwen3Model &model, HIPBackend &backend, size_t capacity, size_t block_tokens = 0,
-              size_t pool_blocks = 0);
+  Qwen3Runner(Qwen3Model &model, HIPBackend &backend, size_t capacity, KVOptions kv = {});
   ~Qwen3Runner();
   infer::expected<void, std::error_code> init();
   // prompt, then n_gen greedy tokens (the first from the prompt's last
@@ -114,6 +126,8 @@ class Qwen3Runner {
   infer::expected<void, std::error_code> generate(const std::vector<int32_t> &prompt, size_t n_gen,
                                                   std::vector<int32_t> &tokens_out,
                                                   GenerationTiming &timing);
+  // Page-in / write-back counts of an offloaded cache (zeros otherwise).
+  OffloadStats offload_stats() const;
 
  private:
   // Enqueues one step; its greedy token lands in token slot `slot` (device)
@@ -125,7 +139,8 @@ class Qwen3Runner {
   Qwen3Model &_model;
   HIPBackend &_backend;
   size_t _capacity;
-  size_t _block_tokens, _pool_blocks;
+  KVOptions _kv_opt;
+  std::unique_ptr<Backend> _host;  // the host tier of an offloaded cache
   std::unique_ptr<KVCacheManager> _kv;
   std::unique_ptr<Scheduler> _sched;
   std::unique_ptr<GraphContext> _ctx;
@@ -134,6 +149,7 @@ class Qwen3Runner {
   std::vector<int32_t> _input;
   int32_t *_token_dev = nullptr;    // [2] sampled-token slots
   int32_t *_token_host = nullptr;   // [2] pinned read-back slots
+  int32_t *_token_host_dev = nullptr;  // the same slots as the device addresses them
   int32_t *_positions_dev = nullptr;  // [capacity]: 0, 1, 2, ...
   hipEvent_t _ready[2] = {nullptr, nullptr};
 };

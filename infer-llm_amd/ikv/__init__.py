@@ -106,7 +106,7 @@ SIGNATURES = {
     "ikv_add_f32": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int64, _c_void_p]),
     "ikv_mul_f32": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int64, _c_void_p]),
     "ikv_silu_f32": (_c_int, [_c_void_p, _c_void_p, _c_int64, _c_void_p]),
-    "ikv_argmax_f32": (_c_int, [_c_void_p, _c_int64, _c_void_p, _c_void_p]),
+    "ikv_argmax_f32": (_c_int, [_c_void_p, _c_int64, _c_void_p, _c_void_p, _c_void_p]),
     "ikv_synth_normal_f32": (
         _c_int, [ctypes.c_uint64, ctypes.c_uint64, _c_size_t, ctypes.c_double, _c_void_p, _c_int]),
     # include/ikv_probe.h
@@ -508,13 +508,14 @@ def elementwise(op: str, a, b=None, out=None, stream=None):
     return out
 
 
-def argmax(logits, token=None, stream=None):
-    """Device int32 [1]: greedy token of logits (ties -> lowest id; -1 on NaN/+inf)."""
+def argmax(logits, token=None, mirror=None, stream=None):
+    """Device int32 [1]: greedy token of logits (ties -> lowest id; -1 on NaN/+inf);
+    `mirror` (e.g. a pinned host tensor) receives a copy."""
     torch = _torch()
     if token is None:
         token = torch.empty(1, dtype=torch.int32, device=logits.device)
     _check("ikv_argmax_f32", load().ikv_argmax_f32(_ptr(logits), logits.numel(), _ptr(token),
-                                                    _stream(stream)))
+                                                    _ptr(mirror), _stream(stream)))
     return token
 
 

@@ -51,11 +51,19 @@ class Stats(ctypes.Structure):
 
 
 _P = ctypes.c_void_p
+class KvStats(ctypes.Structure):
+    _fields_ = [(f, ctypes.c_uint64) for f in ("page_ins", "page_outs", "evictions", "bytes_in",
+                                                "bytes_out")]
+
+
 ENGINE_SIGNATURES = {
     "ikv_qwen3_create": (ctypes.c_int, [ctypes.POINTER(_Config), ctypes.c_int, ctypes.c_int64,
                                         ctypes.POINTER(_P)]),
     "ikv_qwen3_create_paged": (ctypes.c_int, [ctypes.POINTER(_Config), ctypes.c_int, ctypes.c_int64,
                                               ctypes.c_int64, ctypes.c_int64, ctypes.POINTER(_P)]),
+    "ikv_qwen3_create_offload": (ctypes.c_int, [ctypes.POINTER(_Config), ctypes.c_int, ctypes.c_int64,
+                                                ctypes.c_uint64, ctypes.POINTER(_P)]),
+    "ikv_qwen3_kv_stats": (ctypes.c_int, [_P, ctypes.POINTER(KvStats)]),
     "ikv_qwen3_tensor_count": (ctypes.c_int, [_P]),
     "ikv_qwen3_tensor_name": (ctypes.c_char_p, [_P, ctypes.c_int]),
     "ikv_qwen3_tensor_size": (ctypes.c_size_t, [_P, ctypes.c_char_p]),
@@ -114,15 +122,21 @@ def synthetic_weights(cfg: Qwen3Config, seed: int, std: float = 0.02, threads: i
 
 class Qwen3Engine:
     """A Qwen3 model on HIP device `device` with a KV cache of max_ctx tokens:
-    one contiguous cache per layer, or with block_tokens > 0 a paged cache
-    (pool_blocks blocks of block_tokens tokens per layer; 0 = max_ctx worth)."""
+    one contiguous cache per layer; with block_tokens > 0 a paged cache
+    (pool_blocks blocks of block_tokens tokens per layer; 0 = max_ctx worth);
+    with offload_hbm_bytes > 0 per-layer caches in pinned host memory of which
+    at most that many bytes are resident in HBM."""
 
     def __init__(self, cfg: Qwen3Config, max_ctx: int, device: int = 0, block_tokens: int = 0,
-                 pool_blocks: int = 0):
+                 pool_blocks: int = 0, offload_hbm_bytes: int = 0):
         self.cfg = cfg
         c = _Config(*(getattr(cfg, f) for f, _ in _Config._fields_))
         h = _P()
-        if block_tokens:
+        if offload_hbm_bytes:
+            _check("ikv_qwen3_create_offload",
+                   _lib().ikv_qwen3_create_offload(ctypes.byref(c), device, max_ctx,
+                                                   offload_hbm_bytes, ctypes.byref(h)))
+        elif block_tokens:
             _check("ikv_qwen3_create_paged",
                    _lib().ikv_qwen3_create_paged(ctypes.byref(c), device, max_ctx, block_tokens,
                                                  pool_blocks, ctypes.byref(h)))
@@ -141,6 +155,11 @@ class Qwen3Engine:
             self.close()
         except Exception:
             pass
+
+    def kv_stats(self):
+        st = KvStats()
+        _check("ikv_qwen3_kv_stats", _lib().ikv_qwen3_kv_stats(self._h, ctypes.byref(st)))
+        return {f: getattr(st, f) for f, _ in KvStats._fields_}
 
     def tensor_names(self):
         lib = _lib()

@@ -25,6 +25,7 @@
 #include "../../infer-llm_amd/engine/graph.hpp"
 #include "../../infer-llm_amd/engine/hip_backend.hpp"
 #include "../../infer-llm_amd/engine/kvcache/kvcache_manager.hpp"
+#include "../../infer-llm_amd/engine/kvcache/offload_storage.hpp"
 #include "../../infer-llm_amd/engine/op_factory.hpp"
 #include "../../infer-llm_amd/engine/scheduler.hpp"
 #include "../../oracle/oracle.h"
@@ -101,6 +102,8 @@ struct Rng {
 // CPU checks
 
 static void paged_cpu_tests();
+static void offload_cpu_tests();
+static void offload_gpu_tests(HIPBackend *hip);
 
 static void cpu_tests() {
   {
@@ -233,6 +236,7 @@ static void cpu_tests() {
           "graph topo order; append_kv = CPY then VIEW over the cache");
   }
   paged_cpu_tests();
+  offload_cpu_tests();
 }
 
 // Paged strategy over a block pool (KVCacheConfig::block_tokens > 0): block
@@ -317,6 +321,86 @@ static void paged_cpu_tests() {
   auto big = kv.reserve_append(*c, 321);
   CHECK(!big && is_err(big.error(), std::errc::not_enough_memory), "beyond max_tokens_per_sequence");
   CHECK(kv.clear_sequence() && pool->free_blocks(0) == nb && pool->free_blocks(1) == nb, "clear returns all blocks");
+}
+
+// Offload storage: host copies, an HBM budget, LRU eviction with write-back,
+// busy objects, prefetch. The "device" is host memory that reports itself as
+// not host, so every transfer is a memcpy the test can check.
+class FakeDevice : public HostBackend {
+ public:
+  bool is_host() const override { return false; }
+  DeviceType device_type() const override { return DeviceType::HIP; }
+};
+
+static void offload_cpu_tests() {
+  HostBackend host;
+  FakeDevice dev;
+  const size_t L = 3, cap = 16, obj = cap * 8 * 128 * 4 * 2;
+  std::vector<KVLayerSpec> specs(L, KVLayerSpec{8, 128, 128, GGML_TYPE_F32, GGML_TYPE_F32});
+  std::vector<Backend *> place(L, &dev);
+  auto make = [&](std::vector<KVDeviceBudget> budgets) {
+    OffloadKVStorageConfig oc;
+    oc.host_backend = &host;
+    oc.device_budgets = std::move(budgets);
+    return std::make_unique<OffloadKVStorage>(std::move(oc), std::make_unique<LRUKVEvictionPolicy>(),
+                                              std::make_unique<NextAccessKVPrefetchPolicy>(2));
+  };
+  {
+    KVCacheManager bad(std::make_unique<ContiguousKVStrategy>(make({})));
+    auto r = bad.init(specs, place, KVCacheConfig{.layers = L, .max_tokens_per_sequence = cap});
+    CHECK(!r && is_err(r.error(), std::errc::invalid_argument), "offload init: a device without a budget");
+  }
+  auto owner = make({{.backend = &dev, .resident_bytes = 2 * obj, .prefetch_bytes = 2 * obj}});
+  OffloadKVStorage *st = owner.get();
+  KVCacheManager kv(std::make_unique<ContiguousKVStrategy>(std::move(owner)));
+  CHECK(kv.init(specs, place, KVCacheConfig{.layers = L, .max_tokens_per_sequence = cap}), "offload init");
+  const int host_allocs = host.allocs, dev_allocs = dev.allocs;
+  auto sid = kv.create_sequence();
+  CHECK(sid && host.allocs == host_allocs + int(L) && dev.allocs == dev_allocs && st->resident_bytes(&dev) == 0,
+        "sequence: one host copy per layer, nothing in HBM yet");
+  CHECK(kv.reserve_append(*sid, 4), "reserve");
+  const StorageId id0 = 1, id1 = 2, id2 = 3;
+  auto a0 = kv.acquire_layer(*sid, 0);
+  CHECK(a0 && st->resident(id0) && st->stats().page_ins == 1 && st->resident_bytes(&dev) == obj,
+        "acquire uploads the layer");
+  // write a pattern through the view (the HBM copy)
+  float *k0 = a0 ? static_cast<float *>(a0->readable.k.front().view.data) : nullptr;
+  if (k0)
+    for (int i = 0; i < 4 * 1024; ++i) k0[i] = float(i) * 0.5f;
+  if (a0) (void)kv.release_layer(*a0);
+  auto a1 = kv.acquire_layer(*sid, 1);
+  if (a1) (void)kv.release_layer(*a1);
+  auto a2 = kv.acquire_layer(*sid, 2);
+  CHECK(a2 && !st->resident(id0) && st->resident(id1) && st->resident(id2) && st->stats().evictions == 1 &&
+            st->stats().page_outs == 1,
+        "budget of two: the least recently used layer is written back and dropped");
+  if (a2) (void)kv.release_layer(*a2);
+  auto b0 = kv.acquire_layer(*sid, 0);
+  bool same = b0.has_value();
+  if (b0) {
+    const float *k = static_cast<const float *>(b0->readable.k.front().view.data);
+    for (int i = 0; i < 4 * 1024 && same; ++i) same = k[i] == float(i) * 0.5f;
+  }
+  CHECK(same && !st->resident(id1) && st->resident(id0), "paged back in with its rows; LRU victim next was layer 1");
+  auto b2 = kv.acquire_layer(*sid, 2);
+  auto b1 = kv.acquire_layer(*sid, 1);
+  CHECK(b0 && b2 && !b1 && is_err(b1.error(), std::errc::not_enough_memory),
+        "no room while both resident layers are held");
+  auto busy = st->evict(id0);
+  CHECK(!busy && is_err(busy.error(), std::errc::device_or_resource_busy), "evict refuses a held layer");
+  if (b0) (void)kv.release_layer(*b0);
+  if (b2) (void)kv.release_layer(*b2);
+  CHECK(st->evict(id0) && st->evict(id2) && st->resident_bytes(&dev) == 0, "explicit evictions");
+  const KVPrefetchRequest up[] = {{id1, 4}, {id2, 4}, {id0, 4}};
+  auto n = st->prefetch(KVPrefetchContext{.current = id0, .upcoming = up});
+  CHECK(n && *n == 2 && st->resident(id1) && st->resident(id2) && !st->resident(id0),
+        "prefetch uploads the next two within the budget, evicting nothing");
+  auto n2 = st->prefetch(KVPrefetchContext{.current = id1, .upcoming = std::span(up + 2, 1)});
+  CHECK(n2 && *n2 == 0 && !st->resident(id0), "prefetch skips what does not fit");
+  const int dev_frees = dev.frees, host_frees = host.frees;
+  CHECK(kv.commit_append(*sid) && kv.release_sequence(*sid) && dev.frees == dev_frees + 2 &&
+            host.frees == host_frees + int(L),
+        "release frees every copy");
 }
 
 // ---------------------------------------------------------------------------
@@ -494,6 +578,139 @@ static void gpu_tests() {
     }
   }
   CHECK(kv.release_sequence(*sid), "release sequence (frees HBM caches)");
+  for (auto &t : qw_d) hip->free(BufferKind::WEIGHTS, t->data);
+  for (auto &t : kw_d) hip->free(BufferKind::WEIGHTS, t->data);
+  offload_gpu_tests(hip);
+}
+
+// Two sequences on an offloaded cache whose HBM budget holds one sequence's
+// layers: every switch writes the other sequence's layers back to pinned
+// host memory and uploads this one's. Attention within tolerance of the
+// oracle and cache rows bit-exact, after every switch.
+static void offload_gpu_tests(HIPBackend *hip) {
+  const int Hq = 16, Hkv = 8, D = 128, L = 2, P = 21, N = 3;
+  const size_t cap = P + N;
+  const size_t layer_bytes = cap * Hkv * D * 4 * 2;
+  AttentionSliceParams sp;
+  std::vector<KVLayerSpec> specs(L, KVLayerSpec{size_t(Hkv), size_t(D), size_t(D)});
+  std::vector<Backend *> place(L, hip);
+  PinnedHostBackend host(0);
+  OffloadKVStorageConfig oc;
+  oc.host_backend = &host;
+  oc.device_budgets.push_back({.backend = hip, .resident_bytes = L * layer_bytes, .prefetch_bytes = 0});
+  auto owner = std::make_unique<OffloadKVStorage>(std::move(oc), std::make_unique<LRUKVEvictionPolicy>(),
+                                                  std::make_unique<NoKVPrefetchPolicy>());
+  OffloadKVStorage *st = owner.get();
+  KVCacheManager kv(std::make_unique<ContiguousKVStrategy>(std::move(owner)));
+  CHECK(kv.init(specs, place, KVCacheConfig{.layers = L, .max_tokens_per_sequence = cap}), "offload kv init on hip");
+  CHECK(hip->reserve_decode_workspace(Hq, Hkv, D, cap), "offload: workspace");
+  Rng rng(0x1F0000 + 9);
+  std::vector<std::unique_ptr<Tensor>> owned;
+  auto upload = [&](const std::vector<float> &h, std::initializer_list<int64_t> shape) {
+    auto t = std::make_unique<Tensor>("t", GGML_TYPE_F32, shape);
+    t->data = *hip->alloc(BufferKind::WEIGHTS, t->byte_size());
+    t->backend = hip;
+    t->device = DeviceType::HIP;
+    t->tensorRole = TensorRole::TENSOR_ROLE_WEIGHT;
+    hip->copy_tensor_set(t.get(), h.data(), 0, h.size() * 4);
+    return t;
+  };
+  std::vector<std::vector<float>> qw(L), kw(L);
+  std::vector<std::unique_ptr<Tensor>> qw_d, kw_d;
+  for (int l = 0; l < L; ++l) {
+    qw[l] = rng.normal(D, 0.5);
+    kw[l] = rng.normal(D, 0.5);
+    qw_d.push_back(upload(qw[l], {D, 1, 1, 1}));
+    kw_d.push_back(upload(kw[l], {D, 1, 1, 1}));
+  }
+  std::vector<float> theta(size_t(64) * sp.n_ctx_train);
+  oracle_rope_theta_table(sp.rope_theta, D, sp.n_ctx_train, theta.data());
+  struct Seq {
+    SequenceId sid = kInvalidSequenceId;
+    size_t n_past = 0;
+    std::vector<std::vector<float>> hk, hv;
+  };
+  Seq seqs[2];
+  for (auto &q : seqs) {
+    auto sid = kv.create_sequence();
+    q.sid = sid ? *sid : kInvalidSequenceId;
+    q.hk.assign(L, std::vector<float>(cap * Hkv * D, 0.f));
+    q.hv = q.hk;
+  }
+  Scheduler sched(hip);
+  bool all_ok = seqs[0].sid != kInvalidSequenceId && seqs[1].sid != kInvalidSequenceId;
+  for (int round = 0; round <= N && all_ok; ++round) {
+    for (Seq &q : seqs) {
+      const int n = round == 0 ? P : 1;
+      GraphContext ctx(nullptr);
+      Tensor *pos_t = ctx.make_tensor("inp_pos", GGML_TYPE_I32, {n});
+      pos_t->device = DeviceType::CPU;
+      pos_t->tensorRole = TensorRole::TNESOR_ROLE_INPUT;
+      ctx.set_input_pos(pos_t);
+      std::vector<int32_t> pos(n);
+      for (int i = 0; i < n; ++i) pos[i] = int32_t(q.n_past + i);
+      pos_t->data = pos.data();
+      if (!ctx.set_kv_cache(&kv, q.sid) || !kv.reserve_append(q.sid, n)) {
+        all_ok = false;
+        break;
+      }
+      Graph g;
+      std::vector<std::vector<float>> hq(L), hkp(L), hvp(L);
+      std::vector<std::unique_ptr<Tensor>> in;
+      std::vector<Tensor *> outs;
+      for (int l = 0; l < L && all_ok; ++l) {
+        hq[l] = rng.normal(size_t(n) * Hq * D);
+        hkp[l] = rng.normal(size_t(n) * Hkv * D);
+        hvp[l] = rng.normal(size_t(n) * Hkv * D);
+        in.push_back(upload(hq[l], {Hq * D, n, 1, 1}));
+        in.push_back(upload(hkp[l], {Hkv * D, n, 1, 1}));
+        in.push_back(upload(hvp[l], {Hkv * D, n, 1, 1}));
+        auto out = build_attention_slice(g, ctx, in[3 * l].get(), in[3 * l + 1].get(), in[3 * l + 2].get(),
+                                         qw_d[l].get(), kw_d[l].get(), l, sp);
+        if (!out) all_ok = false;
+        else {
+          g.mark_output(*out);
+          outs.push_back(*out);
+        }
+      }
+      all_ok = all_ok && sched.execute(g) && hip->synchronize();
+      for (int l = 0; l < L && all_ok; ++l) {
+        std::vector<float> qn(hq[l].size()), kn(hkp[l].size()), qr(hq[l].size()), kr(hkp[l].size());
+        oracle_rms_norm_f32(hq[l].data(), qw[l].data(), qn.data(), int64_t(n) * Hq, D, sp.rms_norm_eps);
+        oracle_rms_norm_f32(hkp[l].data(), kw[l].data(), kn.data(), int64_t(n) * Hkv, D, sp.rms_norm_eps);
+        oracle_rope_neox_f32(qn.data(), pos.data(), theta.data(), sp.n_ctx_train, qr.data(), D, Hq, n);
+        oracle_rope_neox_f32(kn.data(), pos.data(), theta.data(), sp.n_ctx_train, kr.data(), D, Hkv, n);
+        oracle_cpy(q.hk[l].data() + q.n_past * Hkv * D, kr.data(), kr.size() * 4);
+        oracle_cpy(q.hv[l].data() + q.n_past * Hkv * D, hvp[l].data(), hvp[l].size() * 4);
+        std::vector<float> want(size_t(n) * Hq * D), got(want.size());
+        oracle_flash_attn_f32(qr.data(), q.hk[l].data(), q.hv[l].data(), want.data(), D, Hq, n, Hkv,
+                              int64_t(q.n_past + n), int64_t(q.n_past));
+        hip->copy_tensor_get(outs[l], got.data(), 0, got.size() * 4);
+        double worst;
+        all_ok = attn_close(got.data(), want.data(), got.size(), &worst);
+        if (!all_ok) std::printf("  offload round %d layer %d worst excess %.3e\n", round, l, worst);
+        // the HBM copy this step used holds the committed rows, bit for bit
+        const size_t bytes = (q.n_past + n) * Hkv * D * 4;
+        std::vector<float> dk(bytes / 4), dv(bytes / 4);
+        const StorageState *ss = st->state(StorageId(1 + (&q - seqs) * L + l));
+        (void)hipMemcpy(dk.data(), ss->object.k_base, bytes, hipMemcpyDeviceToHost);
+        (void)hipMemcpy(dv.data(), ss->object.v_base, bytes, hipMemcpyDeviceToHost);
+        all_ok = all_ok && std::memcmp(dk.data(), q.hk[l].data(), bytes) == 0 &&
+                 std::memcmp(dv.data(), q.hv[l].data(), bytes) == 0;
+      }
+      all_ok = all_ok && ctx.release_kv_access() && kv.commit_append(q.sid);
+      q.n_past += n;
+      for (auto &t : in) hip->free(BufferKind::WEIGHTS, t->data);
+    }
+  }
+  const OffloadStats &os = st->stats();
+  CHECK(all_ok, "offload: two sequences in one sequence's HBM, attention and caches exact at every switch");
+  CHECK(os.evictions >= size_t(2 * N + 1) * L && os.page_outs == os.evictions &&
+            os.page_ins == os.evictions + L && os.bytes_in == os.page_ins * layer_bytes,
+        "offload: every switch wrote back and uploaded whole layers");
+  for (auto &q : seqs)
+    if (q.sid != kInvalidSequenceId) (void)kv.release_sequence(q.sid);
+  CHECK(st->resident_bytes(hip) == 0, "offload: released sequences leave nothing in HBM");
   for (auto &t : qw_d) hip->free(BufferKind::WEIGHTS, t->data);
   for (auto &t : kw_d) hip->free(BufferKind::WEIGHTS, t->data);
 }

@@ -135,6 +135,17 @@ def test_argmax_follows_the_greedy_sampler(dev):
     assert int(host(ikv.argmax(big[1:]))[0]) == 5
     w = synth.normal(19, (7,))
     assert int(host(ikv.argmax(dev_t(w, dev)))[0]) == int(np.argmax(w))
+    # the maximum in the last batch of loads, in the scalar tail, at index 0;
+    # ties across load batches; and the mirror output
+    for n, at in ((151936, 151930), (151937, 151936), (40003, 0), (32768 * 4 + 5, 32768 * 4 - 1)):
+        v = synth.normal(20 + n, (n,))
+        v[at] = 50.0
+        mirror = torch.full((1,), -7, dtype=torch.int32, device=dev)
+        tok = ikv.argmax(dev_t(v, dev), mirror=mirror)
+        assert int(host(tok)[0]) == at == int(host(mirror)[0]) == oracle.sample_greedy(v)
+    t = synth.normal(21, (100000,))
+    t[[8191 * 4 + 1, 8192 * 4 + 2, 99999]] = 40.0       # tie between two load batches
+    assert int(host(ikv.argmax(dev_t(t, dev)))[0]) == 8191 * 4 + 1 == oracle.sample_greedy(t)
     del torch
 
 

@@ -233,3 +233,35 @@ def test_paged_engine_pool_too_small_fails_cleanly(dev):
         eng.generate(list(range(1, 100)), 40)                        # 138 do not
     assert len(eng.generate(list(range(1, 60)), 40)[0]) == 40       # blocks came back
     eng.close()
+
+
+# ---------------------------------------------------------------------------
+# the whole model on the HBM <-> host offload tier
+# ---------------------------------------------------------------------------
+
+def test_offload_engine_matches_hbm_cache(dev, oracle_pool):
+    """Every layer of a step is held while the step runs, so a single
+    sequence needs all its layers resident: one upload per layer, same tokens.
+    (Eviction and write-back between sequences are checked by
+    tests/cpp/test_engine.cpp --gpu.)"""
+    from ikv import qwen3
+    cfg = qwen3.Qwen3Config(n_layer=3, n_vocab=8192, n_ctx_train=4096)
+    w = qwen3.synthetic_weights(cfg, synth.config_seed(0, 30))
+    prompt = synth.uniform_ints(synth.config_seed(0, 31), 40, cfg.n_vocab)
+    flat = qwen3.Qwen3Engine(cfg, 256)
+    flat.set_weights(w)
+    layer_bytes = 256 * 8 * 128 * 4 * 2
+    off = qwen3.Qwen3Engine(cfg, 256, offload_hbm_bytes=3 * layer_bytes)
+    off.set_weights(w)
+    want = flat.generate(prompt, 30)[0]
+    assert off.generate(prompt, 30)[0] == want
+    st = off.kv_stats()
+    assert st["page_ins"] == 3 and st["evictions"] == 0 and st["bytes_in"] == 3 * layer_bytes
+    assert want == oracle.Qwen3Oracle(cfg, w, 256).generate(prompt, 30)
+    # two layers of budget cannot hold a step's three: a clean error, no fault
+    small = qwen3.Qwen3Engine(cfg, 256, offload_hbm_bytes=2 * layer_bytes)
+    small.set_weights(w)
+    with pytest.raises(ikv.IkvError):
+        small.generate(prompt, 5)
+    for e in (flat, off, small):
+        e.close()
