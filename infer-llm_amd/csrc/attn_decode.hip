@@ -80,6 +80,7 @@ constexpr int kMergeChunk = 16;
 // Arrival counters: one int per KV head, kCounterStride ints apart.
 constexpr int kCounterStride = 64;
 
+
 // MI355X compute units.
 constexpr int kCUs = 256;
 
@@ -109,16 +110,22 @@ struct Prologue {
 #define IKV_DECODE_MIN_SPLIT_TOKENS 64
 #endif
 
-Plan plan_for(int n_head, int n_head_kv, int64_t n_kv) {
-  // Whole tiles per split; at most `target` splits per KV head, at most
-  // kMergeCap / G so that the merge's weights fit in LDS, and at least
-  // IKV_DECODE_MIN_SPLIT_TOKENS tokens per split.
+// Most splits per KV head any context gets: `target` workgroups over the KV
+// heads, at most kMergeCap / G so that the merge's weights fit in LDS.
+int max_splits(int n_head, int n_head_kv) {
   const int G = n_head / n_head_kv;
   // With one resident workgroup per CU, the workgroups past 256 would run as
   // a second wave behind the first: stay at one per CU.
   const int target_wgs = resident_wgs(G) >= 2 ? IKV_DECODE_TARGET_WGS : kCUs;
-  int64_t target = (target_wgs + n_head_kv - 1) / n_head_kv;
+  int target = (target_wgs + n_head_kv - 1) / n_head_kv;
   if (target > kMergeCap / G) target = kMergeCap / G;
+  return target;
+}
+
+Plan plan_for(int n_head, int n_head_kv, int64_t n_kv) {
+  // Whole tiles per split; at most max_splits per KV head and at least
+  // IKV_DECODE_MIN_SPLIT_TOKENS tokens per split.
+  int64_t target = max_splits(n_head, n_head_kv);
   const int64_t by_min = (n_kv + IKV_DECODE_MIN_SPLIT_TOKENS - 1) / IKV_DECODE_MIN_SPLIT_TOKENS;
   if (target > by_min) target = by_min;
   // Up to two tiles one workgroup per KV head is faster than any split: the
@@ -140,13 +147,16 @@ struct WsLayout {
 };
 
 // [n_head_kv counters, 256 B apart][n_head x n_splits x (max, sum)]
-// [n_head x n_splits x D]. The counters sit at offset 0 for every n_kv, so one
-// workspace serves every context length.
+// [n_head x n_splits x D]. The counters and the (max, sum) region sit at the
+// same offsets for every n_kv (the region is sized for max_splits), so one
+// workspace serves every context length: what one launch leaves zeroed there
+// is what the next one expects, and no launch's partial outputs land in it.
 WsLayout ws_layout(int n_head, int n_head_kv, int n_splits) {
   WsLayout w;
   w.counters = 0;
   w.part_ml = align256(sizeof(int) * kCounterStride * static_cast<size_t>(n_head_kv));
-  w.part_o = w.part_ml + align256(sizeof(float) * 2 * static_cast<size_t>(n_head) * n_splits);
+  w.part_o = w.part_ml + align256(sizeof(float) * 2 * static_cast<size_t>(n_head) *
+                                  max_splits(n_head, n_head_kv));
   w.total = w.part_o + sizeof(float) * static_cast<size_t>(n_head) * n_splits * D;
   return w;
 }
@@ -429,7 +439,6 @@ __global__ __launch_bounds__(WG, waves_per_simd(G)) void decode_kernel(
   __shared__ float s_m[NWAVE][G];
   __shared__ float s_l[NWAVE][G];
   __shared__ MergeLds s_merge;
-  __shared__ int s_last;
 
   const int g = blockIdx.x % n_head_kv;
   const int split = blockIdx.x / n_head_kv;
@@ -616,6 +625,7 @@ __global__ __launch_bounds__(WG, waves_per_simd(G)) void decode_kernel(
   __builtin_amdgcn_s_waitcnt(0);
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __syncthreads();
+  __shared__ int s_last;
   if (tid == 0) {
     int *ctr = counters + static_cast<size_t>(g) * kCounterStride;
     const int before = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -150,6 +150,24 @@ def test_decode_workspace_reuse_is_deterministic(dev):
     kh, vh = k.cpu().numpy(), v.cpu().numpy()
     want = oracle.flash_attn(q.cpu().numpy()[None], kh[:1500], vh[:1500], 1499)[0]
     assert_attn_close(small.cpu().numpy(), want, "ctx 1500 after 8200")
+    # one workspace through contexts whose split counts rise and fall: every
+    # launch equals a launch on a fresh workspace, bit for bit
+    for n in (8200, 1500, 300, 8200, 129, 4097, 200, 8199, 65, 3000):
+        got = ikv.attn_decode(q, k, v, n, workspace=ws).clone()
+        fresh = ikv.attn_decode(q, k, v, n)
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(got.cpu().numpy()), bits(fresh.cpu().numpy())), n
+    # the same with four query heads per KV head
+    # (the split count is not monotone in the context: size for the largest)
+    q4 = rand(g, (32, D))
+    ns = (8200, 700, 8200, 1999)
+    nbytes = max(ikv.decode_workspace_bytes(32, 8, D, n) for n in ns)
+    ws4 = torch.zeros((nbytes + 3) // 4, device=dev)
+    for n in ns:
+        got = ikv.attn_decode(q4, k, v, n, workspace=ws4).clone()
+        fresh = ikv.attn_decode(q4, k, v, n)
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(got.cpu().numpy()), bits(fresh.cpu().numpy())), n
 
 
 # ---------------------------------------------------------------------------
