@@ -287,3 +287,17 @@ def test_decode_with_qk_rope_bad_position_is_flagged(dev):
                          dev_t(s, dev), dev_t(c, dev), status=status)
     assert int(host(status)[0]) == 1
     assert not host(kc)[10].any()       # the appended key row is zeros, not garbage
+
+
+def test_engine_from_gguf_file_equals_synthetic_init(dev, tmp_path):
+    from ikv import gguf
+    cfg = qwen3.Qwen3Config(n_layer=2, n_vocab=4096, n_ctx_train=4096)
+    path = tmp_path / "small.gguf"
+    gguf.write_qwen3_synthetic(path, cfg, seed=0xABC, threads=4)
+    prompt = synth.uniform_ints(5, 24, cfg.n_vocab)
+    a = gguf.load_qwen3(path, 128)
+    b = qwen3.Qwen3Engine(cfg, 128)
+    b.init_synthetic(0xABC)
+    assert a.generate(prompt, 20)[0] == b.generate(prompt, 20)[0]
+    a.close()
+    b.close()
