@@ -187,6 +187,37 @@ def time_prefill(torch, ikv, p, reps):
     return e0.elapsed_time(e1) / 1e3 / reps
 
 
+def prefill_only(torch, ikv, p, reps):
+    """BASELINE config 2 at one prompt length: the append of p K and V rows
+    into a 28-layer contiguous cache and the causal GQA prefill of p tokens,
+    each timed over `reps` launches per layer with HIP events."""
+    dev = torch.device("cuda:0")
+    t_pre = time_prefill(torch, ikv, p, reps)
+    g = torch.Generator(device=dev)
+    g.manual_seed(0x1F0000 + 2000 + p + 1)
+    rows = torch.randn((p, N_HEAD_KV, D), generator=g, device=dev)
+    caches = [torch.empty((p, N_HEAD_KV, D), device=dev) for _ in range(N_LAYER)]
+    for c in caches:
+        ikv.append(c, rows)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        for c in caches:
+            ikv.append(c, rows)
+    e1.record()
+    torch.cuda.synchronize()
+    t_app = e0.elapsed_time(e1) / 1e3 / reps / N_LAYER
+    nbytes = 2 * p * N_HEAD_KV * D * 4  # read and written once
+    tf = prefill_flops(p) / t_pre / 1e12
+    return {"prefill": {"P": p, "us": round(t_pre * 1e6, 2), "tflops": round(tf, 2),
+                        "mfma_frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)},
+            "append": {"rows": p, "us": round(t_app * 1e6, 2), "bytes": nbytes,
+                       "gbs": round(nbytes / t_app / 1e9, 1),
+                       "frac": round(nbytes / t_app / 1e9 / HBM_PEAK_GBS, 4)}}
+
+
 def hbm_probes(torch, ikv):
     """What this box sustains, measured in the same run: a long streaming read
     (897 MiB per kernel), a streaming read of one decode layer's size (33.6 MB
@@ -434,6 +465,9 @@ def main():
     ap.add_argument("--traffic-from", nargs=4, metavar=("FETCH", "WRITE", "CAL_FETCH", "CAL_WRITE"),
                     help="summarise four rocprofv3 --pmc output folders into the traffic file "
                          "(no GPU needed)")
+    ap.add_argument("--prefill-only", type=int, default=0, metavar="P",
+                    help="only the prefill attention and the KV append of P prompt tokens "
+                         "(BASELINE config 2 shape); prints their JSON (for counter runs)")
     ap.add_argument("--pmc-calibrate", action="store_true",
                     help="only run 3 copies of 256 MiB through ikv_append_f32 (counter calibration)")
     args = ap.parse_args()
@@ -465,6 +499,9 @@ def main():
                           "bytes_written": n, "dispatches": 3}), flush=True)
         return
     log(f"[bench] {ikv.version()} on {torch.cuda.get_device_name(0)}")
+    if args.prefill_only:
+        print(json.dumps(prefill_only(torch, ikv, args.prefill_only, args.steps)), flush=True)
+        return
     if args.model_only:
         configs = [int(c) for c in args.model_configs.split(",") if c.strip()]
         print(json.dumps({"model": model_bench(configs, 0 if args.no_cpu else args.cpu_model_tokens)}),
