@@ -56,6 +56,10 @@ constexpr float kRescale = 8.0f;    // log2 headroom before the running max is m
 #ifndef IKV_PREFILL_NW
 #define IKV_PREFILL_NW 0  // waves per workgroup; 0 = chosen per launch
 #endif
+#ifndef IKV_PREFILL_SPLIT
+#define IKV_PREFILL_SPLIT 1  // 8-wave workgroups (two key-split groups) at one block per CU
+#endif
+constexpr int kCUs = 256;  // MI355X compute units
 
 __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -84,29 +88,40 @@ __global__ __launch_bounds__(NW * 64) void prefill_kernel(const float *__restric
                                                           int n_q, int n_kv, int n_past,
                                                           int n_blocks, int paired,
                                                           float scale_log2, ikv::Pages pages) {
-  constexpr int BQ = NW * 16 / G;
-  // [buffer][K | V]; K rows hold 16-byte chunk c at slot c ^ (key & 15)
-  __shared__ __attribute__((aligned(16))) float s_buf0[2 * TILE];
-  __shared__ __attribute__((aligned(16))) float s_buf1[2 * TILE];
+  // NW = 8: two groups of 4 waves hold the same query rows and take
+  // alternate key tiles (group r: tiles r, r + 2, ...), merging their softmax
+  // states at the end, so that each SIMD runs two waves.
+  constexpr int NG = NW == 8 ? 2 : 1;  // wave groups
+  constexpr int WPG = NW / NG;         // waves per group
+  constexpr int BQ = WPG * 16 / G;
+  // [group][buffer][K | V]; K rows hold 16-byte chunk c at slot c ^ (key & 15)
+  __shared__ __attribute__((aligned(16))) float s_buf[NG][2][2 * TILE];
 
   const int g = blockIdx.x % n_head_kv;
   const int item = blockIdx.x / n_head_kv;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  int grp = 0, w = wave;  // group, wave within the group
+  if constexpr (NG == 2) {
+    grp = wave / WPG;
+    w = wave - grp * WPG;
+  }
+  float *const buf0 = s_buf[grp][0];
+  float *const buf1 = s_buf[grp][1];
   const int kk = lane >> 4;
   const int j = lane & 15;
-  const int row = wave * 16 + j;
+  const int row = w * 16 + j;
   const int n_head = n_head_kv * G;
 
-  // this wave's share of one tile: chunks c = wave + NW*i, 1 KB (2 keys) each.
+  // this wave's share of one tile: chunks c = w + WPG*i, 1 KB (2 keys) each.
   // A paged cache's block (a multiple of 64 keys) holds every tile whole, so
   // one block offset serves the tile.
   auto issue = [&](float *buf, int tile) {
     int64_t shift = 0;
     if constexpr (PAGED) shift = ikv::page_shift(pages, tile * BN);
 #pragma unroll
-    for (int i = 0; i < 16 / NW; ++i) {
-      const int c = wave + NW * i;
+    for (int i = 0; i < 16 / WPG; ++i) {
+      const int c = w + WPG * i;
       const int key = 2 * c + (lane >> 5);
       const int slot = lane & 31;
       const int kg = min(tile * BN + key, n_kv - 1);
@@ -135,8 +150,8 @@ __global__ __launch_bounds__(NW * 64) void prefill_kernel(const float *__restric
     const int k_end = min(n_kv, n_past + last_tok + 1);
     const int n_tiles = (k_end + BN - 1) / BN;
 
-    __syncthreads();  // the previous item's readers are done with both buffers
-    issue(s_buf0, 0);
+    __syncthreads();  // the previous item's readers are done with the buffers
+    if (grp < n_tiles) issue(buf0, grp);
 
     float4 qr[8];
     {
@@ -151,7 +166,7 @@ __global__ __launch_bounds__(NW * 64) void prefill_kernel(const float *__restric
     for (int t = 0; t < 8; ++t) o[t] = floatx4{0.f, 0.f, 0.f, 0.f};
     float m_row = -INFINITY, l_part = 0.f;
 
-    auto step = [&](const float *buf, int tile, float *nbuf, bool more) {
+    auto step = [&](const float *buf, int tile, float *nbuf, bool more, int next) {
       floatx4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
       // K fragments are read one step ahead so LDS latency hides under MFMAs
       float4 ka0 = *reinterpret_cast<const float4 *>(buf + koff[0]);
@@ -183,7 +198,7 @@ __global__ __launch_bounds__(NW * 64) void prefill_kernel(const float *__restric
         __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
       }
       __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-      if (more) issue(nbuf, tile + 1);
+      if (more) issue(nbuf, next);
       const int kbase = tile * BN;
       float p[8];
 #pragma unroll
@@ -204,15 +219,20 @@ __global__ __launch_bounds__(NW * 64) void prefill_kernel(const float *__restric
       // move the row's reference max only when a score exceeds it by 2^8
       if (__builtin_amdgcn_ballot_w64(mt > m_row + kRescale) != 0) {
         const float m_new = fmaxf(m_row, row_max4(mt));
-        const float alpha = ikv::fast_exp2(m_row - m_new);
+        float alpha = ikv::fast_exp2(m_row - m_new);
+        // a second group's row can see only masked keys in its first tiles
+        // (its tile 1 lies past an early query): keep -inf - -inf out
+        if constexpr (NG == 2) alpha = (m_new == -INFINITY) ? 1.f : alpha;
         m_row = m_new;
         l_part *= alpha;
 #pragma unroll
         for (int t = 0; t < 8; ++t) o[t] *= alpha;
       }
+      float ref = m_row;
+      if constexpr (NG == 2) ref = (m_row == -INFINITY) ? 0.f : m_row;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        p[i] = ikv::fast_exp2(p[i] - m_row);
+        p[i] = ikv::fast_exp2(p[i] - ref);
         l_part += p[i];
       }
 #pragma unroll
@@ -246,18 +266,49 @@ __global__ __launch_bounds__(NW * 64) void prefill_kernel(const float *__restric
       __builtin_amdgcn_sched_group_barrier(0x008, 16, 1);
     };
 
-    for (int tile = 0; tile < n_tiles; tile += 2) {
-      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's loads of `tile` landed
-      __syncthreads();                      // everyone's landed; buffer 1 is free
-      step(s_buf0, tile, s_buf1, tile + 1 < n_tiles);
-      if (tile + 1 >= n_tiles) break;
+    // Rounds of NG tiles, one per group, alternating the buffers.
+    for (int t0 = 0; t0 < n_tiles; t0 += 2 * NG) {
+      const int ta = t0 + grp;
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's loads of its tile landed
+      __syncthreads();                      // everyone's landed; the other buffers are free
+      if (ta < n_tiles) step(buf0, ta, buf1, ta + NG < n_tiles, ta + NG);
+      if (t0 + NG >= n_tiles) break;
+      const int tb = t0 + NG + grp;
       __builtin_amdgcn_s_waitcnt(0x0F70);
       __syncthreads();
-      step(s_buf1, tile + 1, s_buf0, tile + 2 < n_tiles);
+      if (tb < n_tiles) step(buf1, tb, buf0, tb + NG < n_tiles, tb + NG);
+    }
+
+    if constexpr (NG == 2) {
+      // Group 1 hands its (O, max, per-lane sum) to group 0 through LDS
+      // (the tile buffers are free now); group 0 merges and writes.
+      __syncthreads();
+      float *xch = s_buf[0][0] + (w * 64 + lane) * 34;
+      if (grp == 1) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) xch[4 * t + r] = o[t][r];
+        xch[32] = m_row;
+        xch[33] = l_part;
+      }
+      __syncthreads();
+      if (grp == 0) {
+        const float mb = xch[32];
+        const float M = fmaxf(m_row, mb);
+        const float a = (m_row == -INFINITY) ? 0.f : ikv::fast_exp2(m_row - M);
+        const float b = (mb == -INFINITY) ? 0.f : ikv::fast_exp2(mb - M);
+        l_part = l_part * a + xch[33] * b;
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) o[t][r] = o[t][r] * a + xch[4 * t + r] * b;
+        m_row = M;
+      }
     }
 
     const float l_row = row_sum4(l_part);
-    if (row_ok) {
+    if (row_ok && grp == 0) {
       const float inv = 1.0f / l_row;
       float *op = out + (static_cast<size_t>(tok) * n_head + head) * D;
 #pragma unroll
@@ -278,7 +329,7 @@ template <int G, int NW>
 void launch_nw(const float *q, const float *k, const float *v, float *out, int n_head_kv, int n_q,
                int n_kv, int n_past, float scale_log2, int paired, const ikv::Pages *pg,
                hipStream_t s) {
-  constexpr int BQ = NW * 16 / G;
+  constexpr int BQ = (NW == 8 ? 4 : NW) * 16 / G;
   const int n_blocks = (n_q + BQ - 1) / BQ;
   const int items = paired ? (n_blocks + 1) / 2 : n_blocks;
   if (pg)
@@ -301,7 +352,12 @@ void launch(const float *q, const float *k, const float *v, float *out, int n_he
   if (nw == 0) nw = blocks(4) * n_head_kv >= IKV_PREFILL_PAIR_MIN_WGS ? 4 : 2;
   const int nb = blocks(nw);
   const int paired = (nb >= 2 && (nb + 1) / 2 * n_head_kv >= IKV_PREFILL_PAIR_MIN_WGS) ? 1 : 0;
-  if (nw == 4)
+  // With at most one 4-wave workgroup per CU, each SIMD would run one wave:
+  // give every block a second wave group instead (NW = 8).
+  if (nw == 4 && IKV_PREFILL_SPLIT && n_head_kv * (paired ? (nb + 1) / 2 : nb) <= kCUs) nw = 8;
+  if (nw == 8)
+    launch_nw<G, 8>(q, k, v, out, n_head_kv, n_q, n_kv, n_past, scale_log2, paired, pg, s);
+  else if (nw == 4)
     launch_nw<G, 4>(q, k, v, out, n_head_kv, n_q, n_kv, n_past, scale_log2, paired, pg, s);
   else
     launch_nw<G, 2>(q, k, v, out, n_head_kv, n_q, n_kv, n_past, scale_log2, paired, pg, s);
