@@ -40,8 +40,9 @@
 // order (the reference's loop), and all lanes then normalise and rotate the
 // RoPE pairs with the resident sin/cos tables — the arithmetic of
 // ikv_qk_norm_rope_f32 with contraction off, so the key row appended to the
-// cache is bit-identical to the one the separate ops produce. The K/V loads of
-// the first tile are issued before this prologue and land during it.
+// cache is bit-identical to the one the separate ops produce. The prologue's
+// loads are issued first and the first tile's K/V loads right after them, so
+// the prologue's arithmetic runs while the tile is in flight.
 #include "ikv_common.hpp"
 #include "../../include/ikv.h"
 
@@ -247,52 +248,126 @@ __device__ __forceinline__ void merge_waves(const float (&s_acc)[NWAVE][G][D],
   }
 }
 
-// Stages q rows g*G .. g*G+G-1 and the new key row of KV head g into s, then
-// applies RMSNorm (ordered double sum per row, one lane per row) and NeoX
-// RoPE at position pos[0]: s[h] = rope(norm(q_h)), s[G] = rope(norm(k_g)).
-// A position outside [0, n_ctx) gives zero rows and raises *status.
+// The register stage of the folded qk-norm + RoPE prologue: this thread's
+// elements of q rows g*G .. g*G+G-1 and of the new key row of KV head g, and
+// for its RoPE pairs the norm weights and the sin/cos of row n_kv - 1 (the
+// new token's position whenever the caller's positions follow the cache, as
+// in a decode step). The kernel issues these loads before those of its first
+// K/V tile, so that waiting for them does not wait for the tile, and the
+// prologue's arithmetic runs while the tile is in flight.
+// Row stride of the prologue's LDS rows: 4 floats of padding put the G+1
+// rows that the summing lanes read in lockstep on different banks.
+constexpr int kRowPad = D + 4;
+
 template <int G>
-__device__ __forceinline__ void qk_prologue(const Prologue &pro, const float *q, const float *k_new, int g,
-                            float (&s)[G + 1][D], float (&scl)[G + 1]) {
-#pragma clang fp contract(off)
-  const int tid = threadIdx.x;
-  const int32_t p = pro.pos[0];
-  const bool ok = p >= 0 && p < pro.n_ctx;
-  constexpr int hd = D / 2;
-  // This thread's RoPE pairs (row r, index j; i = tid + u * WG) and their
-  // norm weights and sin/cos, loaded first so that they arrive while the rows
-  // are staged and their norms are summed. A position outside the table
-  // reads row 0 (in bounds) and the result is zeroed below.
-  constexpr int n_pairs = (G + 1) * hd;
-  constexpr int PPT = (n_pairs + WG - 1) / WG;
+struct ProStage {
+  static constexpr int hd = D / 2;
+  static constexpr int n_el = (G + 1) * D;
+  static constexpr int EPT = (n_el + WG - 1) / WG;
+  static constexpr int n_pairs = (G + 1) * hd;
+  static constexpr int PPT = (n_pairs + WG - 1) / WG;
+  float el[EPT];
   float w0[PPT], w1[PPT], cs[PPT], sn[PPT];
-  const int64_t prow = static_cast<int64_t>(ok ? p : 0) * hd;
+  int32_t p;
+  int spec;
+};
+
+template <int G>
+__device__ __forceinline__ void qk_prologue_load(const Prologue &pro, const float *q, const float *k_new,
+                                                 int g, int n_kv, ProStage<G> &st) {
+  using S = ProStage<G>;
+  const int tid = threadIdx.x;
 #pragma unroll
-  for (int u = 0; u < PPT; ++u) {
+  for (int u = 0; u < S::EPT; ++u) {
     const int i = tid + u * WG;
-    if (i < n_pairs) {
-      const int r = i / hd;
-      const int j = i - r * hd;
-      const float *w = r < G ? pro.q_norm_w : pro.k_norm_w;
-      w0[u] = w[j];
-      w1[u] = w[j + hd];
-      cs[u] = pro.cos_tab[prow + j];
-      sn[u] = pro.sin_tab[prow + j];
+    if (i < S::n_el) {
+      const int r = i / D;
+      const int d = i - r * D;
+      st.el[u] = r < G ? q[static_cast<size_t>(g * G + r) * D + d] : k_new[static_cast<size_t>(g) * D + d];
     }
   }
-  for (int i = tid; i < (G + 1) * D; i += WG) {
-    const int r = i / D;
-    const int d = i - r * D;
-    s[r][d] = r < G ? q[static_cast<size_t>(g * G + r) * D + d] : k_new[static_cast<size_t>(g) * D + d];
+  st.spec = min(n_kv - 1, static_cast<int>(min(pro.n_ctx, static_cast<int64_t>(INT_MAX))) - 1);
+#pragma unroll
+  for (int u = 0; u < S::PPT; ++u) {
+    const int i = tid + u * WG;
+    if (i < S::n_pairs) {
+      const int r = i / S::hd;
+      const int j = i - r * S::hd;
+      const float *w = r < G ? pro.q_norm_w : pro.k_norm_w;
+      st.w0[u] = w[j];
+      st.w1[u] = w[j + S::hd];
+      st.cs[u] = pro.cos_tab[static_cast<int64_t>(st.spec) * S::hd + j];
+      st.sn[u] = pro.sin_tab[static_cast<int64_t>(st.spec) * S::hd + j];
+    }
+  }
+  st.p = pro.pos[0];
+}
+
+// Completes the prologue from the register stage: s[h] = rope(norm(q_h)),
+// s[G] = rope(norm(k_g)), RMSNorm with an ordered double sum per row (one
+// lane per row) and NeoX RoPE at position pos[0]; if pos[0] is not the row
+// staged, that row's sin/cos are loaded here. A position outside
+// [0, n_ctx) reads row 0 (in bounds), gives zero rows and raises *status.
+template <int G>
+__device__ __forceinline__ void qk_prologue(const Prologue &pro, ProStage<G> &st,
+                                            float (&s)[G + 1][kRowPad], float (&scl)[G + 1]) {
+#pragma clang fp contract(off)
+  using S = ProStage<G>;
+  const int tid = threadIdx.x;
+  constexpr int hd = S::hd;
+  constexpr int n_pairs = S::n_pairs;
+  constexpr int PPT = S::PPT;
+  float(&w0)[PPT] = st.w0;
+  float(&w1)[PPT] = st.w1;
+  float(&cs)[PPT] = st.cs;
+  float(&sn)[PPT] = st.sn;
+  const int32_t p = st.p;
+  const bool ok = p >= 0 && p < pro.n_ctx;
+  const int prow = ok ? p : 0;
+  if (prow != st.spec) {
+#pragma unroll
+    for (int u = 0; u < PPT; ++u) {
+      const int i = tid + u * WG;
+      if (i < n_pairs) {
+        const int j = i - (i / hd) * hd;
+        cs[u] = pro.cos_tab[static_cast<int64_t>(prow) * hd + j];
+        sn[u] = pro.sin_tab[static_cast<int64_t>(prow) * hd + j];
+      }
+    }
+    // These loads were issued after the first tile's. Waiting for them here
+    // (vmcnt(0); expcnt and lgkmcnt left at their maxima) keeps that wait on
+    // this rare path: otherwise the compiler's wait where the paths join
+    // would also hold the common path until its tile has landed.
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+  }
+#pragma unroll
+  for (int u = 0; u < S::EPT; ++u) {
+    const int i = tid + u * WG;
+    if (i < S::n_el) s[i / D][i - (i / D) * D] = st.el[u];
   }
   __syncthreads();
   if (tid <= G) {
+    // In index order, as the reference's loop. The row's next 8 floats are
+    // read from LDS while the current 8 are added, so the chain of dependent
+    // double adds is not broken up by LDS round trips.
+    const float4 *row = reinterpret_cast<const float4 *>(&s[tid][0]);
     double sum = 0.0;
-#pragma unroll 8
-    for (int d = 0; d < D; ++d) {
-      const float xv = s[tid][d];
-      const float sq = xv * xv;
-      sum += static_cast<double>(sq);
+    float4 a = row[0], b = row[1];
+#pragma unroll
+    for (int c = 0; c < D / 8; ++c) {
+      float4 na = a, nb = b;
+      if (c + 1 < D / 8) {
+        na = row[2 * c + 2];
+        nb = row[2 * c + 3];
+      }
+      const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float sq = v[e] * v[e];
+        sum += static_cast<double>(sq);
+      }
+      a = na;
+      b = nb;
     }
     scl[tid] = static_cast<float>(1.0 / sqrt(sum / static_cast<double>(D) + static_cast<double>(pro.eps)));
   }
@@ -466,15 +541,17 @@ __global__ __launch_bounds__(WG, waves_per_simd(G)) void decode_kernel(
   // Two register buffers of K/V rows: tile t+1 loads into one while tile t
   // is scored from the other.
   float4 ka[R], va[R], kb[R], vb[R];
+  ProStage<G> st;
+  if constexpr (PRO) qk_prologue_load<G>(pro, q, k_new, g, n_kv, st);
   load_tile(ka, va, t_begin, t_end - 1, wave, half, new_row, kc, vc, k_new, v_new, tok_stride,
             head_off, shift_of(t_begin));
 
   float4 qv[G];
   float4 knew_rot = make_float4(0.f, 0.f, 0.f, 0.f);  // this lane's piece of rope(norm(k_new))
   if constexpr (PRO) {
-    __shared__ float s_qk[G + 1][D];
+    __shared__ float s_qk[G + 1][kRowPad];
     __shared__ float s_scl[G + 1];
-    qk_prologue<G>(pro, q, k_new, g, s_qk, s_scl);
+    qk_prologue<G>(pro, st, s_qk, s_scl);
 #pragma unroll
     for (int h = 0; h < G; ++h) qv[h] = *reinterpret_cast<const float4 *>(&s_qk[h][4 * sub]);
     knew_rot = *reinterpret_cast<const float4 *>(&s_qk[G][4 * sub]);
