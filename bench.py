@@ -527,10 +527,17 @@ def main():
         if t.get("ctx") == args.ctx:
             traffic = t.get("hbm_bytes_per_launch")
 
-    extra = {"eager_gbs": None, "ctx_sweep_gbs": {}, "short_ctx_us": {}, "g4_ctx4096": None,
-             "paged_ctx4096_gbs": {},
+    extra = {"repeats": None, "eager_gbs": None, "ctx_sweep_gbs": {}, "short_ctx_us": {},
+             "g4_ctx4096": None, "paged_ctx4096_gbs": {},
              "mall_hot_gbs": None, "prefill": {}, "hbm_probes": None, "model": None}
     if not args.no_extra:
+        # Five more timed regions of the same K steps (no warmup between them):
+        # their spread and median, beside the single region `value` reports.
+        reps = sorted(bpl * launches / rig.time(args.steps, 0) / 1e9 for _ in range(5))
+        extra["repeats"] = {"n": 5, "steps_each": args.steps, "median_gbs": round(reps[2], 1),
+                            "min_gbs": round(reps[0], 1), "max_gbs": round(reps[-1], 1)}
+        log(f"[bench] 5 repeats of {args.steps} steps: median {reps[2]:.1f} GB/s "
+            f"(min {reps[0]:.1f}, max {reps[-1]:.1f})")
         rig.graph = None
         es = rig.time(max(args.steps // 2, 5), 2)
         extra["eager_gbs"] = round(bpl * max(args.steps // 2, 5) * N_LAYER / es / 1e9, 1)
