@@ -510,10 +510,11 @@ __global__ __launch_bounds__(WG, waves_per_simd(G)) void decode_kernel(
     const float *__restrict__ q, float *kc, float *vc, const float *k_new, const float *v_new,
     float *__restrict__ out, int *counters, float *part_ml, float *part_o, int n_head_kv, int n_kv,
     int tokens_per_split, int n_splits, float scale_log2, Prologue pro, ikv::Pages pages) {
-  __shared__ float s_acc[NWAVE][G][D];
+  // Arrays read or written as float4 are declared 16-byte aligned.
+  __shared__ __attribute__((aligned(16))) float s_acc[NWAVE][G][D];
   __shared__ float s_m[NWAVE][G];
   __shared__ float s_l[NWAVE][G];
-  __shared__ MergeLds s_merge;
+  __shared__ __attribute__((aligned(16))) MergeLds s_merge;
 
   const int g = blockIdx.x % n_head_kv;
   const int split = blockIdx.x / n_head_kv;
@@ -549,7 +550,7 @@ __global__ __launch_bounds__(WG, waves_per_simd(G)) void decode_kernel(
   float4 qv[G];
   float4 knew_rot = make_float4(0.f, 0.f, 0.f, 0.f);  // this lane's piece of rope(norm(k_new))
   if constexpr (PRO) {
-    __shared__ float s_qk[G + 1][kRowPad];
+    __shared__ __attribute__((aligned(16))) float s_qk[G + 1][kRowPad];
     __shared__ float s_scl[G + 1];
     qk_prologue<G>(pro, st, s_qk, s_scl);
 #pragma unroll

@@ -28,12 +28,14 @@
 //    input (ikv_model.h) use the same order, so fused and unfused paths agree
 //    bit for bit.
 //
-// Short rows: each workgroup is one wavefront owning up to 64 rows, loaded
-// with coalesced accesses into LDS (row stride dim+1 floats, so the per-lane
-// row walks are bank-conflict free); lane r sums row r; then every lane
-// takes elements (or RoPE pairs) of the block in turn, so weights, sin/cos
-// and outputs move coalesced. Rows are independent and each output element is
-// written by the lane that read its inputs, so x == out (in place) is safe.
+// Short rows: each workgroup is 4 wavefronts owning up to 16 rows. It issues
+// all of its row loads at once (coalesced, float4 when aligned) together with
+// the positions, norm weights and sin/cos rows of its first RoPE pairs, then
+// stages the rows in LDS (row stride dim+1 floats, so the per-lane row walks
+// are bank-conflict free); lane r sums row r while the RoPE inputs land; then
+// every thread takes elements (or RoPE pairs) of the block in turn, so
+// weights, sin/cos and outputs move coalesced. A block stages all its rows
+// before writing any output, so x == out (in place) is safe.
 #pragma clang fp contract(off)
 
 #include "ikv_common.hpp"
@@ -43,60 +45,172 @@
 
 namespace {
 
-constexpr int kLdsFloats = 64 * 129;  // 33 KB: 64 rows of 128, or fewer longer rows
+constexpr int kLdsFloats = 64 * 129;  // 33 KB: the largest short-row block staged in LDS
 constexpr int kLongRow = 512;
+constexpr int kRowThreads = 256;     // 4 wavefronts per short-row block
+constexpr int kMaxRows = 16;         // rows per short-row block
+// Staging registers per thread: every float (or float4) of the largest block.
+constexpr int kStage = (kLdsFloats + kRowThreads - 1) / kRowThreads;
+constexpr int kStage4 = (kLdsFloats / 4 + kRowThreads - 1) / kRowThreads;
+// RoPE pairs per thread whose position, sin/cos and weights are loaded before
+// the sums (all of them for head_dim 128); further pairs load afterwards.
+constexpr int kPairPF = 4;
 
 int rows_per_block(int dim) {
   int r = kLdsFloats / (dim + 1);
-  if (r > 64) r = 64;
+  if (r > kMaxRows) r = kMaxRows;
   if (r < 1) r = 1;
   return r;
 }
 
 bool long_row(int64_t dim) { return dim >= kLongRow && dim % 256 == 0; }
 
+// The reference's ordered sum of one row's float squares in double
+// (cpu_backend.cpp:369), reading the row from LDS eight floats ahead of the
+// adds so that the chain of dependent double adds is not broken up by LDS
+// round trips.
+__device__ __forceinline__ double ordered_sq_sum(const float *rp, int dim) {
+  double sum = 0.0;
+  int c = 0;
+  float a[8];
+  if (dim >= 8) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) a[e] = rp[e];
+  }
+  for (; c + 8 <= dim; c += 8) {
+    float b[8];
+    const bool more = c + 16 <= dim;
+    if (more) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) b[e] = rp[c + 8 + e];
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float sq = a[e] * a[e];
+      sum += static_cast<double>(sq);
+    }
+    if (more) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) a[e] = b[e];
+    }
+  }
+  for (; c < dim; ++c) {
+    const float xv = rp[c];
+    const float sq = xv * xv;
+    sum += static_cast<double>(sq);
+  }
+  return sum;
+}
+
+// Short rows (head_dim rows of qk-norm and RoPE, rows shorter than kLongRow).
+// A block of 4 wavefronts owns up to kMaxRows rows. Every load the block needs
+// before its sums is issued at once: the rows (float4 when `vec`), and for
+// this thread's first kPairPF RoPE pairs the position, the norm weights and,
+// once the position is back, the sin/cos row; those land while lanes
+// 0..rows-1 of wavefront 0 run the ordered double sums. All of a block's rows
+// are staged in LDS before any output is written, so x == out is safe.
 template <bool NORM, bool ROPE>
-__global__ __launch_bounds__(64) void row_kernel(const float *__restrict__ x,
-                                                 const float *__restrict__ w, float *out,
-                                                 const int32_t *__restrict__ pos, int64_t rows,
-                                                 int dim, int rpb, float eps, int n_heads,
-                                                 const float *__restrict__ sin_tab,
-                                                 const float *__restrict__ cos_tab, int64_t n_ctx,
-                                                 int *status) {
+__global__ __launch_bounds__(kRowThreads) void row_kernel(const float *__restrict__ x,
+                                                          const float *__restrict__ w, float *out,
+                                                          const int32_t *__restrict__ pos, int64_t rows,
+                                                          int dim, int rpb, float eps, int n_heads,
+                                                          const float *__restrict__ sin_tab,
+                                                          const float *__restrict__ cos_tab,
+                                                          int64_t n_ctx, int *status, int vec) {
   extern __shared__ float lds[];
-  __shared__ float s_scale[64];
-  const int lane = threadIdx.x;
+  __shared__ float s_scale[kMaxRows];
+  const int tid = threadIdx.x;
   const int64_t row0 = static_cast<int64_t>(blockIdx.x) * rpb;
   const int64_t left = rows - row0;
   const int nr = static_cast<int>(left < rpb ? left : rpb);
   const int stride = dim + 1;
   const int total = nr * dim;
-
+  const int hd = dim / 2;
+  const int n_pairs = ROPE ? nr * hd : 0;
   const float *xb = x + row0 * dim;
-  for (int i = lane; i < total; i += 64) {
-    const int r = i / dim;
-    const int c = i - r * dim;
-    lds[r * stride + c] = xb[i];
+
+  // Stage the rows: all loads first, then the LDS stores.
+  if (vec) {
+    const float4 *xb4 = reinterpret_cast<const float4 *>(xb);
+    const int total4 = total >> 2;
+    float4 v[kStage4];
+#pragma unroll
+    for (int k = 0; k < kStage4; ++k) {
+      const int i = tid + k * kRowThreads;
+      if (i < total4) v[k] = xb4[i];
+    }
+#pragma unroll
+    for (int k = 0; k < kStage4; ++k) {
+      const int i = tid + k * kRowThreads;
+      if (i < total4) {
+        const int e = 4 * i;  // dim % 4 == 0: the four floats share a row
+        const int r = e / dim;
+        float *d = &lds[r * stride + (e - r * dim)];
+        d[0] = v[k].x;
+        d[1] = v[k].y;
+        d[2] = v[k].z;
+        d[3] = v[k].w;
+      }
+    }
+  } else {
+    float v[kStage];
+#pragma unroll
+    for (int k = 0; k < kStage; ++k) {
+      const int i = tid + k * kRowThreads;
+      if (i < total) v[k] = xb[i];
+    }
+#pragma unroll
+    for (int k = 0; k < kStage; ++k) {
+      const int i = tid + k * kRowThreads;
+      if (i < total) {
+        const int r = i / dim;
+        lds[r * stride + (i - r * dim)] = v[k];
+      }
+    }
+  }
+
+  // RoPE inputs of this thread's first pairs, in flight during the sums.
+  int32_t pp[kPairPF];
+  float w0[kPairPF], w1[kPairPF], cs[kPairPF], sn[kPairPF];
+  if constexpr (ROPE) {
+#pragma unroll
+    for (int k = 0; k < kPairPF; ++k) {
+      const int i = tid + k * kRowThreads;
+      pp[k] = -1;
+      if (i < n_pairs) {
+        const int r = i / hd;
+        const int j = i - r * hd;
+        pp[k] = pos[(row0 + r) / n_heads];
+        if (NORM) {
+          w0[k] = w[j];
+          w1[k] = w[j + hd];
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kPairPF; ++k) {
+      const int i = tid + k * kRowThreads;
+      cs[k] = 0.0f;
+      sn[k] = 0.0f;
+      if (i < n_pairs && pp[k] >= 0 && pp[k] < n_ctx) {
+        const int j = i - (i / hd) * hd;
+        cs[k] = cos_tab[static_cast<int64_t>(pp[k]) * hd + j];
+        sn[k] = sin_tab[static_cast<int64_t>(pp[k]) * hd + j];
+      }
+    }
   }
   __syncthreads();
 
-  if (NORM && lane < nr) {
-    const float *rp = &lds[lane * stride];
-    double sum = 0.0;
-#pragma unroll 8
-    for (int c = 0; c < dim; ++c) {
-      const float xv = rp[c];
-      const float sq = xv * xv;
-      sum += static_cast<double>(sq);
-    }
-    s_scale[lane] =
+  if (NORM && tid < nr) {
+    const double sum = ordered_sq_sum(&lds[tid * stride], dim);
+    s_scale[tid] =
         static_cast<float>(1.0 / sqrt(sum / static_cast<double>(dim) + static_cast<double>(eps)));
   }
   __syncthreads();
 
   float *ob = out + row0 * dim;
   if (!ROPE) {
-    for (int i = lane; i < total; i += 64) {
+    for (int i = tid; i < total; i += kRowThreads) {
       const int r = i / dim;
       const int c = i - r * dim;
       const float t = lds[r * stride + c] * s_scale[r];
@@ -104,8 +218,10 @@ __global__ __launch_bounds__(64) void row_kernel(const float *__restrict__ x,
     }
     return;
   }
-  const int hd = dim / 2;
-  for (int i = lane; i < nr * hd; i += 64) {
+  // One pair: x0 = x[j], x1 = x[j + hd] (normed first when NORM), rotated by
+  // the angle of its token's position; a position outside the table gives a
+  // zero pair and raises *status.
+  auto rotate = [&](int i, int32_t p, float wa, float wb, float c, float s) {
     const int r = i / hd;
     const int j = i - r * hd;
     float x0 = lds[r * stride + j];
@@ -114,16 +230,13 @@ __global__ __launch_bounds__(64) void row_kernel(const float *__restrict__ x,
       const float sc = s_scale[r];
       const float t0 = x0 * sc;
       const float t1 = x1 * sc;
-      x0 = t0 * w[j];
-      x1 = t1 * w[j + hd];
+      x0 = t0 * wa;
+      x1 = t1 * wb;
     }
-    const int32_t p = pos[(row0 + r) / n_heads];
     float o0 = 0.0f, o1 = 0.0f;
     if (p < 0 || p >= n_ctx) {
       if (status) *status = 1;
     } else {
-      const float c = cos_tab[static_cast<int64_t>(p) * hd + j];
-      const float s = sin_tab[static_cast<int64_t>(p) * hd + j];
       const float a = x0 * c;
       const float b = x1 * s;
       const float e = x0 * s;
@@ -133,6 +246,20 @@ __global__ __launch_bounds__(64) void row_kernel(const float *__restrict__ x,
     }
     ob[static_cast<int64_t>(r) * dim + j] = o0;
     ob[static_cast<int64_t>(r) * dim + j + hd] = o1;
+  };
+#pragma unroll
+  for (int k = 0; k < kPairPF; ++k) {
+    const int i = tid + k * kRowThreads;
+    if (i < n_pairs) rotate(i, pp[k], NORM ? w0[k] : 0.0f, NORM ? w1[k] : 0.0f, cs[k], sn[k]);
+  }
+  for (int i = tid + kPairPF * kRowThreads; i < n_pairs; i += kRowThreads) {
+    const int r = i / hd;
+    const int j = i - r * hd;
+    const int32_t p = pos[(row0 + r) / n_heads];
+    const bool ok = p >= 0 && p < n_ctx;
+    const float c = ok ? cos_tab[static_cast<int64_t>(p) * hd + j] : 0.0f;
+    const float s = ok ? sin_tab[static_cast<int64_t>(p) * hd + j] : 0.0f;
+    rotate(i, p, NORM ? w[j] : 0.0f, NORM ? w[j + hd] : 0.0f, c, s);
   }
 }
 
@@ -164,8 +291,11 @@ int launch_rows(const float *x, const float *w, float *out, const int32_t *pos, 
   const int64_t blocks = (rows + rpb - 1) / rpb;
   if (blocks > INT_MAX) return -EOVERFLOW;
   const size_t shmem = sizeof(float) * static_cast<size_t>(rpb) * (dim + 1);
-  row_kernel<NORM, ROPE><<<static_cast<unsigned>(blocks), 64, shmem, static_cast<hipStream_t>(stream)>>>(
-      x, w, out, pos, rows, dim, rpb, eps, n_heads, sin_tab, cos_tab, n_ctx, status);
+  // float4 staging needs 16-byte rows: dim % 4 == 0 and x 16-byte aligned.
+  const int vec = (dim % 4 == 0 && ikv::aligned16(x)) ? 1 : 0;
+  row_kernel<NORM, ROPE><<<static_cast<unsigned>(blocks), kRowThreads, shmem,
+                           static_cast<hipStream_t>(stream)>>>(
+      x, w, out, pos, rows, dim, rpb, eps, n_heads, sin_tab, cos_tab, n_ctx, status, vec);
   return ikv::launch_status();
 }
 

@@ -242,7 +242,8 @@ def test_decode_steps_equal_prefill_rows_on_gpu(dev):
 # RMSNorm / RoPE (bit-exact)
 # ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize("rows,dim", [(1, 128), (24, 128), (65, 128), (49152, 128), (3, 1024), (7, 100)])
+@pytest.mark.parametrize("rows,dim", [(1, 128), (24, 128), (65, 128), (49152, 128), (3, 1024), (7, 100),
+                                      (33, 102), (5, 6), (17, 1000)])
 def test_rms_norm_bit_exact(dev, rows, dim):
     x = synth.normal(100 + rows, (rows, dim), std=3.0)
     w = synth.normal(200 + dim, (dim,))
@@ -283,6 +284,32 @@ def test_qk_norm_rope_bit_exact(dev, n_tokens, n_heads):
     want = oracle.rope_neox(oracle.rms_norm(x, w, 1e-6), pos, th)
     assert np.array_equal(bits(got.cpu().numpy()), bits(want))
     assert np.array_equal(bits(inplace.cpu().numpy()), bits(want))
+
+
+@pytest.mark.parametrize("n_tokens,n_heads,hd", [(7, 3, 6), (33, 5, 64), (40, 4, 256), (3, 2, 130)])
+def test_norm_rope_other_head_dims_and_unaligned_rows(dev, n_tokens, n_heads, hd):
+    # head_dim 256 gives each thread more RoPE pairs than it loads before the
+    # sums; 6 is shorter than one 8-float chunk of the ordered sum; 130 is not
+    # a multiple of 4 (scalar staging). The rows also run from an address
+    # 4 bytes past a 16-byte boundary, which takes the scalar staging path.
+    th = oracle.rope_theta_table(1e6, hd, 4096)
+    s, c = ikv.rope_sincos_table(th)
+    s, c = torch.from_numpy(s).to(dev), torch.from_numpy(c).to(dev)
+    x = synth.normal(500 + hd, (n_tokens, n_heads, hd), std=2.0)
+    w = synth.normal(501 + hd, (hd,))
+    pos = synth.uniform_ints(502 + hd, n_tokens, 4096)
+    pos_d, w_d = torch.from_numpy(pos).to(dev), torch.from_numpy(w).to(dev)
+    want_rope = oracle.rope_neox(x, pos, th)
+    want_qk = oracle.rope_neox(oracle.rms_norm(x, w, 1e-6), pos, th)
+    want_norm = oracle.rms_norm(x, w, 1e-6)
+    flat = torch.empty(x.size + 1, device=dev)
+    for xd in (torch.from_numpy(x).to(dev), flat[1:].view(x.shape).copy_(torch.from_numpy(x))):
+        got = ikv.rope_neox(xd, pos_d, s, c)
+        assert np.array_equal(bits(got.cpu().numpy()), bits(want_rope))
+        got = ikv.qk_norm_rope(xd, w_d, pos_d, 1e-6, s, c)
+        assert np.array_equal(bits(got.cpu().numpy()), bits(want_qk))
+        got = ikv.rms_norm(xd, w_d, 1e-6)
+        assert np.array_equal(bits(got.cpu().numpy()), bits(want_norm))
 
 
 def test_rope_bad_position_sets_status_without_fault(dev):
