@@ -99,6 +99,15 @@ Tensor *OpFactory::reshape(Graph &g, Tensor *x, std::initializer_list<int64_t> s
   return r;
 }
 
+Tensor *OpFactory::view_rows(Graph &g, Tensor *x, int64_t row0, int64_t n_rows, std::string_view name) {
+  assert(x->is_contiguous() && x->dims[2] == 1 && x->dims[3] == 1);
+  assert(row0 >= 0 && n_rows > 0 && row0 + n_rows <= x->dims[1]);
+  Tensor *r = new_node(g, name, x->dataType, {x->dims[0], n_rows, 1, 1}, OperationType::GGML_OP_VIEW);
+  r->src[0] = x;
+  r->offset = row0 * x->strides[1];
+  return r;
+}
+
 Tensor *append_kv(Graph &g, Tensor *current, const Tensor &writable, const Tensor &readable) {
   // The copies keep data pointing at the storage's cache memory.
   auto write = std::make_unique<Tensor>(writable);

@@ -37,6 +37,10 @@ struct OpFactory {
                             std::string_view name);
   static Tensor *reshape(Graph &g, Tensor *x, std::initializer_list<int64_t> shape,
                          std::string_view name);
+  // Rows [row0, row0 + n_rows) of a contiguous [dims0, rows] activation, as a
+  // VIEW node aliasing its bytes (data = x's data + offset, set when the
+  // scheduler places x; no kernel runs).
+  static Tensor *view_rows(Graph &g, Tensor *x, int64_t row0, int64_t n_rows, std::string_view name);
 };
 
 // KV append: a CPY node writing `current` into the writable cache view,

@@ -154,7 +154,14 @@ infer::expected<Graph, std::error_code> Qwen3Model::build_graph(GraphContext &ct
     Tensor *ffn_out = OpFactory::mul_mat(g, L.ffn_down, inter, "ffn_out_" + s);
     inpL = OpFactory::add(g, ffn_out, ffn_inp, "result_out_" + s);
   }
-  Tensor *final_norm = OpFactory::rms_norm(g, inpL, _output_norm, eps, "result_norm");
+  // The sampler reads only the last token's logits (reference
+  // src/sampler.cpp:5-35 reads row n_tokens - 1 of the full [vocab, n_tokens]
+  // result). The output norm and the projection act on each row alone, so
+  // computing them for the last row gives that row's values without the
+  // other n_tokens - 1 rows (a [vocab x n_embd] x [n_embd x n_tokens] GEMM at
+  // prefill).
+  Tensor *last = n_tokens > 1 ? OpFactory::view_rows(g, inpL, n_tokens - 1, 1, "result_last") : inpL;
+  Tensor *final_norm = OpFactory::rms_norm(g, last, _output_norm, eps, "result_norm");
   Tensor *logits = OpFactory::mul_mat(g, _token_embd, final_norm, "logits");  // tied output
   g.mark_output(logits);
   return g;
@@ -274,7 +281,7 @@ infer::expected<void, std::error_code> Qwen3Runner::enqueue_step(const int32_t *
   if (auto r = _sched->execute(*graph); !r) return abort(r.error());
   const Tensor *logits = graph->outputs().front();
   const int64_t vocab = logits->dims[0];
-  const float *row = static_cast<const float *>(logits->data) + (n - 1) * vocab;
+  const float *row = static_cast<const float *>(logits->data) + (logits->dims[1] - 1) * vocab;
   hipStream_t s = _backend.stream();
   // The sampler writes the token to the device slot the next step embeds
   // and to the pinned host slot the host reads once the event has fired.

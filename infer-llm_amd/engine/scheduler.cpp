@@ -4,6 +4,13 @@
 
 namespace {
 size_t align256(size_t b) { return (b + 255) & ~static_cast<size_t>(255); }
+
+// A VIEW node without memory of its own (OpFactory::view_rows): it takes its
+// source's bytes at its offset. KV-cache views are placed by their storage
+// when the graph is built and never reach this test.
+bool aliases_src(const Tensor *n) {
+  return n->op == OperationType::GGML_OP_VIEW && !n->data && n->src[0];
+}
 }  // namespace
 
 Scheduler::~Scheduler() {
@@ -57,6 +64,7 @@ infer::expected<void, std::error_code> Scheduler::execute(Graph &g) {
   for (Tensor *n : g.nodes()) {
     if (n->data) continue;
     if (n->op == OperationType::GGML_OP_RESHAPE && n->src[0] && n->src[0]->is_contiguous()) continue;
+    if (aliases_src(n)) continue;
     total += align256(n->byte_size());
   }
   if (total > _arena_bytes) {
@@ -78,6 +86,10 @@ infer::expected<void, std::error_code> Scheduler::execute(Graph &g) {
     if (n->data) continue;
     if (n->op == OperationType::GGML_OP_RESHAPE && n->src[0] && n->src[0]->is_contiguous()) {
       n->data = n->src[0]->data;  // same bytes, new shape
+      continue;
+    }
+    if (aliases_src(n)) {
+      n->data = static_cast<char *>(n->src[0]->data) + n->offset;  // rows of the source
       continue;
     }
     n->data = cursor;

@@ -235,6 +235,21 @@ static void cpu_tests() {
               g.nodes()[1]->data == cache_w.data && view->data == cache_r.data && g.leafs().size() == 2,
           "graph topo order; append_kv = CPY then VIEW over the cache");
   }
+  // view_rows: a VIEW of the last rows of an activation, aliased at its offset
+  {
+    Graph g;
+    Tensor x("x", GGML_TYPE_F32, {1024, 5, 1, 1}), w("w", GGML_TYPE_F32, {1024, 1, 1, 1});
+    std::vector<float> xb(5 * 1024), wb(1024);
+    x.data = xb.data();
+    w.data = wb.data();
+    Tensor *n = OpFactory::rms_norm(g, &x, &w, 1e-6f, "n");
+    Tensor *last = OpFactory::view_rows(g, n, 4, 1, "last");
+    g.mark_output(last);
+    CHECK(g.compute() && last->op == OperationType::GGML_OP_VIEW && last->src[0] == n &&
+              last->dims == (std::array<int64_t, 4>{1024, 1, 1, 1}) && last->offset == 4 * 1024 * 4 &&
+              !last->data && last->is_contiguous(),
+          "view_rows: [1024, 1] VIEW of row 4 at byte offset 16384, placed with its source");
+  }
   paged_cpu_tests();
   offload_cpu_tests();
 }
