@@ -239,6 +239,89 @@ bool fast_ok(int64_t k, std::initializer_list<const void *> ptrs) {
 
 int grid_for(int64_t waves) { return static_cast<int>((waves + kWaves - 1) / kWaves); }
 
+// Few-token products (2 <= m <= kSkinnyMaxM, the prefill of a short prompt):
+// out[t][n] = sum_k w[n][k] x[t][k] (+ residual[t][n]) on F32 MFMA
+// (v_mfma_f32_16x16x4_f32). A workgroup owns a 16-row tile of w and a
+// 16-token tile of x; its 8 wavefronts take 8 equal slices of k, each lane
+// streaming 32 contiguous bytes of one w row and of one token row per step,
+// and the 8 partial tiles are summed through LDS in wave order, so results do
+// not depend on timing. blockIdx = n_tile + n_tiles * m_tile: with n_tiles a
+// multiple of 8, the token tiles of one w tile run on the same XCD and share
+// its L2. A library GEMM of these shapes picks output tiles so large that a
+// 3072-row projection of 32 tokens runs on 48 workgroups.
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+constexpr int kSkinnyMaxM = 64;
+constexpr int kSkinnyWaves = 8;
+
+__global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_kernel(const float *__restrict__ w,
+                                                                   const float *__restrict__ x,
+                                                                   float *out, const float *residual,
+                                                                   int n_out, int k, int m, int n_tiles) {
+  __shared__ float s_red[kSkinnyWaves][64][4];
+  const int nt = blockIdx.x % n_tiles;
+  const int mt = blockIdx.x / n_tiles;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int j = lane & 15;
+  const int kk = lane >> 4;
+  const int n0 = nt * 16, m0 = mt * 16;
+  // A operand: w row n0 + j; B operand: token m0 + j (clamped; its outputs
+  // are not written). Lane group kk covers k = kb + 8 kk .. kb + 8 kk + 7.
+  const float *wr = w + static_cast<size_t>(n0 + j) * k + 8 * kk;
+  const float *xr = x + static_cast<size_t>(min(m0 + j, m - 1)) * k + 8 * kk;
+  const int kw = k / kSkinnyWaves;  // a multiple of 32
+  const int kb0 = wave * kw;
+  const int n_steps = kw / 32;
+  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+  float4 a0 = *reinterpret_cast<const float4 *>(wr + kb0);
+  float4 a1 = *reinterpret_cast<const float4 *>(wr + kb0 + 4);
+  float4 b0 = *reinterpret_cast<const float4 *>(xr + kb0);
+  float4 b1 = *reinterpret_cast<const float4 *>(xr + kb0 + 4);
+  for (int s = 0; s < n_steps; ++s) {
+    const float4 ca0 = a0, ca1 = a1, cb0 = b0, cb1 = b1;
+    if (s + 1 < n_steps) {  // the next step's loads fly during this step's MFMAs
+      const int kb = kb0 + 32 * (s + 1);
+      a0 = *reinterpret_cast<const float4 *>(wr + kb);
+      a1 = *reinterpret_cast<const float4 *>(wr + kb + 4);
+      b0 = *reinterpret_cast<const float4 *>(xr + kb);
+      b1 = *reinterpret_cast<const float4 *>(xr + kb + 4);
+    }
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ca0.x, cb0.x, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ca0.y, cb0.y, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ca0.z, cb0.z, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ca0.w, cb0.w, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ca1.x, cb1.x, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ca1.y, cb1.y, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ca1.z, cb1.z, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ca1.w, cb1.w, acc, 0, 0, 0);
+  }
+  // lane l, register r: w row n0 + 4 (l / 16) + r, token m0 + l % 16
+#pragma unroll
+  for (int r = 0; r < 4; ++r) s_red[wave][lane][r] = acc[r];
+  __syncthreads();
+  if (threadIdx.x < 256) {
+    const int l = threadIdx.x >> 2;
+    const int r = threadIdx.x & 3;
+    const int t = m0 + (l & 15);
+    const int n = n0 + 4 * (l >> 4) + r;
+    float v = s_red[0][l][r];
+#pragma unroll
+    for (int q = 1; q < kSkinnyWaves; ++q) v += s_red[q][l][r];
+    if (t < m) {
+      const size_t o = static_cast<size_t>(t) * n_out + n;
+      if (residual) v += residual[o];
+      out[o] = v;
+    }
+  }
+}
+
+bool skinny_ok(int64_t n_out, int64_t k, int64_t m, std::initializer_list<const void *> ptrs) {
+  if (m < 2 || m > kSkinnyMaxM || n_out % 16 != 0 || k % (32 * kSkinnyWaves) != 0) return false;
+  for (const void *p : ptrs)
+    if (p && !ikv::aligned16(p)) return false;
+  return true;
+}
+
 // rocBLAS handle of the current device, created on first use.
 rocblas_handle blas_handle() {
   static std::mutex mu;
@@ -275,6 +358,13 @@ extern "C" int ikv_mul_mat_f32(const float *w, const float *x, float *out, int64
       gemv_generic_kernel<<<grid_for(n_out), kThreads, 0, s>>>(w, x, out, residual, int(n_out),
                                                                 int(k), 0, nullptr);
     }
+    return ikv::launch_status();
+  }
+  if (skinny_ok(n_out, k, m, {w, x})) {
+    const int n_tiles = static_cast<int>(n_out / 16);
+    const int m_tiles = static_cast<int>((m + 15) / 16);
+    skinny_kernel<<<n_tiles * m_tiles, kSkinnyWaves * 64, 0, s>>>(w, x, out, residual, int(n_out),
+                                                                  int(k), int(m), n_tiles);
     return ikv::launch_status();
   }
   rocblas_handle h = blas_handle();

@@ -45,7 +45,8 @@ def test_gemv_matches_oracle(dev, oracle_pool, n_out, k):
     assert proj_close(got, w, x[None], oracle.mul_mat(w, x))
 
 
-@pytest.mark.parametrize("n_out,k,m", [(2048, 1024, 37), (1024, 3072, 5), (300, 200, 2)])
+@pytest.mark.parametrize("n_out,k,m", [(2048, 1024, 37), (1024, 3072, 5), (300, 200, 2), (3072, 1024, 64),
+                                        (16, 256, 2), (4096, 4096, 17), (1024, 2048, 65)])
 def test_mul_mat_multi_token_matches_oracle(dev, oracle_pool, n_out, k, m):
     w = synth.normal(300 + m, (n_out, k), 0.02)
     x = synth.normal(400 + m, (m, k))
@@ -54,6 +55,17 @@ def test_mul_mat_multi_token_matches_oracle(dev, oracle_pool, n_out, k, m):
     assert proj_close(got, w, x, oracle.mul_mat(w, x))
     got_r = host(ikv.mul_mat(dev_t(w, dev), dev_t(x, dev), residual=dev_t(r, dev)))
     assert proj_close(got_r, w, x, oracle.mul_mat(w, x).astype(np.float64) + r)
+
+
+def test_mul_mat_few_tokens_residual_in_place(dev, oracle_pool):
+    # out = out + W x for a 32-token batch (the few-token MFMA path)
+    n_out, k, m = 1024, 2048, 32
+    w = synth.normal(610, (n_out, k), 0.02)
+    x = synth.normal(611, (m, k))
+    r = synth.normal(612, (m, n_out))
+    buf = dev_t(r, dev)
+    ikv.mul_mat(dev_t(w, dev), dev_t(x, dev), out=buf, residual=buf)
+    assert proj_close(host(buf), w, x, oracle.mul_mat(w, x).astype(np.float64) + r)
 
 
 def test_gemv_residual_in_place(dev, oracle_pool):
