@@ -27,12 +27,14 @@ extern "C" {
  * mul_mat: out[m][n] = sum_k x[m][k] * w[n][k]   (w: [n_out][k] rows, the
  * ggml [K, N] weight of CPUBackend::compute_mul_mat,
  * src/backends/cpu_backend.cpp:386-424; x: [m][k]; out: [m][n_out]).
- * m == 1 (decode) runs a hand-written streaming GEMV; m > 1 runs rocBLAS
- * SGEMM (full F32). The first m > 1 call on a device creates that device's
- * rocBLAS handle (kept until exit); calls that share a device must come
- * from one host thread at a time.
- * residual: NULL, or [m][n_out] added to the result (out may equal residual
- * for m == 1).
+ * m == 1 (decode) runs a hand-written streaming GEMV. 2 <= m <= 64 with
+ * n_out % 16 == 0, k % 256 == 0 and 16-byte aligned w and x runs a
+ * hand-written F32 MFMA kernel (deterministic: fixed reduction order). Other
+ * m > 1 run rocBLAS SGEMM (full F32); the first such call on a device
+ * creates that device's rocBLAS handle (kept until exit), and calls that
+ * share a device must come from one host thread at a time.
+ * residual: NULL, or [m][n_out] added to the result (out may equal
+ * residual).
  * ------------------------------------------------------------------- */
 int ikv_mul_mat_f32(const float *w, const float *x, float *out, int64_t n_out, int64_t k,
                     int64_t m, const float *residual, void *stream);
