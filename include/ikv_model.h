@@ -85,6 +85,17 @@ int ikv_silu_f32(const float *x, float *out, int64_t n, void *stream);
 int ikv_argmax_f32(const float *logits, int64_t n, int32_t *token, int32_t *token_mirror,
                    void *stream);
 
+/* The same sampler over up to 64 workgroups (no counterpart in the reference:
+ * its sampler runs on the host). workspace: device memory of at least
+ * ikv_argmax_workspace_bytes() bytes, 256-byte aligned, zero-filled once
+ * before its first use; each call leaves it as it expects to find it, so it
+ * is reused call after call. Calls sharing a workspace must not overlap
+ * (one stream). Returns -EINVAL for a missing, small or misaligned
+ * workspace. The result equals ikv_argmax_f32's. */
+size_t ikv_argmax_workspace_bytes(void);
+int ikv_argmax_ws_f32(const float *logits, int64_t n, int32_t *token, int32_t *token_mirror,
+                      void *workspace, size_t workspace_bytes, void *stream);
+
 /* ---------------------------------------------------------------------
  * Host helper: the benchmarks' synthetic weights. out_host[i] =
  * std * N(0,1) sample number (offset + i) of the stream `seed`:

@@ -181,6 +181,7 @@ Qwen3Runner::~Qwen3Runner() {
     if (e) (void)hipEventDestroy(e);
   if (_token_dev) (void)hipFree(_token_dev);
   if (_positions_dev) (void)hipFree(_positions_dev);
+  if (_argmax_ws) (void)hipFree(_argmax_ws);
   if (_token_host) (void)hipHostFree(_token_host);
 }
 
@@ -227,6 +228,9 @@ infer::expected<void, std::error_code> Qwen3Runner::init() {
   };
   if (hipMalloc(&_token_dev, 2 * sizeof(int32_t)) != hipSuccess) return fail_alloc();
   if (hipMalloc(&_positions_dev, _capacity * sizeof(int32_t)) != hipSuccess) return fail_alloc();
+  if (hipMalloc(&_argmax_ws, ikv_argmax_workspace_bytes()) != hipSuccess ||
+      hipMemset(_argmax_ws, 0, ikv_argmax_workspace_bytes()) != hipSuccess)
+    return fail_alloc();
   // Mapped and coherent: the sampler's store reaches host memory directly.
   if (hipHostMalloc(&_token_host, 2 * sizeof(int32_t), hipHostMallocMapped | hipHostMallocCoherent) !=
           hipSuccess ||
@@ -285,7 +289,8 @@ infer::expected<void, std::error_code> Qwen3Runner::enqueue_step(const int32_t *
   hipStream_t s = _backend.stream();
   // The sampler writes the token to the device slot the next step embeds
   // and to the pinned host slot the host reads once the event has fired.
-  if (ikv_argmax_f32(row, vocab, _token_dev + slot, _token_host_dev + slot, s) != 0 ||
+  if (ikv_argmax_ws_f32(row, vocab, _token_dev + slot, _token_host_dev + slot, _argmax_ws,
+                        ikv_argmax_workspace_bytes(), s) != 0 ||
       hipEventRecord(_ready[slot], s) != hipSuccess)
     return abort(std::make_error_code(std::errc::io_error));
   // The kernels of this step hold no host-side state: hand the layer

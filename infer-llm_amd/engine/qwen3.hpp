@@ -151,5 +151,6 @@ class Qwen3Runner {
   int32_t *_token_host = nullptr;   // [2] pinned read-back slots
   int32_t *_token_host_dev = nullptr;  // the same slots as the device addresses them
   int32_t *_positions_dev = nullptr;  // [capacity]: 0, 1, 2, ...
+  void *_argmax_ws = nullptr;         // the multi-workgroup sampler's workspace (zeroed once)
   hipEvent_t _ready[2] = {nullptr, nullptr};
 };

@@ -107,6 +107,9 @@ SIGNATURES = {
     "ikv_mul_f32": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int64, _c_void_p]),
     "ikv_silu_f32": (_c_int, [_c_void_p, _c_void_p, _c_int64, _c_void_p]),
     "ikv_argmax_f32": (_c_int, [_c_void_p, _c_int64, _c_void_p, _c_void_p, _c_void_p]),
+    "ikv_argmax_workspace_bytes": (_c_size_t, []),
+    "ikv_argmax_ws_f32": (
+        _c_int, [_c_void_p, _c_int64, _c_void_p, _c_void_p, _c_void_p, _c_size_t, _c_void_p]),
     "ikv_synth_normal_f32": (
         _c_int, [ctypes.c_uint64, ctypes.c_uint64, _c_size_t, ctypes.c_double, _c_void_p, _c_int]),
     # include/ikv_probe.h
@@ -508,15 +511,29 @@ def elementwise(op: str, a, b=None, out=None, stream=None):
     return out
 
 
-def argmax(logits, token=None, mirror=None, stream=None):
+def argmax(logits, token=None, mirror=None, workspace=None, stream=None):
     """Device int32 [1]: greedy token of logits (ties -> lowest id; -1 on NaN/+inf);
-    `mirror` (e.g. a pinned host tensor) receives a copy."""
+    `mirror` (e.g. a pinned host tensor) receives a copy. With `workspace`
+    (argmax_workspace()), the multi-workgroup form runs."""
     torch = _torch()
     if token is None:
         token = torch.empty(1, dtype=torch.int32, device=logits.device)
-    _check("ikv_argmax_f32", load().ikv_argmax_f32(_ptr(logits), logits.numel(), _ptr(token),
-                                                    _ptr(mirror), _stream(stream)))
+    if workspace is None:
+        _check("ikv_argmax_f32", load().ikv_argmax_f32(_ptr(logits), logits.numel(), _ptr(token),
+                                                        _ptr(mirror), _stream(stream)))
+    else:
+        _check("ikv_argmax_ws_f32",
+               load().ikv_argmax_ws_f32(_ptr(logits), logits.numel(), _ptr(token), _ptr(mirror),
+                                        _ptr(workspace), workspace.numel() * workspace.element_size(),
+                                        _stream(stream)))
     return token
+
+
+def argmax_workspace(device=None):
+    """Zeroed device workspace of the multi-workgroup greedy sampler."""
+    torch = _torch()
+    n = int(load().ikv_argmax_workspace_bytes())
+    return torch.zeros(n, dtype=torch.uint8, device=device or "cuda")
 
 
 def synth_normal(seed: int, shape, std: float = 1.0, offset: int = 0, threads: int = 8):

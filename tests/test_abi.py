@@ -76,6 +76,17 @@ def test_prefill_and_rows_reject_bad_arguments():
     assert _rc("ikv_append_f32", P, P, 2**62, 2**8, None) == -errno.EOVERFLOW
 
 
+def test_argmax_workspace_form_rejects_bad_arguments():
+    P, W = 64, 256  # 16-byte aligned logits, 256-byte aligned workspace addresses
+    need = ikv.load().ikv_argmax_workspace_bytes()
+    assert 256 < need <= 4096
+    assert _rc("ikv_argmax_ws_f32", P, 10, P, None, None, need, None) == -errno.EINVAL   # no workspace
+    assert _rc("ikv_argmax_ws_f32", P, 10, P, None, W, need - 8, None) == -errno.EINVAL  # too small
+    assert _rc("ikv_argmax_ws_f32", P, 10, P, None, W + 8, need, None) == -errno.EINVAL  # misaligned
+    assert _rc("ikv_argmax_ws_f32", P, 0, P, None, W, need, None) == -errno.EINVAL       # n < 1
+    assert _rc("ikv_argmax_ws_f32", None, 10, P, None, W, need, None) == -errno.EINVAL
+
+
 def test_workspace_bytes_grow_with_context_and_are_bounded():
     sizes = [ikv.decode_workspace_bytes(16, 8, 128, n) for n in (1, 256, 4097, 32769, 10**6)]
     assert all(s > 0 for s in sizes)

@@ -129,35 +129,54 @@ def test_elementwise(dev, n):
                        rtol=1e-6, atol=1e-7)
 
 
-def test_argmax_follows_the_greedy_sampler(dev):
+@pytest.mark.parametrize("form", ["one_workgroup", "workspace"])
+def test_argmax_follows_the_greedy_sampler(dev, form):
     import torch
+    ws = ikv.argmax_workspace(dev) if form == "workspace" else None  # shared by every call below
     x = synth.normal(18, (151936,))
-    assert int(host(ikv.argmax(dev_t(x, dev)))[0]) == oracle.sample_greedy(x)
+    assert int(host(ikv.argmax(workspace=ws, logits=dev_t(x, dev)))[0]) == oracle.sample_greedy(x)
     y = x.copy()
     y[[5, 70000, 151935]] = 100.0                       # tie: lowest id wins
-    assert int(host(ikv.argmax(dev_t(y, dev)))[0]) == 5 == oracle.sample_greedy(y)
+    assert int(host(ikv.argmax(workspace=ws, logits=dev_t(y, dev)))[0]) == 5 == oracle.sample_greedy(y)
     for bad in (np.nan, np.inf):
         z = x.copy()
         z[1234] = bad
-        assert int(host(ikv.argmax(dev_t(z, dev)))[0]) == -1 == oracle.sample_greedy(z)
+        assert int(host(ikv.argmax(workspace=ws, logits=dev_t(z, dev)))[0]) == -1 == oracle.sample_greedy(z)
     ninf = np.full(1000, -np.inf, np.float32)
-    assert int(host(ikv.argmax(dev_t(ninf, dev)))[0]) == -1
+    assert int(host(ikv.argmax(workspace=ws, logits=dev_t(ninf, dev)))[0]) == -1
     # unaligned start (scalar path) and a short odd length
     big = dev_t(np.concatenate([[0.0], y]).astype(np.float32), dev)
-    assert int(host(ikv.argmax(big[1:]))[0]) == 5
+    assert int(host(ikv.argmax(workspace=ws, logits=big[1:]))[0]) == 5
     w = synth.normal(19, (7,))
-    assert int(host(ikv.argmax(dev_t(w, dev)))[0]) == int(np.argmax(w))
+    assert int(host(ikv.argmax(workspace=ws, logits=dev_t(w, dev)))[0]) == int(np.argmax(w))
     # the maximum in the last batch of loads, in the scalar tail, at index 0;
     # ties across load batches; and the mirror output
     for n, at in ((151936, 151930), (151937, 151936), (40003, 0), (32768 * 4 + 5, 32768 * 4 - 1)):
         v = synth.normal(20 + n, (n,))
         v[at] = 50.0
         mirror = torch.full((1,), -7, dtype=torch.int32, device=dev)
-        tok = ikv.argmax(dev_t(v, dev), mirror=mirror)
+        tok = ikv.argmax(workspace=ws, logits=dev_t(v, dev), mirror=mirror)
         assert int(host(tok)[0]) == at == int(host(mirror)[0]) == oracle.sample_greedy(v)
     t = synth.normal(21, (100000,))
     t[[8191 * 4 + 1, 8192 * 4 + 2, 99999]] = 40.0       # tie between two load batches
-    assert int(host(ikv.argmax(dev_t(t, dev)))[0]) == 8191 * 4 + 1 == oracle.sample_greedy(t)
+    assert int(host(ikv.argmax(workspace=ws, logits=dev_t(t, dev)))[0]) == 8191 * 4 + 1 == oracle.sample_greedy(t)
+    if ws is not None:
+        # the workspace form's slices: 151936 logits = 37984 float4 over 64
+        # workgroups of 594 float4 (2376 logits); a tie across the first
+        # boundary, NaN in the last workgroup's tail, one logit, an all-equal row
+        u = synth.normal(22, (151936,))
+        u[[2375, 2376]] = 60.0
+        assert int(host(ikv.argmax(workspace=ws, logits=dev_t(u, dev)))[0]) == 2375
+        u[[2375]] = 0.0
+        assert int(host(ikv.argmax(workspace=ws, logits=dev_t(u, dev)))[0]) == 2376
+        tail = synth.normal(23, (151939,))
+        tail[151938] = np.nan
+        assert int(host(ikv.argmax(workspace=ws, logits=dev_t(tail, dev)))[0]) == -1
+        one = np.array([3.0], np.float32)
+        assert int(host(ikv.argmax(workspace=ws, logits=dev_t(one, dev)))[0]) == 0
+        flat = np.full(70000, 2.5, np.float32)
+        assert int(host(ikv.argmax(workspace=ws, logits=dev_t(flat, dev)))[0]) == 0
+        assert not host(ws)[:4].any()  # the arrival counter is back at zero
     del torch
 
 
