@@ -72,6 +72,10 @@ int ikv_get_rows_f32(const float *table, const int32_t *ids, float *out, int64_t
 int ikv_add_f32(const float *a, const float *b, float *out, int64_t n, void *stream);
 int ikv_mul_f32(const float *a, const float *b, float *out, int64_t n, void *stream);
 int ikv_silu_f32(const float *x, float *out, int64_t n, void *stream);
+/* out = up * silu(gate): the SILU node and the MUL that consumes it
+ * (src/models/Qwen3.cpp:107-112) in one pass, bitwise equal to the two ops.
+ * out may equal gate or up. */
+int ikv_silu_mul_f32(const float *gate, const float *up, float *out, int64_t n, void *stream);
 
 /* ---------------------------------------------------------------------
  * Greedy sampling on the device (sample_greedy, src/sampler.cpp:42-65):

@@ -370,21 +370,24 @@ extern "C" int ikv_mul_mat_f32(const float *w, const float *x, float *out, int64
   rocblas_handle h = blas_handle();
   if (!h) return static_cast<int>(hipErrorNotInitialized);
   if (rocblas_set_stream(h, s) != rocblas_status_success) return static_cast<int>(hipErrorUnknown);
-  float beta = 0.f;
-  if (residual) {
-    beta = 1.f;
-    if (residual != out) {
-      const hipError_t e = hipMemcpyAsync(out, residual, sizeof(float) * n_out * m,
-                                          hipMemcpyDeviceToDevice, s);
-      if (e != hipSuccess) return static_cast<int>(e);
-    }
-  }
   const float alpha = 1.f;
   // Row-major out[m][n] is the column-major n x m matrix C = W^T(col) * X:
-  // A = w viewed column-major k x n, transposed; B = x viewed k x m.
-  const rocblas_status st = rocblas_sgemm(h, rocblas_operation_transpose, rocblas_operation_none,
-                                          int(n_out), int(m), int(k), &alpha, w, int(k), x, int(k),
-                                          &beta, out, int(n_out));
+  // A = w viewed column-major k x n, transposed; B = x viewed k x m. With a
+  // residual, D = A B + C reads C = residual and writes D = out, so the
+  // residual is never copied into out first (out may equal residual).
+  rocblas_status st;
+  if (residual) {
+    const float beta = 1.f;
+    st = rocblas_gemm_ex(h, rocblas_operation_transpose, rocblas_operation_none, int(n_out), int(m),
+                         int(k), &alpha, w, rocblas_datatype_f32_r, int(k), x, rocblas_datatype_f32_r,
+                         int(k), &beta, residual, rocblas_datatype_f32_r, int(n_out), out,
+                         rocblas_datatype_f32_r, int(n_out), rocblas_datatype_f32_r,
+                         rocblas_gemm_algo_standard, 0, 0);
+  } else {
+    const float beta = 0.f;
+    st = rocblas_sgemm(h, rocblas_operation_transpose, rocblas_operation_none, int(n_out), int(m),
+                       int(k), &alpha, w, int(k), x, int(k), &beta, out, int(n_out));
+  }
   if (st != rocblas_status_success) return static_cast<int>(hipErrorLaunchFailure);
   return ikv::launch_status();
 }

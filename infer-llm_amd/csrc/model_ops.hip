@@ -6,7 +6,8 @@
 //             259-332): one workgroup per index copies a table row with
 //             16-byte accesses; an out-of-range id writes zeros and raises a
 //             status flag instead of reading outside the table.
-//   add/mul/silu  src/backends/cpu_backend.cpp:636-703: grid-stride float4.
+//   add/mul/silu  src/backends/cpu_backend.cpp:636-703: grid-stride float4;
+//             silu_mul = up * silu(gate), the SILU then MUL pair in one pass.
 //   argmax    sample_greedy (src/sampler.cpp:42-65): one workgroup of 1024
 //             threads scans the logits (16-byte loads, 8 in flight per
 //             lane), keeps (max, lowest index) per lane, and reduces through
@@ -42,13 +43,17 @@ __global__ __launch_bounds__(kThreads) void get_rows_kernel(const float *__restr
   }
 }
 
-enum class Ew { kAdd, kMul, kSilu };
+enum class Ew { kAdd, kMul, kSilu, kSiluMul };
 
 template <Ew OP>
 __device__ __forceinline__ float ew(float a, float b) {
   if constexpr (OP == Ew::kAdd) return a + b;
   else if constexpr (OP == Ew::kMul) return a * b;
-  else return a / (1.0f + expf(-a));
+  else if constexpr (OP == Ew::kSilu) return a / (1.0f + expf(-a));
+  else {  // b * silu(a): the silu value is rounded to float, then multiplied
+    const float g = a / (1.0f + expf(-a));
+    return b * g;
+  }
 }
 
 template <Ew OP>
@@ -297,6 +302,11 @@ extern "C" int ikv_mul_f32(const float *a, const float *b, float *out, int64_t n
 
 extern "C" int ikv_silu_f32(const float *x, float *out, int64_t n, void *stream) {
   return launch_ew<Ew::kSilu>(x, nullptr, out, n, stream);
+}
+
+extern "C" int ikv_silu_mul_f32(const float *gate, const float *up, float *out, int64_t n,
+                                void *stream) {
+  return launch_ew<Ew::kSiluMul>(gate, up, out, n, stream);
 }
 
 extern "C" int ikv_argmax_f32(const float *logits, int64_t n, int32_t *token,

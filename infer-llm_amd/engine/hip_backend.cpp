@@ -366,6 +366,7 @@ infer::expected<void, std::error_code> HIPBackend::compute(Graph &graph) {
   _norm_into_rope.clear();
   _append_into_attn.clear();
   _swiglu.clear();
+  _silu_mul.clear();
   _residual.clear();
   _qkv.clear();
   _norm_into_mm.clear();
@@ -454,7 +455,8 @@ bool mm_operands_ok(const Tensor *mm) {
 
 // Model-level fusions of the Qwen3 graph (src/models/Qwen3.cpp:53-113):
 //  * MUL(up, SILU(gate)) with gate = MUL_MAT(w_gate, x), up = MUL_MAT(w_up, x)
-//    and one token -> one ikv_gemv_swiglu_f32;
+//    and one token -> one ikv_gemv_swiglu_f32; with several tokens the SILU
+//    and MUL -> one ikv_silu_mul_f32 pass;
 //  * ADD(MUL_MAT(w, x), r) -> the product with the residual added in its
 //    epilogue (o_proj and ffn_down);
 //  * three single-token MUL_MATs of one input (q, k, v) -> one ikv_gemv3_f32.
@@ -471,6 +473,21 @@ void HIPBackend::plan_model_fusions(Graph &graph, std::unordered_map<const Tenso
       if (!mm_operands_ok(up) || !mm_operands_ok(gate) || up->dims != gate->dims) continue;
       _swiglu[n] = {gate, up};
       _skip[up] = _skip[act] = _skip[gate] = true;
+      break;
+    }
+  }
+  // The remaining MUL(up, SILU(gate)) pairs (several tokens: the projections
+  // are separate GEMMs) -> one elementwise pass, up * silu(gate).
+  for (Tensor *n : graph.nodes()) {
+    if (n->op != OperationType::GGML_OP_MUL || _swiglu.count(n) || !n->src[0] || !n->src[1]) continue;
+    for (int side = 0; side < 2; ++side) {
+      const Tensor *act = n->src[1 - side], *up = n->src[side];
+      if (!is_silu(act) || uses[act] != 1 || !act->src[0]) continue;
+      const Tensor *gate = act->src[0];
+      if (!contiguous_f32(gate) || !contiguous_f32(up) || gate->dims != n->dims || up->dims != n->dims)
+        continue;
+      _silu_mul[n] = {gate, up};
+      _skip[act] = true;
       break;
     }
   }
@@ -800,6 +817,14 @@ infer::expected<void, std::error_code> HIPBackend::dispatch(Tensor *node) {
                                              nw ? static_cast<const float *>(nw->data) : nullptr,
                                              eps, s),
                          "gemv_swiglu");
+      }
+      if (const auto f = _silu_mul.find(node); f != _silu_mul.end()) {
+        const Tensor *gate = f->second.first, *up = f->second.second;
+        return check_ikv(ikv_silu_mul_f32(static_cast<const float *>(gate->data),
+                                          static_cast<const float *>(up->data),
+                                          static_cast<float *>(node->data),
+                                          int64_t(node->element_count()), s),
+                         "silu_mul");
       }
       if (!contiguous_f32(a) || !contiguous_f32(b) || a->dims != node->dims || b->dims != node->dims)
         return infer::fail(std::errc::invalid_argument);

@@ -97,6 +97,7 @@ class HIPBackend : public Backend {
   std::unordered_map<const Tensor *, const Tensor *> _norm_into_rope;  // rope -> its rms_norm
   std::unordered_map<const Tensor *, std::pair<const Tensor *, const Tensor *>> _append_into_attn;
   std::unordered_map<const Tensor *, std::pair<const Tensor *, const Tensor *>> _swiglu;    // mul -> gate, up
+  std::unordered_map<const Tensor *, std::pair<const Tensor *, const Tensor *>> _silu_mul;  // mul -> gate, up (SILU input, other factor)
   std::unordered_map<const Tensor *, std::pair<const Tensor *, const Tensor *>> _residual;  // add -> mm, r
   std::unordered_map<const Tensor *, std::array<const Tensor *, 3>> _qkv;  // first mm -> group
   std::unordered_map<const Tensor *, const Tensor *> _norm_into_mm;  // qkv first mm / swiglu mul -> norm

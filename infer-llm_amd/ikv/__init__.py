@@ -106,6 +106,7 @@ SIGNATURES = {
     "ikv_add_f32": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int64, _c_void_p]),
     "ikv_mul_f32": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int64, _c_void_p]),
     "ikv_silu_f32": (_c_int, [_c_void_p, _c_void_p, _c_int64, _c_void_p]),
+    "ikv_silu_mul_f32": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int64, _c_void_p]),
     "ikv_argmax_f32": (_c_int, [_c_void_p, _c_int64, _c_void_p, _c_void_p, _c_void_p]),
     "ikv_argmax_workspace_bytes": (_c_size_t, []),
     "ikv_argmax_ws_f32": (

@@ -127,6 +127,12 @@ def test_elementwise(dev, n):
     assert np.array_equal(host(ikv.elementwise("mul", da, db)), oracle.elementwise("mul", a, b))
     assert np.allclose(host(ikv.elementwise("silu", da)), oracle.elementwise("silu", a),
                        rtol=1e-6, atol=1e-7)
+    # up * silu(gate) in one pass equals SILU then MUL bit for bit (in place too)
+    sep = host(ikv.elementwise("mul", db, ikv.elementwise("silu", da)))
+    assert np.array_equal(host(ikv.elementwise("silu_mul", da, db)).view(np.uint32), sep.view(np.uint32))
+    inplace = da.clone()
+    ikv.elementwise("silu_mul", inplace, db, out=inplace)
+    assert np.array_equal(host(inplace).view(np.uint32), sep.view(np.uint32))
 
 
 @pytest.mark.parametrize("form", ["one_workgroup", "workspace"])
