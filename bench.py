@@ -455,6 +455,61 @@ def cpu_baseline(ctx, seconds):
     }
 
 
+def cpu_sweep():
+    """The oracle on this host at every ctx of config 1 (decode step: append +
+    attention, GB/s) and every prompt length of config 2 (prefill attention +
+    append, ms), 1 warm-up and the median of 3 runs (benchmarks/cpu/bench.cpp
+    :414-431)."""
+    import numpy as np
+
+    import oracle
+    from ikv import synth
+
+    workers = min(oracle.default_workers(), 15)
+    threads = oracle.set_workers(workers)
+
+    def median3(fn):
+        # a warm-up run, then 3 timed runs; a run longer than 0.5 s is warm
+        # enough by itself, so its warm-up counts as the first timed run
+        t0 = time.perf_counter()
+        fn()
+        first = time.perf_counter() - t0
+        ts = [first] if first > 0.5 else []
+        while len(ts) < 3:
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return sorted(ts)[1]
+
+    res = {"threads": threads, "decode_gbs": {}, "prefill_ms": {}, "prefill_gflops": {}}
+    q = synth.normal(synth.config_seed(1, 300), (N_HEAD, D))
+    kn = synth.normal(synth.config_seed(1, 301), (N_HEAD_KV, D))
+    vn = synth.normal(synth.config_seed(1, 302), (N_HEAD_KV, D))
+    for ctx in (256, 1024, 4096, 16384, 32768):
+        kc = synth.normal(synth.config_seed(1, 100), ((ctx + 1), N_HEAD_KV, D))
+        vc = synth.normal(synth.config_seed(1, 200), ((ctx + 1), N_HEAD_KV, D))
+        t = median3(lambda: oracle.decode_append_attn(q, kn, vn, kc, vc, ctx))
+        res["decode_gbs"][str(ctx)] = round(decode_bytes(ctx) / t / 1e9, 2)
+        del kc, vc
+    for P in (32, 64, 128, 256, 2048):
+        qp = synth.normal(synth.config_seed(2, 10 + P), (P, N_HEAD, D))
+        kp = synth.normal(synth.config_seed(2, 20 + P), (P, N_HEAD_KV, D))
+        vp = synth.normal(synth.config_seed(2, 30 + P), (P, N_HEAD_KV, D))
+        kcache = np.empty_like(kp)
+        vcache = np.empty_like(vp)
+
+        def run():
+            oracle.cpy(kcache, kp)
+            oracle.cpy(vcache, vp)
+            oracle.flash_attn(qp, kcache, vcache, 0)
+        t = median3(run)
+        res["prefill_ms"][str(P)] = round(t * 1e3, 3)
+        res["prefill_gflops"][str(P)] = round(prefill_flops(P) / t / 1e9, 2)
+    log(f"[bench] cpu sweep ({threads} threads): decode GB/s {res['decode_gbs']}, "
+        f"prefill ms {res['prefill_ms']}")
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -538,7 +593,8 @@ def main():
 
     extra = {"repeats": None, "eager_gbs": None, "ctx_sweep_gbs": {}, "short_ctx_us": {},
              "g4_ctx4096": None, "paged_ctx4096_gbs": {},
-             "mall_hot_gbs": None, "prefill": {}, "hbm_probes": None, "model": None}
+             "mall_hot_gbs": None, "prefill": {}, "hbm_probes": None, "model": None,
+             "cpu_sweep": None}
     if not args.no_extra:
         # Five more timed regions of the same K steps (no warmup between them):
         # their spread and median, beside the single region `value` reports.
@@ -611,6 +667,8 @@ def main():
         log(f"[bench] cpu baseline ({args.cpu_seconds:.0f} s)...")
         cpu = cpu_baseline(args.ctx, args.cpu_seconds)
         log(f"[bench] cpu baseline {cpu['value']} GB/s on {cpu['cores']} threads")
+        if not args.no_extra:
+            extra["cpu_sweep"] = cpu_sweep()
 
     line = {
         "metric": METRIC,
