@@ -112,7 +112,11 @@ def run_decode_case(dev, ctx, Hq=16, Hkv=8, seed=0, fused=True):
     return out.cpu().numpy(), want, k_cache.cpu().numpy(), v_cache.cpu().numpy(), k_host, v_host
 
 
-@pytest.mark.parametrize("ctx", [0, 1, 2, 31, 32, 33, 255, 256, 1024, 4096, 16384, 32768])
+# 63/64: the new row at the end of / just past one 64-token tile; 127/128: the
+# last single-split context and the first split one (n_kv 129); 191/192 and
+# 4096/8191: a last split holding a single token
+@pytest.mark.parametrize("ctx", [0, 1, 2, 31, 32, 33, 63, 64, 127, 128, 129, 191, 192, 255, 256,
+                                 1024, 4096, 8191, 16384, 32768])
 def test_decode_fused_append_qwen3_06b(dev, ctx):
     out, want, kc, vc, k_ref, v_ref = run_decode_case(dev, ctx)
     assert_attn_close(out, want, f"ctx={ctx}")
