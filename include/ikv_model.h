@@ -28,7 +28,7 @@ extern "C" {
  * ggml [K, N] weight of CPUBackend::compute_mul_mat,
  * src/backends/cpu_backend.cpp:386-424; x: [m][k]; out: [m][n_out]).
  * m == 1 (decode) runs a hand-written streaming GEMV. 2 <= m <= 64 with
- * n_out % 16 == 0, k % 256 == 0 and 16-byte aligned w and x runs a
+ * n_out % 16 == 0, k % 1024 == 0 and 16-byte aligned w and x runs a
  * hand-written F32 MFMA kernel (deterministic: fixed reduction order). Other
  * m > 1 run rocBLAS SGEMM (full F32); the first such call on a device
  * creates that device's rocBLAS handle (kept until exit), and calls that

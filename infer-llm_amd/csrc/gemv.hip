@@ -242,21 +242,29 @@ int grid_for(int64_t waves) { return static_cast<int>((waves + kWaves - 1) / kWa
 // Few-token products (2 <= m <= kSkinnyMaxM, the prefill of a short prompt):
 // out[t][n] = sum_k w[n][k] x[t][k] (+ residual[t][n]) on F32 MFMA
 // (v_mfma_f32_16x16x4_f32). A workgroup owns a 16-row tile of w and a
-// 16-token tile of x; its 8 wavefronts take 8 equal slices of k, each lane
-// streaming 32 contiguous bytes of one w row and of one token row per step,
-// and the 8 partial tiles are summed through LDS in wave order, so results do
-// not depend on timing. blockIdx = n_tile + n_tiles * m_tile: with n_tiles a
-// multiple of 8, the token tiles of one w tile run on the same XCD and share
-// its L2. A library GEMM of these shapes picks output tiles so large that a
-// 3072-row projection of 32 tokens runs on 48 workgroups.
+// 16-token tile of x; its 8 wavefronts take 8 equal slices of k. A wavefront
+// moves its slice in steps of 64 columns: each load instruction reads 4 rows
+// x 256 contiguous bytes (w, then x), the step is written to the wavefront's
+// own LDS tile with 16-byte slots XOR-swizzled by row, and read back in the
+// MFMA operand layout (lane (kk, j) takes row j, columns 16u + 4kk..+3), the
+// swizzle keeping both the writes and the reads free of bank conflicts. Two
+// steps of loads are in flight in registers; a wavefront's LDS accesses run
+// in order, so one LDS tile per wavefront suffices. The 8 partial tiles are
+// summed through LDS in wave order, so results do not depend on timing.
+// blockIdx = n_tile + n_tiles * m_tile: with n_tiles a multiple of 8, the
+// token tiles of one w tile run on the same XCD and share its L2. A library
+// GEMM of these shapes picks output tiles so large that a 3072-row
+// projection of 32 tokens runs on 48 workgroups.
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 constexpr int kSkinnyMaxM = 64;
 constexpr int kSkinnyWaves = 8;
+constexpr int kSkinnyCols = 64;  // k columns per step
 
 __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_kernel(const float *__restrict__ w,
                                                                    const float *__restrict__ x,
                                                                    float *out, const float *residual,
                                                                    int n_out, int k, int m, int n_tiles) {
+  __shared__ __attribute__((aligned(16))) float s_tile[kSkinnyWaves][2][16][kSkinnyCols];
   __shared__ float s_red[kSkinnyWaves][64][4];
   const int nt = blockIdx.x % n_tiles;
   const int mt = blockIdx.x / n_tiles;
@@ -265,36 +273,59 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_kernel(const float *
   const int j = lane & 15;
   const int kk = lane >> 4;
   const int n0 = nt * 16, m0 = mt * 16;
-  // A operand: w row n0 + j; B operand: token m0 + j (clamped; its outputs
-  // are not written). Lane group kk covers k = kb + 8 kk .. kb + 8 kk + 7.
-  const float *wr = w + static_cast<size_t>(n0 + j) * k + 8 * kk;
-  const float *xr = x + static_cast<size_t>(min(m0 + j, m - 1)) * k + 8 * kk;
-  const int kw = k / kSkinnyWaves;  // a multiple of 32
+  const int kw = k / kSkinnyWaves;  // a multiple of 2 * kSkinnyCols
   const int kb0 = wave * kw;
-  const int n_steps = kw / 32;
-  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-  float4 a0 = *reinterpret_cast<const float4 *>(wr + kb0);
-  float4 a1 = *reinterpret_cast<const float4 *>(wr + kb0 + 4);
-  float4 b0 = *reinterpret_cast<const float4 *>(xr + kb0);
-  float4 b1 = *reinterpret_cast<const float4 *>(xr + kb0 + 4);
-  for (int s = 0; s < n_steps; ++s) {
-    const float4 ca0 = a0, ca1 = a1, cb0 = b0, cb1 = b1;
-    if (s + 1 < n_steps) {  // the next step's loads fly during this step's MFMAs
-      const int kb = kb0 + 32 * (s + 1);
-      a0 = *reinterpret_cast<const float4 *>(wr + kb);
-      a1 = *reinterpret_cast<const float4 *>(wr + kb + 4);
-      b0 = *reinterpret_cast<const float4 *>(xr + kb);
-      b1 = *reinterpret_cast<const float4 *>(xr + kb + 4);
-    }
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ca0.x, cb0.x, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ca0.y, cb0.y, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ca0.z, cb0.z, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ca0.w, cb0.w, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ca1.x, cb1.x, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ca1.y, cb1.y, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ca1.z, cb1.z, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ca1.w, cb1.w, acc, 0, 0, 0);
+  const int n_steps = kw / kSkinnyCols;
+  // staging: instruction i reads rows 4i + lane / 16, 16-byte column lane % 16
+  const int sc = lane & 15;
+  const float *wsrc[4], *xsrc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 4 * i + (lane >> 4);
+    wsrc[i] = w + static_cast<size_t>(n0 + r) * k + kb0 + 4 * sc;
+    xsrc[i] = x + static_cast<size_t>(min(m0 + r, m - 1)) * k + kb0 + 4 * sc;  // clamped token
   }
+  float(*tw)[kSkinnyCols] = s_tile[wave][0];
+  float(*tx)[kSkinnyCols] = s_tile[wave][1];
+  floatx4 rw0[4], rx0[4], rw1[4], rx1[4];  // two steps in flight
+  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+  auto load_step = [&](floatx4 (&rw)[4], floatx4 (&rx)[4], int step) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      rw[i] = *reinterpret_cast<const floatx4 *>(wsrc[i] + kSkinnyCols * step);
+      rx[i] = *reinterpret_cast<const floatx4 *>(xsrc[i] + kSkinnyCols * step);
+    }
+  };
+  // store a register set as the current step, refill it with step `next`
+  // (if any), then multiply the step out of LDS
+  auto body = [&](floatx4 (&rw)[4], floatx4 (&rx)[4], int next) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 4 * i + (lane >> 4);
+      *reinterpret_cast<floatx4 *>(&tw[r][4 * (sc ^ r)]) = rw[i];
+      *reinterpret_cast<floatx4 *>(&tx[r][4 * (sc ^ r)]) = rx[i];
+    }
+    if (next >= 0) load_step(rw, rx, next);
+    __builtin_amdgcn_sched_barrier(0);  // the refill stays ahead of this step's reads and MFMAs
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int slot = (4 * u + kk) ^ j;
+      const floatx4 a = *reinterpret_cast<const floatx4 *>(&tw[j][4 * slot]);
+      const floatx4 c = *reinterpret_cast<const floatx4 *>(&tx[j][4 * slot]);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[0], c[0], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[1], c[1], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[2], c[2], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[3], c[3], acc, 0, 0, 0);
+    }
+  };
+  load_step(rw0, rx0, 0);
+  load_step(rw1, rx1, 1);
+  for (int s = 0; s + 2 < n_steps; s += 2) {  // n_steps is even: every refill is a real step
+    body(rw0, rx0, s + 2);
+    body(rw1, rx1, s + 3);
+  }
+  body(rw0, rx0, -1);
+  body(rw1, rx1, -1);
   // lane l, register r: w row n0 + 4 (l / 16) + r, token m0 + l % 16
 #pragma unroll
   for (int r = 0; r < 4; ++r) s_red[wave][lane][r] = acc[r];
@@ -316,7 +347,8 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_kernel(const float *
 }
 
 bool skinny_ok(int64_t n_out, int64_t k, int64_t m, std::initializer_list<const void *> ptrs) {
-  if (m < 2 || m > kSkinnyMaxM || n_out % 16 != 0 || k % (32 * kSkinnyWaves) != 0) return false;
+  if (m < 2 || m > kSkinnyMaxM || n_out % 16 != 0 || k % (2 * kSkinnyCols * kSkinnyWaves) != 0)
+    return false;
   for (const void *p : ptrs)
     if (p && !ikv::aligned16(p)) return false;
   return true;
