@@ -346,14 +346,19 @@ def model_bench(configs, cpu_tokens):
 
     res = {}
     gpu_tokens0 = None
-    runs = [(c, 0) for c in configs]
+    runs = [(c, 0, False) for c in configs]
     if 3 in configs:
-        runs.append((3, 256))  # config 3 again on a paged cache of 256-token blocks
-    for c, bt in runs:
+        runs.append((3, 256, False))  # config 3 again on a paged cache of 256-token blocks
+        # and on the HBM <-> host offload tier, HBM budget = every layer of the sequence: each
+        # new sequence's layers start in pinned host memory and are uploaded at first use
+        runs.append((3, 0, True))
+    for c, bt, off in runs:
         arch, P, N = MODEL_CONFIGS[c]
         cfg = getattr(qwen3, arch)
+        layer_bytes = (P + N) * cfg.n_head_kv * cfg.head_dim * 4 * 2
         t0 = time.perf_counter()
-        eng = qwen3.Qwen3Engine(cfg, P + N, block_tokens=bt)
+        eng = qwen3.Qwen3Engine(cfg, P + N, block_tokens=bt,
+                                offload_hbm_bytes=cfg.n_layer * layer_bytes if off else 0)
         eng.init_synthetic(synth.config_seed(c, 1), threads=16)
         init_s = time.perf_counter() - t0
         prompt = synth.uniform_ints(synth.config_seed(c, 0), P, cfg.n_vocab)
@@ -362,7 +367,9 @@ def model_bench(configs, cpu_tokens):
         # (the library loads its kernels on first use)
         eng.generate(prompt, 4)
         # 3 timed runs, medians reported (benchmarks/cpu/bench.cpp:421-431)
+        kv0 = eng.kv_stats() if off else None
         runs3 = [eng.generate(prompt, N) for _ in range(3)]
+        kv1 = eng.kv_stats() if off else None
         toks = runs3[0][0]
         if any(r[0] != toks for r in runs3[1:]):
             raise RuntimeError(f"config {c}: repeated runs gave different tokens")
@@ -372,7 +379,8 @@ def model_bench(configs, cpu_tokens):
         eng.close()
         if c == 0:
             gpu_tokens0 = toks
-        res[f"config{c}" + (f"_paged{bt}" if bt else "")] = {
+        key = f"config{c}" + (f"_paged{bt}" if bt else "") + ("_offload" if off else "")
+        res[key] = {
             "model": arch.lower().replace("_", "-").replace("-0-6b", "-0.6b"),
             "prompt": P, "generated": N, "ttft_ms": round(ttft_med * 1e3, 3),
             "tpot_ms": round(t.tpot_s * 1e3, 4), "decode_tok_s": round(1 / t.tpot_s, 1),
@@ -383,8 +391,20 @@ def model_bench(configs, cpu_tokens):
                                      for _, sh in qwen3.tensor_layout(cfg)) * 4 / 2**30, 2),
             "init_s": round(init_s, 1),
         }
-        log(f"[bench] model config {c}{f' paged {bt}' if bt else ''} ({arch}, P={P}, N={N}): "
-            f"TTFT {ttft_med * 1e3:.2f} ms, TPOT {t.tpot_s * 1e3:.3f} ms (medians of 3)")
+        if off:
+            # per timed run: the bytes uploaded host -> HBM, and the rate implied by the TTFT
+            # over the all-HBM run of the same config (the uploads sit in the prefill step)
+            per_run = {k: (kv1[k] - kv0[k]) // 3 for k in kv1}
+            r = res[key]
+            r["kv_per_run"] = per_run
+            base = res.get(f"config{c}")
+            if base and r["ttft_ms"] > base["ttft_ms"]:
+                r["page_in_gbs_vs_hbm_ttft"] = round(
+                    per_run["bytes_in"] / ((r["ttft_ms"] - base["ttft_ms"]) * 1e-3) / 1e9, 1)
+        tail = f", per run {res[key]['kv_per_run']}" if off else ""
+        log(f"[bench] model config {c}{f' paged {bt}' if bt else ''}{' offload' if off else ''} "
+            f"({arch}, P={P}, N={N}): TTFT {ttft_med * 1e3:.2f} ms, TPOT {t.tpot_s * 1e3:.3f} ms "
+            f"(medians of 3){tail}")
     if cpu_tokens and 0 in configs:
         import oracle
 
