@@ -350,7 +350,7 @@ def model_bench(configs, cpu_tokens):
     if 3 in configs:
         runs.append((3, 256, False))  # config 3 again on a paged cache of 256-token blocks
         # and on the HBM <-> host offload tier, HBM budget = every layer of the sequence: each
-        # new sequence's layers start in pinned host memory and are uploaded at first use
+        # new sequence's layers start in pinned host memory holding no rows, so nothing moves
         runs.append((3, 0, True))
     for c, bt, off in runs:
         arch, P, N = MODEL_CONFIGS[c]
@@ -398,7 +398,7 @@ def model_bench(configs, cpu_tokens):
             r = res[key]
             r["kv_per_run"] = per_run
             base = res.get(f"config{c}")
-            if base and r["ttft_ms"] > base["ttft_ms"]:
+            if base and per_run["bytes_in"] > 0 and r["ttft_ms"] > base["ttft_ms"]:
                 r["page_in_gbs_vs_hbm_ttft"] = round(
                     per_run["bytes_in"] / ((r["ttft_ms"] - base["ttft_ms"]) * 1e-3) / 1e9, 1)
         tail = f", per run {res[key]['kv_per_run']}" if off else ""

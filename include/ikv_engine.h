@@ -57,7 +57,9 @@ int ikv_qwen3_create_paged(const ikv_qwen3_config *cfg, int device, int64_t max_
  * offloadKVStorage.hpp): every layer's cache has a pinned host copy, and at
  * most hbm_bytes of them are resident in HBM; a layer is uploaded when a step
  * acquires it, and the least recently used layer is written back and
- * dropped to make room. Tokens are those of the all-HBM cache. */
+ * dropped to make room. Only token rows that hold data move: an upload copies
+ * the rows the host copy holds (none for a new sequence), a write-back the
+ * rows written since the upload. Tokens are those of the all-HBM cache. */
 int ikv_qwen3_create_offload(const ikv_qwen3_config *cfg, int device, int64_t max_ctx,
                              uint64_t hbm_bytes, ikv_qwen3 **out);
 

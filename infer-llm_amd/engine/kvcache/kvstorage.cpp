@@ -14,15 +14,17 @@ void KVStorage::free(StorageId id) noexcept {
   _states.erase(id);
 }
 
-infer::expected<KVStorageObject, std::error_code> KVStorage::acquire(StorageId id, std::size_t layer) {
+infer::expected<KVStorageObject, std::error_code> KVStorage::acquire(StorageId id, std::size_t layer,
+                                                                   const KVObjectAccessRequest *request) {
   auto it = _states.find(id);
   if (it == _states.end() || it->second.pending_free || it->second.layer != layer ||
       layer >= _backend_layer.size() || !_backend_layer[layer])
     return infer::fail(std::errc::invalid_argument);
+  if (request && (request->id != id || request->layer != layer)) return infer::fail(std::errc::invalid_argument);
+  const KVObjectAccessRequest req = request ? *request : KVObjectAccessRequest{.id = id, .layer = layer};
   if (it->second.active_users == std::numeric_limits<std::size_t>::max())
     return infer::fail(std::errc::value_too_large);
   if (it->second.active_users == 0) {
-    KVObjectAccessRequest req{.id = id, .layer = layer};
     auto prepared = prepare_object(req);
     if (!prepared) return infer::unexpected(prepared.error());
     it = _states.find(id);  // prepare may have touched the table
@@ -34,7 +36,7 @@ infer::expected<KVStorageObject, std::error_code> KVStorage::acquire(StorageId i
       !obj.k_base || !obj.v_base)
     return infer::fail(std::errc::invalid_argument);
   ++st.active_users;
-  record_access(id);
+  record_access(req);
   return obj;
 }
 

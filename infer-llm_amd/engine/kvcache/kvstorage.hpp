@@ -17,11 +17,16 @@
 #include "../expected.hpp"
 #include "kvutil.hpp"
 
+// What one access does with an object, in the object's own token rows:
+// reads rows [0, history_tokens) written by earlier accesses, and writes
+// rows `writable`. ranges_known false: unknown (treated as any row read or
+// written).
 struct KVObjectAccessRequest {
   StorageId id = kInvalidStorageId;
   std::size_t layer = 0;
   std::size_t history_tokens = 0;
   TokenRange writable;
+  bool ranges_known = false;
 };
 
 struct KVStorageObject {
@@ -52,7 +57,10 @@ class KVStorage {
   // Gives up ownership: destroyed now, or when the last user releases it.
   void free(StorageId id) noexcept;
   // Prepares the object for its layer's backend; on success active_users++.
-  infer::expected<KVStorageObject, std::error_code> acquire(StorageId id, std::size_t layer);
+  // request, if not NULL, says which rows this access reads and writes (its
+  // id and layer must match).
+  infer::expected<KVStorageObject, std::error_code> acquire(StorageId id, std::size_t layer,
+                                                          const KVObjectAccessRequest *request = nullptr);
   void release_access(StorageId id) noexcept;
 
   // Introspection for tests and tools.
@@ -70,8 +78,9 @@ class KVStorage {
   virtual infer::expected<void, std::error_code> prepare_object(const KVObjectAccessRequest &req) = 0;
   // Called only with active_users == 0; the base erases the entry after it.
   virtual void destroy_object(StorageId id) noexcept = 0;
-  // Called on every successful acquire (recency for eviction policies).
-  virtual void record_access(StorageId) noexcept {}
+  // Called on every successful acquire, with that acquire's request
+  // (recency for eviction policies, rows written for write-back).
+  virtual void record_access(const KVObjectAccessRequest &) noexcept {}
 
   std::unordered_map<StorageId, StorageState> _states;
   std::vector<KVLayerSpec> _layers;

@@ -20,17 +20,43 @@ infer::expected<KVLayerAccess, std::error_code> KVStrategy::acquire_layer(Sequen
   auto write_map = lookup(id, layer, pending);
   if (!write_map) return infer::unexpected(write_map.error());
 
+  // Per object, in its own rows: the rows written (the pending slices) and the
+  // history read before them (the readable slices up to the first written row).
+  std::unordered_map<StorageId, KVObjectAccessRequest> requests;
+  std::unordered_map<StorageId, std::size_t> read_end;
+  for (const auto *slices : {&read_map->k, &read_map->v})
+    for (const KVSlice &sl : *slices) {
+      std::size_t &e = read_end[sl.storage_id];
+      e = std::max(e, sl.token_offset + sl.token_count);
+    }
+  for (const auto *slices : {&write_map->k, &write_map->v})
+    for (const KVSlice &sl : *slices) {
+      auto [it, fresh] = requests.try_emplace(sl.storage_id, KVObjectAccessRequest{.id = sl.storage_id,
+                                                                                  .layer = layer,
+                                                                                  .ranges_known = true});
+      TokenRange &w = it->second.writable;
+      const std::size_t b = fresh ? sl.token_offset : std::min(w.begin, sl.token_offset);
+      const std::size_t e = fresh ? sl.token_offset + sl.token_count
+                                  : std::max(w.end(), sl.token_offset + sl.token_count);
+      w = TokenRange{.begin = b, .count = e - b};
+    }
+  for (const auto &[sid, e] : read_end) {
+    auto [it, fresh] = requests.try_emplace(sid, KVObjectAccessRequest{.id = sid, .layer = layer,
+                                                                       .ranges_known = true});
+    it->second.history_tokens = fresh ? e : std::min(e, it->second.writable.begin);
+  }
+
   KVLayerAccess access;
   access._owner = this;
   access.n_past = n_past;
   access.n_new = n_new;
   std::unordered_map<StorageId, KVStorageObject> objects;
-  auto readable = make_KVRangeAccess(*read_map, read_range, layer, objects, access);
+  auto readable = make_KVRangeAccess(*read_map, read_range, layer, objects, access, &requests);
   if (!readable) {
     (void)release_layer(access);
     return infer::unexpected(readable.error());
   }
-  auto writable = make_KVRangeAccess(*write_map, pending, layer, objects, access);
+  auto writable = make_KVRangeAccess(*write_map, pending, layer, objects, access, &requests);
   if (!writable) {
     (void)release_layer(access);
     return infer::unexpected(writable.error());
@@ -63,7 +89,8 @@ infer::expected<void, std::error_code> KVStrategy::release_layer(KVLayerAccess &
 // 73-168). Each storage object is acquired once per access.
 infer::expected<KVRangeAccess, std::error_code> KVStrategy::make_KVRangeAccess(
     const KVMapping &mapping, TokenRange range, std::size_t layer,
-    std::unordered_map<StorageId, KVStorageObject> &objects, KVLayerAccess &access) {
+    std::unordered_map<StorageId, KVStorageObject> &objects, KVLayerAccess &access,
+    const std::unordered_map<StorageId, KVObjectAccessRequest> *requests) {
   if (!_storage || layer >= _layers.size()) return infer::fail(std::errc::invalid_argument);
   const KVLayerSpec &spec = _layers[layer];
   Backend *backend = objects.empty() ? nullptr : objects.begin()->second.backend;
@@ -91,7 +118,12 @@ infer::expected<KVRangeAccess, std::error_code> KVStrategy::make_KVRangeAccess(
         return infer::fail(std::errc::invalid_argument);
       auto it = objects.find(slice.storage_id);
       if (it == objects.end()) {
-        auto acquired = _storage->acquire(slice.storage_id, layer);
+        const KVObjectAccessRequest *req = nullptr;
+        if (requests) {
+          auto r = requests->find(slice.storage_id);
+          if (r != requests->end()) req = &r->second;
+        }
+        auto acquired = _storage->acquire(slice.storage_id, layer, req);
         if (!acquired) return infer::unexpected(acquired.error());
         access._storage_ids.push_back(slice.storage_id);
         it = objects.emplace(slice.storage_id, *acquired).first;

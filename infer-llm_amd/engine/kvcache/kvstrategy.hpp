@@ -51,9 +51,12 @@ class KVStrategy {
 
   virtual infer::expected<KVMapping, std::error_code> lookup(SequenceId id, std::size_t layer,
                                                              TokenRange range) const = 0;
+  // requests: per object, the rows this access reads and writes (passed to
+  // the storage's acquire; NULL or a missing entry: unknown).
   infer::expected<KVRangeAccess, std::error_code> make_KVRangeAccess(
       const KVMapping &mapping, TokenRange range, std::size_t layer,
-      std::unordered_map<StorageId, KVStorageObject> &objects, KVLayerAccess &access);
+      std::unordered_map<StorageId, KVStorageObject> &objects, KVLayerAccess &access,
+      const std::unordered_map<StorageId, KVObjectAccessRequest> *requests = nullptr);
 
   std::unique_ptr<KVStorage> _storage;
   std::vector<KVLayerSpec> _layers;

@@ -149,7 +149,7 @@ infer::expected<void, std::error_code> OffloadKVStorage::make_room(Backend &back
       if (s == _states.end() || s->second.active_users != 0) continue;
       cands.push_back({.id = id,
                        .resident_bytes = st.dev->bytes,
-                       .writeback_bytes = (st.dev_dirty || !st.host) ? st.dev->bytes : 0,
+                       .writeback_bytes = writeback_bytes(id, st),
                        .last_access_order = st.last_access_order,
                        .admission_order = st.admission_order});
     }
@@ -170,13 +170,22 @@ infer::expected<void, std::error_code> OffloadKVStorage::writeback(StorageId id)
     auto mem = _config.host_backend->alloc(BufferKind::KVCACHE, st.dev->bytes);
     if (!mem) return infer::unexpected(mem.error());
     st.host = Copy{_config.host_backend, *mem, st.dev->bytes};
+    st.host_valid = 0;
   }
-  // The device backend's copy is ordered after its queued kernels.
-  const Tensor dev = bytes_view(st.dev->base, st.dev->bytes);
-  if (auto r = st.dev->backend->copy_tensor_get(&dev, st.host->base, 0, st.dev->bytes); !r) return r;
-  st.dev_dirty = false;
-  ++_stats.page_outs;
-  _stats.bytes_out += st.dev->bytes;
+  const auto [lo, hi] = writeback_rows(id, st);
+  if (lo < hi) {
+    // The device backend's copies are ordered after its queued kernels.
+    const RowBytes rb = row_bytes(id, lo, hi);
+    const Tensor dev = bytes_view(st.dev->base, st.dev->bytes);
+    auto *h = static_cast<std::byte *>(st.host->base);
+    if (auto r = st.dev->backend->copy_tensor_get(&dev, h + rb.k_off, rb.k_off, rb.k_len); !r) return r;
+    if (auto r = st.dev->backend->copy_tensor_get(&dev, h + rb.v_off, rb.v_off, rb.v_len); !r) return r;
+    st.host_valid = std::max(st.host_valid, hi);
+    ++_stats.page_outs;
+    _stats.bytes_out += rb.k_len + rb.v_len;
+  }
+  st.dirty_lo = SIZE_MAX;
+  st.dirty_hi = 0;
   return {};
 }
 
@@ -187,7 +196,7 @@ infer::expected<void, std::error_code> OffloadKVStorage::evict(StorageId id) {
   ObjectState &st = it->second;
   if (!st.dev) return {};
   if (s->second.active_users != 0) return infer::fail(std::errc::device_or_resource_busy);
-  if (st.dev_dirty || !st.host) {
+  if (st.dirty() || !st.host) {
     if (auto r = writeback(id); !r) return r;  // the HBM copy stays on failure
   }
   // No queued kernel may still read the HBM copy when it is freed.
@@ -223,15 +232,22 @@ infer::expected<void, std::error_code> OffloadKVStorage::ensure_resident(Storage
   }
   auto mem = backend->alloc(BufferKind::KVCACHE, bytes);
   if (!mem) return infer::unexpected(mem.error());
-  Tensor dev = bytes_view(*mem, bytes);
-  if (auto r = backend->copy_tensor_set(&dev, st.host->base, 0, bytes); !r) {
-    backend->free(BufferKind::KVCACHE, *mem);
-    return r;
+  if (st.host_valid > 0) {  // the rows the host copy holds, of K and of V
+    const RowBytes rb = row_bytes(id, 0, st.host_valid);
+    Tensor dev = bytes_view(*mem, bytes);
+    const auto *h = static_cast<const std::byte *>(st.host->base);
+    auto r = backend->copy_tensor_set(&dev, h + rb.k_off, rb.k_off, rb.k_len);
+    if (r) r = backend->copy_tensor_set(&dev, h + rb.v_off, rb.v_off, rb.v_len);
+    if (!r) {
+      backend->free(BufferKind::KVCACHE, *mem);
+      return r;
+    }
+    ++_stats.page_ins;
+    _stats.bytes_in += rb.k_len + rb.v_len;
   }
   st.dev = Copy{backend, *mem, bytes};
-  st.dev_dirty = false;
-  ++_stats.page_ins;
-  _stats.bytes_in += bytes;
+  st.dirty_lo = SIZE_MAX;
+  st.dirty_hi = 0;
   point_object_at(id, &*st.dev);
   return {};
 }
@@ -239,15 +255,56 @@ infer::expected<void, std::error_code> OffloadKVStorage::ensure_resident(Storage
 infer::expected<void, std::error_code> OffloadKVStorage::prepare_object(const KVObjectAccessRequest &req) {
   if (req.layer >= _layers.size() || !_states.contains(req.id))
     return infer::fail(std::errc::invalid_argument);
-  if (auto r = ensure_resident(req.id, true); !r) return r;
-  // The access may append rows: the host copy is stale from here on.
-  _objects[req.id].dev_dirty = true;
-  return {};
+  return ensure_resident(req.id, true);
 }
 
-void OffloadKVStorage::record_access(StorageId id) noexcept {
-  auto it = _objects.find(id);
-  if (it != _objects.end()) it->second.last_access_order = ++_clock;
+void OffloadKVStorage::record_access(const KVObjectAccessRequest &req) noexcept {
+  auto it = _objects.find(req.id);
+  auto s = _states.find(req.id);
+  if (it == _objects.end() || s == _states.end()) return;
+  ObjectState &st = it->second;
+  st.last_access_order = ++_clock;
+  // The rows this access may write; not known: all of them.
+  const std::size_t cap = s->second.object.capacity_tokens;
+  std::size_t lo = 0, hi = cap;
+  if (req.ranges_known) {
+    if (req.writable.empty()) return;
+    lo = std::min(req.writable.begin, cap);
+    hi = std::min(req.writable.end(), cap);
+  }
+  if (st.dev) {
+    st.dirty_lo = std::min(st.dirty_lo, lo);
+    st.dirty_hi = std::max(st.dirty_hi, hi);
+  } else if (st.host) {  // a host-computed layer writes its host copy
+    st.host_valid = std::max(st.host_valid, hi);
+  }
+}
+
+OffloadKVStorage::RowBytes OffloadKVStorage::row_bytes(StorageId id, std::size_t lo, std::size_t hi) const {
+  const StorageState &ss = _states.at(id);
+  const KVLayerSpec &sp = _layers[ss.layer];
+  const std::size_t k_row = sp.n_kv_heads * sp.k_head_dim * dataType_size(sp.k_type);
+  const std::size_t v_row = sp.n_kv_heads * sp.v_head_dim * dataType_size(sp.v_type);
+  const std::size_t k_bytes = k_row * ss.object.capacity_tokens;
+  return {.k_off = lo * k_row, .v_off = k_bytes + lo * v_row, .k_len = (hi - lo) * k_row,
+          .v_len = (hi - lo) * v_row};
+}
+
+std::pair<std::size_t, std::size_t> OffloadKVStorage::writeback_rows(StorageId id, const ObjectState &st) const {
+  if (!st.dirty()) return {0, 0};
+  // Rows the host copy lacks that the HBM copy may hold start at host_valid
+  // at the latest (everything below it was uploaded unchanged unless dirty).
+  const std::size_t cap = _states.at(id).object.capacity_tokens;
+  const std::size_t hi = std::min(st.dirty_hi, cap);
+  const std::size_t lo = std::min({st.dirty_lo, st.host ? st.host_valid : 0, hi});
+  return {lo, hi};
+}
+
+std::size_t OffloadKVStorage::writeback_bytes(StorageId id, const ObjectState &st) const {
+  const auto [lo, hi] = writeback_rows(id, st);
+  if (lo >= hi) return 0;
+  const RowBytes rb = row_bytes(id, lo, hi);
+  return rb.k_len + rb.v_len;
 }
 
 infer::expected<std::size_t, std::error_code> OffloadKVStorage::prefetch(const KVPrefetchContext &context) {

@@ -10,10 +10,20 @@
 // acquire() makes it resident (uploading the host copy), under a hard
 // per-device byte budget; when the budget is full, the eviction policy picks
 // an object nobody holds, its HBM copy is written back to the host (if
-// kernels may have written it since it was uploaded) and freed. Objects are
-// moved whole, with the backend's synchronous copies, so the stream's queued
-// kernels finish before any copy or free. No disk tier (the reference
-// declares one and implements none of it).
+// kernels may have written it since it was uploaded) and freed.
+//
+// Only token rows that hold data move (the reference's per-copy valid_tokens,
+// offloadKVStorage.hpp:113-160): a host copy holds rows [0, host_valid) as of
+// its last write-back (0 when new), and an upload copies those rows of K and
+// of V; each access names the rows it writes (KVObjectAccessRequest), and a
+// write-back copies the rows written since the HBM copy was made, from
+// min(first written row, host_valid) on. So a new sequence's first step
+// uploads nothing, and a switch between sequences moves each cache's
+// committed rows in, and only the rows written since, out. An access whose
+// rows are not known marks the whole object written. Copies use the
+// backend's synchronous copies, so the stream's queued kernels finish before
+// any copy or free. No disk tier (the reference declares one and implements
+// none of it).
 #pragma once
 
 #include <cstddef>
@@ -23,6 +33,7 @@
 #include <span>
 #include <string>
 #include <unordered_map>
+#include <utility>
 #include <vector>
 
 #include "kvstorage.hpp"
@@ -51,8 +62,9 @@ class LRUKVEvictionPolicy final : public KVEvictionPolicy {
   std::optional<StorageId> select_victim(std::span<const KVEvictionCandidate> candidates) const override;
 };
 
-// history_tokens: the committed prefix the next access reads (the whole
-// object is moved here, so it only orders and filters requests).
+// history_tokens: the committed prefix the next access reads (an upload
+// copies the rows the host copy holds, so it only orders and filters
+// requests).
 struct KVPrefetchRequest {
   StorageId id = kInvalidStorageId;
   std::size_t history_tokens = 0;
@@ -136,7 +148,7 @@ class OffloadKVStorage final : public KVStorage {
  protected:
   infer::expected<void, std::error_code> prepare_object(const KVObjectAccessRequest &req) override;
   void destroy_object(StorageId id) noexcept override;
-  void record_access(StorageId id) noexcept override;
+  void record_access(const KVObjectAccessRequest &req) noexcept override;
 
  private:
   struct Copy {
@@ -146,9 +158,23 @@ class OffloadKVStorage final : public KVStorage {
   };
   struct ObjectState {
     std::optional<Copy> host, dev;
-    bool dev_dirty = false;  // kernels may have written the HBM copy since upload
+    std::size_t host_valid = 0;  // rows [0, host_valid) of the host copy hold data
+    // Rows [dirty_lo, dirty_hi) of the HBM copy may have been written by
+    // kernels since it was made or last written back (empty: lo >= hi).
+    std::size_t dirty_lo = SIZE_MAX, dirty_hi = 0;
     std::uint64_t last_access_order = 0, admission_order = 0;
+    bool dirty() const { return dirty_lo < dirty_hi; }
   };
+  // The byte range of rows [lo, hi) within the K region and within the V
+  // region of an object of this storage's layer `layer`.
+  struct RowBytes {
+    std::size_t k_off, v_off, k_len, v_len;
+  };
+  RowBytes row_bytes(StorageId id, std::size_t lo, std::size_t hi) const;
+  // The rows a write-back of this object would copy: [lo, hi), empty if none,
+  // and their bytes (K and V).
+  std::pair<std::size_t, std::size_t> writeback_rows(StorageId id, const ObjectState &st) const;
+  std::size_t writeback_bytes(StorageId id, const ObjectState &st) const;
 
   const KVDeviceBudget *budget_for(const Backend *backend) const;
   infer::expected<void, std::error_code> ensure_resident(StorageId id, bool may_evict);

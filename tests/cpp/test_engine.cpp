@@ -375,9 +375,11 @@ static void offload_cpu_tests() {
         "sequence: one host copy per layer, nothing in HBM yet");
   CHECK(kv.reserve_append(*sid, 4), "reserve");
   const StorageId id0 = 1, id1 = 2, id2 = 3;
+  const size_t row = 8 * 128 * 4 * 2;  // one token row of K and of V
   auto a0 = kv.acquire_layer(*sid, 0);
-  CHECK(a0 && st->resident(id0) && st->stats().page_ins == 1 && st->resident_bytes(&dev) == obj,
-        "acquire uploads the layer");
+  CHECK(a0 && st->resident(id0) && st->stats().page_ins == 0 && st->stats().bytes_in == 0 &&
+            st->resident_bytes(&dev) == obj,
+        "acquire makes a new layer resident without a transfer (its host copy holds no rows)");
   // write a pattern through the view (the HBM copy)
   float *k0 = a0 ? static_cast<float *>(a0->readable.k.front().view.data) : nullptr;
   if (k0)
@@ -387,8 +389,8 @@ static void offload_cpu_tests() {
   if (a1) (void)kv.release_layer(*a1);
   auto a2 = kv.acquire_layer(*sid, 2);
   CHECK(a2 && !st->resident(id0) && st->resident(id1) && st->resident(id2) && st->stats().evictions == 1 &&
-            st->stats().page_outs == 1,
-        "budget of two: the least recently used layer is written back and dropped");
+            st->stats().page_outs == 1 && st->stats().bytes_out == 4 * row,
+        "budget of two: the least recently used layer is written back (its 4 written rows) and dropped");
   if (a2) (void)kv.release_layer(*a2);
   auto b0 = kv.acquire_layer(*sid, 0);
   bool same = b0.has_value();
@@ -396,7 +398,9 @@ static void offload_cpu_tests() {
     const float *k = static_cast<const float *>(b0->readable.k.front().view.data);
     for (int i = 0; i < 4 * 1024 && same; ++i) same = k[i] == float(i) * 0.5f;
   }
-  CHECK(same && !st->resident(id1) && st->resident(id0), "paged back in with its rows; LRU victim next was layer 1");
+  CHECK(same && !st->resident(id1) && st->resident(id0) && st->stats().page_ins == 1 &&
+            st->stats().bytes_in == 4 * row,
+        "paged back in with its 4 rows; LRU victim next was layer 1");
   auto b2 = kv.acquire_layer(*sid, 2);
   auto b1 = kv.acquire_layer(*sid, 1);
   CHECK(b0 && b2 && !b1 && is_err(b1.error(), std::errc::not_enough_memory),
@@ -599,8 +603,8 @@ static void gpu_tests() {
 }
 
 // Two sequences on an offloaded cache whose HBM budget holds one sequence's
-// layers: every switch writes the other sequence's layers back to pinned
-// host memory and uploads this one's. Attention within tolerance of the
+// layers: every switch writes the rows the other sequence's last step wrote
+// back to pinned host memory and uploads this one's committed rows. Attention within tolerance of the
 // oracle and cache rows bit-exact, after every switch.
 static void offload_gpu_tests(HIPBackend *hip) {
   const int Hq = 16, Hkv = 8, D = 128, L = 2, P = 21, N = 3;
@@ -654,9 +658,23 @@ static void offload_gpu_tests(HIPBackend *hip) {
   }
   Scheduler sched(hip);
   bool all_ok = seqs[0].sid != kInvalidSequenceId && seqs[1].sid != kInvalidSequenceId;
+  // Transfers the valid-row rules imply: a step evicts the other sequence's
+  // layers, each writing back the rows that sequence's last step wrote, and
+  // uploads this sequence's committed rows (none on its first step).
+  const size_t row = size_t(Hkv) * D * 4 * 2;
+  size_t want_in = 0, want_out = 0, want_page_ins = 0, last_n[2] = {0, 0};
+  bool first_step = true;
   for (int round = 0; round <= N && all_ok; ++round) {
     for (Seq &q : seqs) {
       const int n = round == 0 ? P : 1;
+      const size_t qi = size_t(&q - seqs);
+      if (!first_step) want_out += L * last_n[1 - qi] * row;
+      if (q.n_past > 0) {
+        want_in += L * q.n_past * row;
+        want_page_ins += L;
+      }
+      first_step = false;
+      last_n[qi] = size_t(n);
       GraphContext ctx(nullptr);
       Tensor *pos_t = ctx.make_tensor("inp_pos", GGML_TYPE_I32, {n});
       pos_t->device = DeviceType::CPU;
@@ -720,9 +738,10 @@ static void offload_gpu_tests(HIPBackend *hip) {
   }
   const OffloadStats &os = st->stats();
   CHECK(all_ok, "offload: two sequences in one sequence's HBM, attention and caches exact at every switch");
-  CHECK(os.evictions >= size_t(2 * N + 1) * L && os.page_outs == os.evictions &&
-            os.page_ins == os.evictions + L && os.bytes_in == os.page_ins * layer_bytes,
-        "offload: every switch wrote back and uploaded whole layers");
+  CHECK(os.evictions == size_t(2 * N + 1) * L && os.page_outs == os.evictions && os.page_ins == want_page_ins &&
+            os.bytes_in == want_in && os.bytes_out == want_out,
+        "offload: every switch wrote back only the rows written since the upload and uploaded only "
+        "committed rows");
   for (auto &q : seqs)
     if (q.sid != kInvalidSequenceId) (void)kv.release_sequence(q.sid);
   CHECK(st->resident_bytes(hip) == 0, "offload: released sequences leave nothing in HBM");

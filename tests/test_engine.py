@@ -27,4 +27,6 @@ def test_engine_attention_slice_on_hip_backend(dev):
     out = run("--gpu")
     assert "PASS fusions decode step 5" in out
     assert "PASS cache bit-exact, layer 1, decode step 5" in out
-    assert "PASS offload: every switch wrote back and uploaded whole layers" in out
+    assert "PASS offload: two sequences in one sequence's HBM, attention and caches exact at every switch" in out
+    assert ("PASS offload: every switch wrote back only the rows written since the upload and uploaded only "
+            "committed rows") in out
