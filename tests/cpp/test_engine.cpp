@@ -420,6 +420,61 @@ static void offload_cpu_tests() {
   CHECK(kv.commit_append(*sid) && kv.release_sequence(*sid) && dev.frees == dev_frees + 2 &&
             host.frees == host_frees + int(L),
         "release frees every copy");
+
+  // Valid rows across an aborted append and its retry: an HBM budget of one
+  // layer, so every acquire of the other layer writes this one back.
+  {
+    auto own = make({{.backend = &dev, .resident_bytes = obj, .prefetch_bytes = 0}});
+    OffloadKVStorage *s2 = own.get();
+    KVCacheManager kv2(std::make_unique<ContiguousKVStrategy>(std::move(own)));
+    const size_t L2 = 2, row_floats = 8 * 128;
+    std::vector<KVLayerSpec> specs2(L2, specs[0]);
+    std::vector<Backend *> place2(L2, &dev);
+    bool ok = bool(kv2.init(specs2, place2, KVCacheConfig{.layers = L2, .max_tokens_per_sequence = cap}));
+    auto q = kv2.create_sequence();
+    ok = ok && bool(q);
+    // one step: write rows [n_past, n_past + n) of layer 0 (K = base + i,
+    // V = -(base + i) by float index i), touch layer 1, then commit or abort
+    auto step = [&](size_t n, float base, bool commit) {
+      if (!kv2.reserve_append(*q, n)) return false;
+      auto a = kv2.acquire_layer(*q, 0);
+      if (!a) return false;
+      auto *k = static_cast<float *>(a->readable.k.front().view.data);
+      auto *v = static_cast<float *>(a->readable.v.front().view.data);
+      for (size_t i = a->n_past * row_floats; i < (a->n_past + n) * row_floats; ++i) {
+        k[i] = base + float(i);
+        v[i] = -(base + float(i));
+      }
+      (void)kv2.release_layer(*a);
+      auto b = kv2.acquire_layer(*q, 1);
+      if (!b) return false;
+      (void)kv2.release_layer(*b);
+      return commit ? bool(kv2.commit_append(*q)) : bool(kv2.abort_append(*q));
+    };
+    ok = ok && step(4, 100.f, true);   // rows 0..3
+    const OffloadStats after_first = s2->stats();
+    ok = ok && step(2, 500.f, false);  // rows 4..5, aborted
+    ok = ok && step(2, 900.f, true);   // rows 4..5 again
+    bool rows_ok = false;
+    if (ok && kv2.reserve_append(*q, 1)) {
+      auto c = kv2.acquire_layer(*q, 0);
+      if (c) {
+        const auto *k = static_cast<const float *>(c->readable.k.front().view.data);
+        const auto *v = static_cast<const float *>(c->readable.v.front().view.data);
+        rows_ok = true;
+        for (size_t i = 0; i < 6 * row_floats && rows_ok; ++i) {
+          const float want = (i < 4 * row_floats ? 100.f : 900.f) + float(i);
+          rows_ok = k[i] == want && v[i] == -want;
+        }
+        (void)kv2.release_layer(*c);
+      }
+      (void)kv2.abort_append(*q);
+    }
+    CHECK(ok && after_first.page_ins == 0 && after_first.bytes_out == 4 * row,
+          "first step: nothing uploaded, the 4 written rows written back");
+    CHECK(rows_ok, "a retried append's rows replace the aborted ones in the host copy");
+    if (q) (void)kv2.release_sequence(*q);
+  }
 }
 
 // ---------------------------------------------------------------------------
