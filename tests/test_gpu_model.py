@@ -292,6 +292,40 @@ def test_norm_folded_into_gemv_equals_separate_norm(dev, k):
     assert np.array_equal(host(normed).view(np.uint32), ref.view(np.uint32))
 
 
+# Products of at least 16M weight floats stage their input in LDS once per
+# workgroup and walk several row groups per wave: q/k/v at Qwen3-8B width
+# (one group per wave), twice as many rows (two per wave), odd row counts
+# (one row per group), and the 8B SwiGLU pair (four rows per wave).
+@pytest.mark.parametrize("ns", [(4096, 1024, 1024), (8192, 2048, 2048), (4095, 1025, 1023)])
+def test_staged_gemv3_folded_equals_separate_norm(dev, oracle_pool, ns):
+    k = 4096
+    x = synth.normal(30, (k,)) * 2
+    nw = 1 + 0.2 * synth.normal(31, (k,))
+    ws = [synth.normal(32 + i, (n, k), 0.02) for i, n in enumerate(ns)]
+    wd = [dev_t(w, dev) for w in ws]
+    xd, nwd = dev_t(x, dev), dev_t(nw, dev)
+    normed = ikv.rms_norm(xd[None], nwd, 1e-6)[0]
+    sep = [host(o) for o in ikv.gemv3(*wd, normed)]
+    fused = [host(o) for o in ikv.gemv3(*wd, xd, norm_w=nwd, eps=1e-6)]
+    xn = host(normed)
+    for w, a, b in zip(ws, sep, fused):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+        assert proj_close(a, w, xn[None], oracle.mul_mat(w, xn))
+
+
+def test_staged_swiglu_folded_equals_separate_norm(dev):
+    n_out, k = 12288, 4096
+    x = synth.normal(40, (k,)) * 2
+    nw = 1 + 0.2 * synth.normal(41, (k,))
+    wg = dev_t(synth.normal(42, (n_out, k), 0.02), dev)
+    wu = dev_t(synth.normal(43, (n_out, k), 0.02), dev)
+    xd, nwd = dev_t(x, dev), dev_t(nw, dev)
+    normed = ikv.rms_norm(xd[None], nwd, 1e-6)[0]
+    sep = host(ikv.gemv_swiglu(wg, wu, normed))
+    fused = host(ikv.gemv_swiglu(wg, wu, xd, norm_w=nwd, eps=1e-6))
+    assert np.array_equal(sep.view(np.uint32), fused.view(np.uint32))
+
+
 @pytest.mark.parametrize("Hq,Hkv,ctx", [(16, 8, 0), (16, 8, 37), (16, 8, 4096), (32, 8, 1000),
                                         (8, 8, 300), (64, 8, 129)])
 def test_decode_with_qk_rope_equals_separate_ops(dev, oracle_pool, Hq, Hkv, ctx):
