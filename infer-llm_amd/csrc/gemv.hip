@@ -505,7 +505,10 @@ extern "C" int ikv_mul_mat_f32(const float *w, const float *x, float *out, int64
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (m == 1) {
     if (fast_ok(k, {w, x})) {
-      const int rpw = (n_out >= 8192 && n_out % 2 == 0) ? 2
+      // two rows per wave for many rows or a large product (x is then read
+      // once per two rows); one for the small products of Qwen3-0.6B
+      const bool big = n_out >= 8192 || n_out * k >= kStagedMinFloats;
+      const int rpw = (big && n_out % 2 == 0) ? 2
                       : (n_out % IKV_GEMV_RPW_SMALL == 0 ? IKV_GEMV_RPW_SMALL : 1);
       if (rpw == 2)
         gemv_kernel<2><<<grid_for(n_out / 2), kThreads, 0, s>>>(w, x, out, residual, int(n_out), int(k));
