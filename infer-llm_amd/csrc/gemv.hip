@@ -66,6 +66,34 @@ __device__ __forceinline__ float4 normed(float4 v, float scale, float4 g) {
   return make_float4(a * g.x, b * g.y, c * g.z, d * g.w);
 }
 
+// ikv::rms_scale_strided(row, dim, eps, lane) with the lane's first kBatch
+// float4 reads (row[64 j + lane], j < kBatch) already in first: the same adds
+// in the same order, so the same scale bit for bit.
+__device__ __forceinline__ float rms_scale_from_first(const float4 (&first)[kBatch], const float4 *row,
+                                                      int dim, float eps, int lane) {
+  double s = 0.0;
+#pragma unroll
+  for (int j = 0; j < kBatch; ++j) {
+    const float4 v = first[j];
+    const float a = v.x * v.x, b = v.y * v.y, c = v.z * v.z, d = v.w * v.w;
+    s += static_cast<double>(a);
+    s += static_cast<double>(b);
+    s += static_cast<double>(c);
+    s += static_cast<double>(d);
+  }
+#pragma unroll 4
+  for (int j = kBatch; j < dim / 256; ++j) {
+    const float4 v = row[64 * j + lane];
+    const float a = v.x * v.x, b = v.y * v.y, c = v.z * v.z, d = v.w * v.w;
+    s += static_cast<double>(a);
+    s += static_cast<double>(b);
+    s += static_cast<double>(c);
+    s += static_cast<double>(d);
+  }
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+  return static_cast<float>(1.0 / sqrt(s / static_cast<double>(dim) + static_cast<double>(eps)));
+}
+
 // Sums of NR rows (row r at rows[r], K columns, K % 1024 == 0) dotted with
 // x (RMS-normalised with weight nw when nw is not null); every lane gets the
 // sums.
@@ -82,8 +110,18 @@ __device__ __forceinline__ void wave_dots(const float *const (&rows)[NR], const 
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) cur[r][j] = nt_load4(rows[r] + 4 * lane + 256 * j);
   }
-  const float scale =
-      nw ? ikv::rms_scale_strided(reinterpret_cast<const float4 *>(x), K, eps, lane) : 1.f;
+  // The first batch of x (and of the norm weights) is loaded once, with the
+  // weights: the scale's sum starts from it (lane-strided, these are its
+  // first kBatch reads) and the first batch's products use it, so no second
+  // L2 round trip follows the scale.
+  float4 x0[kBatch], g0[kBatch];
+#pragma unroll
+  for (int j = 0; j < kBatch; ++j) {
+    x0[j] = *reinterpret_cast<const float4 *>(x + 4 * lane + 256 * j);
+    if (nw) g0[j] = *reinterpret_cast<const float4 *>(nw + 4 * lane + 256 * j);
+  }
+  const float scale = nw ? rms_scale_from_first(x0, reinterpret_cast<const float4 *>(x), K, eps, lane)
+                         : 1.f;
   for (int k0 = 0; k0 < K; k0 += kBatchCols) {
     const bool more = k0 + kBatchCols < K;
     if (more) {
@@ -96,11 +134,12 @@ __device__ __forceinline__ void wave_dots(const float *const (&rows)[NR], const 
     float4 xv[kBatch];
 #pragma unroll
     for (int j = 0; j < kBatch; ++j)
-      xv[j] = *reinterpret_cast<const float4 *>(x + k0 + 4 * lane + 256 * j);
+      xv[j] = k0 == 0 ? x0[j] : *reinterpret_cast<const float4 *>(x + k0 + 4 * lane + 256 * j);
     if (nw) {
 #pragma unroll
       for (int j = 0; j < kBatch; ++j)
-        xv[j] = normed(xv[j], scale, *reinterpret_cast<const float4 *>(nw + k0 + 4 * lane + 256 * j));
+        xv[j] = normed(xv[j], scale,
+                       k0 == 0 ? g0[j] : *reinterpret_cast<const float4 *>(nw + k0 + 4 * lane + 256 * j));
     }
 #pragma unroll
     for (int r = 0; r < NR; ++r)
