@@ -17,10 +17,14 @@
 extern "C" {
 #endif
 
-/* Reads `bytes` (a multiple of 16) from src with `grid` workgroups of 256
- * threads, 16-byte loads in a grid-stride loop; each workgroup writes one
- * float of its sum to sink[blockIdx] (sink holds >= grid floats). */
-int ikv_probe_read(const void *src, size_t bytes, float *sink, int grid, void *stream);
+/* Reads `bytes` (a multiple of 16) from src with `grid` workgroups of 512
+ * threads. Workgroup b reads the b-th of `grid` contiguous slices; each lane
+ * issues `loads_per_lane` (1, 4, 8 or 16) independent 16-byte non-temporal
+ * loads before using any, so a slice of at most grid * 8 KiB * loads_per_lane
+ * bytes is in flight at once. Each workgroup writes one float of its sum to
+ * sink[blockIdx] (sink holds >= grid floats). */
+int ikv_probe_read(const void *src, size_t bytes, float *sink, int grid, int loads_per_lane,
+                   void *stream);
 
 /* Launches an empty kernel of `grid` workgroups. */
 int ikv_probe_empty(int grid, void *stream);

@@ -61,6 +61,7 @@ constexpr int WG = NWAVE * 64;
 #endif
 constexpr int R = IKV_DECODE_R;      // K and V rows per lane per iteration
 constexpr int TILE = NWAVE * 2 * R;  // tokens per workgroup iteration
+static_assert(64 % TILE == 0, "a paged block (a multiple of 64 tokens) must hold each tile whole");
 
 #ifndef IKV_DECODE_TARGET_WGS
 // Workgroups aimed for over all KV heads: one 8-wave workgroup per CU of

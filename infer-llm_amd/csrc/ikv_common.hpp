@@ -63,8 +63,10 @@ __device__ __forceinline__ float wave_sum(float v) {
 // -inf gives 0, which is what masked softmax terms need.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// A 4-term dot product as one explicit fma chain: the same rounding in every
+// kernel that uses it, whatever the compiler would contract.
 __device__ __forceinline__ float dot4(const float4 a, const float4 b) {
-  return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
+  return fmaf(a.w, b.w, fmaf(a.z, b.z, fmaf(a.y, b.y, a.x * b.x)));
 }
 
 __device__ __forceinline__ float4 fma4(float s, const float4 v, const float4 acc) {

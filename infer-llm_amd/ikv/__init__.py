@@ -114,7 +114,7 @@ SIGNATURES = {
     "ikv_synth_normal_f32": (
         _c_int, [ctypes.c_uint64, ctypes.c_uint64, _c_size_t, ctypes.c_double, _c_void_p, _c_int]),
     # include/ikv_probe.h
-    "ikv_probe_read": (_c_int, [_c_void_p, _c_size_t, _c_void_p, _c_int, _c_void_p]),
+    "ikv_probe_read": (_c_int, [_c_void_p, _c_size_t, _c_void_p, _c_int, _c_int, _c_void_p]),
     "ikv_probe_empty": (_c_int, [_c_int, _c_void_p]),
 }
 

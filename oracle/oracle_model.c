@@ -10,6 +10,7 @@
  * index order (no FMA: baseline x86-64, -ffp-contract=off); silu is
  * x / (1.0f + expf(-x)).
  */
+#include <emmintrin.h>
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -53,8 +54,77 @@ static void mm_elem(int64_t i, void *p) {
     c->out[i] = sum;
 }
 
+/* Several tokens at once (prompt steps): the same per-element arithmetic on
+ * tiles of MM_TO outputs x MM_TT tokens, so that long prompts finish in
+ * minutes. Each output element is still one float accumulator from 0.0f,
+ * updated for k = 0..K-1 in index order with a rounded product and then a
+ * rounded add: _mm_mul_ps / _mm_add_ps are four independent IEEE single
+ * multiplies / adds (SSE2, baseline x86-64, no FMA), one lane per output.
+ * Only the loop nest differs from mm_elem (16 independent chains in flight
+ * instead of one), so every element has mm_elem's bits. */
+#define MM_TO 32
+#define MM_TT 32
+
+struct mm_tile_ctx {
+    const float *w, *x;
+    float *out;
+    int64_t n_out, k, m, n_otiles;
+};
+
+static void mm_tile(int64_t i, void *p) {
+    const struct mm_tile_ctx *c = p;
+    const int64_t K = c->k;
+    const int64_t o0 = (i % c->n_otiles) * MM_TO;
+    const int64_t t0 = (i / c->n_otiles) * MM_TT;
+    const int64_t no = c->n_out - o0 < MM_TO ? c->n_out - o0 : MM_TO;
+    const int64_t nt = c->m - t0 < MM_TT ? c->m - t0 : MM_TT;
+    /* rows o0..o0+no-1 interleaved by 4: wi[(g*K + k)*4 + r] = w[o0+4g+r][k] */
+    float *wi = (float *)aligned_alloc(16, sizeof(float) * (size_t)(MM_TO * K));
+    for (int64_t g = 0; g < MM_TO / 4; ++g)
+        for (int64_t r = 0; r < 4; ++r) {
+            const int64_t o = 4 * g + r;
+            float *dst = wi + g * K * 4 + r;
+            if (o < no) {
+                const float *src = c->w + (o0 + o) * K;
+                for (int64_t kk = 0; kk < K; ++kk) dst[kk * 4] = src[kk];
+            } else {
+                for (int64_t kk = 0; kk < K; ++kk) dst[kk * 4] = 0.0f;
+            }
+        }
+    for (int64_t g = 0; 4 * g < no; ++g) {
+        const float *wg = wi + g * K * 4;
+        for (int64_t tq = 0; tq < nt; tq += 4) {
+            const float *xr[4];
+            for (int j = 0; j < 4; ++j)
+                xr[j] = c->x + (t0 + (tq + j < nt ? tq + j : tq)) * K;
+            __m128 a0 = _mm_setzero_ps(), a1 = a0, a2 = a0, a3 = a0;
+            for (int64_t kk = 0; kk < K; ++kk) {
+                const __m128 wv = _mm_load_ps(wg + kk * 4);
+                a0 = _mm_add_ps(a0, _mm_mul_ps(_mm_set1_ps(xr[0][kk]), wv));
+                a1 = _mm_add_ps(a1, _mm_mul_ps(_mm_set1_ps(xr[1][kk]), wv));
+                a2 = _mm_add_ps(a2, _mm_mul_ps(_mm_set1_ps(xr[2][kk]), wv));
+                a3 = _mm_add_ps(a3, _mm_mul_ps(_mm_set1_ps(xr[3][kk]), wv));
+            }
+            float acc[4][4];
+            _mm_storeu_ps(acc[0], a0);
+            _mm_storeu_ps(acc[1], a1);
+            _mm_storeu_ps(acc[2], a2);
+            _mm_storeu_ps(acc[3], a3);
+            for (int j = 0; j < 4 && tq + j < nt; ++j)
+                for (int r = 0; r < 4 && 4 * g + r < no; ++r)
+                    c->out[(t0 + tq + j) * c->n_out + o0 + 4 * g + r] = acc[j][r];
+        }
+    }
+    free(wi);
+}
+
 void oracle_mul_mat_f32(const float *w, const float *x, float *out, int64_t n_out, int64_t k,
                         int64_t m) {
+    if (m >= 4 && k > 0) {
+        struct mm_tile_ctx c = {w, x, out, n_out, k, m, (n_out + MM_TO - 1) / MM_TO};
+        oracle_pool_for(c.n_otiles * ((m + MM_TT - 1) / MM_TT), mm_tile, &c);
+        return;
+    }
     struct mm_ctx c = {w, x, out, n_out, k};
     oracle_pool_for(n_out * m, mm_elem, &c);
 }

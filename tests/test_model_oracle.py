@@ -86,6 +86,27 @@ def test_mul_mat_is_the_sequential_float_sum():
     w = np.ones((1, 4), np.float32)
     # ((0 + 1) + 1e8) - 1e8 + 1 = 1 in float; a pairwise sum gives 2, reversed gives 0
     assert oracle.mul_mat(w, x)[0, 0] == np.float32(1.0)
+    # the same rows as part of a multi-token product (the tiled loop nest)
+    x4 = np.repeat(x, 5, axis=0)
+    x4[1:, 0] = 2.0  # ((0 + 2) + 1e8) - 1e8 + 1 = 1 as well; reversed order gives 0
+    assert np.all(oracle.mul_mat(np.repeat(w, 3, axis=0), x4) == np.float32(1.0))
+
+
+@pytest.mark.parametrize("n_out,k,m", [(45, 1031, 37), (64, 1024, 4), (3, 7, 9), (96, 256, 64)])
+def test_mul_mat_tiles_equal_per_token_products(n_out, k, m):
+    """Products of four or more tokens run a tiled loop nest (32 outputs x 32
+    tokens, four tokens per SSE chain); each element must keep the one-token
+    path's bits (a sequential float sum), ragged tiles included."""
+    w = synth.normal(51 + k, (n_out, k))
+    x = synth.normal(52 + m, (m, k))
+    got = oracle.mul_mat(w, x)
+    for t in range(m):
+        assert np.array_equal(got[t].view(np.uint32), oracle.mul_mat(w, x[t]).view(np.uint32))
+    # and the one-token path is the sequential float32 sum
+    seq = np.zeros(n_out, np.float32)
+    for kk in range(k):
+        seq = seq + x[m - 1, kk] * w[:, kk]
+    assert np.array_equal(got[m - 1].view(np.uint32), seq.view(np.uint32))
 
 
 # ---------------------------------------------------------------------------
