@@ -19,7 +19,7 @@
  *   - No entry point allocates, frees or synchronises. Work is enqueued on
  *     `stream` and errors inside kernels never fault the device.
  *   - Return value: 0 on success; a negative errno (-EINVAL, -ENOTSUP,
- *     -EOVERFLOW) when arguments are rejected before any launch; a positive
+ *     -EOVERFLOW, -ENOSPC) when arguments are rejected before any launch; a positive
  *     hipError_t when a launch fails. The HIP backend maps negative codes to
  *     std::errc and positive ones to std::errc::io_error, as check_cuda does
  *     (reference include/cuda_util.hpp:7-16).
@@ -81,6 +81,29 @@ int ikv_attn_decode_f32(const float *q, float *k_cache, float *v_cache, const fl
                         const float *v_new, float *out, int n_head, int n_head_kv, int head_dim,
                         int64_t n_kv, float scale, void *workspace, size_t workspace_bytes,
                         void *stream);
+
+/* ---------------------------------------------------------------------
+ * ikv_attn_decode_f32 without a workspace argument, for callers that
+ * cannot allocate one: code under HIP graph capture, serving loops and
+ * harnesses that forbid allocation. It has no counterpart in the reference.
+ * It allocates nothing (no hipMalloc, no allocating library call): the
+ * split partials and arrival counters live in a device array of
+ * IKV_DECODE_NOALLOC_SCRATCH_BYTES that the library holds on each device it
+ * runs on until the process ends. Every call on one device shares that
+ * array, so calls that overlap on one device race (order them on one
+ * stream). Each call clears the counters it needs with a fill kernel on
+ * `stream` before the attention launch. Returns -ENOSPC when
+ * ikv_attn_decode_workspace_bytes() of the shape exceeds that size (every
+ * supported shape of up to 128 KV heads fits). Other arguments, results and
+ * return codes as for ikv_attn_decode_f32: the output and cache rows are
+ * bit-identical to its.
+ * ------------------------------------------------------------------- */
+#define IKV_DECODE_NOALLOC_SCRATCH_BYTES (2u << 20)
+
+int ikv_attn_decode_noalloc_f32(const float *q, float *k_cache, float *v_cache,
+                                const float *k_new, const float *v_new, float *out, int n_head,
+                                int n_head_kv, int head_dim, int64_t n_kv, float scale,
+                                void *stream);
 
 /* ---------------------------------------------------------------------
  * Decode with the step's qk-RMSNorm + RoPE folded into the same launch:

@@ -47,6 +47,7 @@
 #include "../../include/ikv.h"
 
 #include <climits>
+#include <mutex>
 
 namespace {
 
@@ -748,22 +749,36 @@ void launch(const float *q, float *kc, float *vc, const float *kn, const float *
                                 n_kv, p, scale_log2, none, flat, s);
 }
 
+// Zeroes the n arrival counters (kCounterStride ints apart) a launch starts
+// from: a kernel, not a memset, so that a caller may capture it in a graph.
+__global__ void clear_counters_kernel(int *counters, int n) {
+  const int i = static_cast<int>(blockIdx.x * blockDim.x + threadIdx.x);
+  if (i < n) counters[static_cast<size_t>(i) * kCounterStride] = 0;
+}
+
+// 0 when decode supports the shape, else the code it is rejected with.
+int shape_status(int n_head, int n_head_kv, int head_dim, int64_t n_kv) {
+  if (n_head <= 0 || n_head_kv <= 0 || n_head % n_head_kv != 0) return -EINVAL;
+  if (n_kv <= 0) return -EINVAL;
+  if (head_dim != D) return -ENOTSUP;
+  if (!supported_group(n_head / n_head_kv)) return -ENOTSUP;
+  if (n_kv > INT_MAX - 2 * TILE) return -EOVERFLOW;
+  return 0;
+}
+
 int decode_common(const float *q, float *k_cache, float *v_cache, const float *k_new,
                   const float *v_new, float *out, int n_head, int n_head_kv, int head_dim,
                   int64_t n_kv, float scale, void *workspace, size_t workspace_bytes,
-                  const Prologue *pro, const ikv_kv_pages *pages, void *stream) {
+                  const Prologue *pro, const ikv_kv_pages *pages, void *stream,
+                  bool clear_counters = false) {
   if (!q || !k_cache || !v_cache || !out) return -EINVAL;
   ikv::Pages pg;
   if (pages) {
     if (const int rc = ikv::pages_arg(pages, pg)) return rc;
   }
   if ((k_new == nullptr) != (v_new == nullptr)) return -EINVAL;
-  if (n_head <= 0 || n_head_kv <= 0 || n_head % n_head_kv != 0) return -EINVAL;
-  if (n_kv <= 0) return -EINVAL;
-  if (head_dim != D) return -ENOTSUP;
+  if (const int rc = shape_status(n_head, n_head_kv, head_dim, n_kv)) return rc;
   const int G = n_head / n_head_kv;
-  if (!supported_group(G)) return -ENOTSUP;
-  if (n_kv > INT_MAX - 2 * TILE) return -EOVERFLOW;
   if (!ikv::aligned16(q) || !ikv::aligned16(k_cache) || !ikv::aligned16(v_cache) ||
       !ikv::aligned16(out) || (k_new && (!ikv::aligned16(k_new) || !ikv::aligned16(v_new))))
     return -EINVAL;
@@ -782,6 +797,10 @@ int decode_common(const float *q, float *k_cache, float *v_cache, const float *k
   const float sl2 = scale * ikv::kLog2e;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int nk = static_cast<int>(n_kv);
+  if (clear_counters && p.n_splits > 1) {
+    clear_counters_kernel<<<(n_head_kv + 255) / 256, 256, 0, s>>>(counters, n_head_kv);
+    if (const int rc = ikv::launch_status()) return rc;
+  }
   switch (G) {
     case 1: launch<1>(q, k_cache, v_cache, k_new, v_new, out, counters, part_ml, part_o, n_head_kv, nk, p, sl2, pro, pages ? &pg : nullptr, s); break;
     case 2: launch<2>(q, k_cache, v_cache, k_new, v_new, out, counters, part_ml, part_o, n_head_kv, nk, p, sl2, pro, pages ? &pg : nullptr, s); break;
@@ -795,9 +814,7 @@ int decode_common(const float *q, float *k_cache, float *v_cache, const float *k
 
 extern "C" size_t ikv_attn_decode_workspace_bytes(int n_head, int n_head_kv, int head_dim,
                                                   int64_t n_kv) {
-  if (n_head <= 0 || n_head_kv <= 0 || n_head % n_head_kv != 0 || head_dim != D || n_kv <= 0)
-    return 0;
-  if (!supported_group(n_head / n_head_kv) || n_kv > INT_MAX - 2 * TILE) return 0;
+  if (shape_status(n_head, n_head_kv, head_dim, n_kv)) return 0;
   const Plan p = plan_for(n_head, n_head_kv, n_kv);
   return ws_layout(n_head, n_head_kv, p.n_splits).total;
 }
@@ -868,4 +885,57 @@ extern "C" int ikv_attn_decode_rope_paged_f32(
   return decode_rope_common(q_raw, k_raw, v_new, k_pool, v_pool, pages, out, n_head, n_head_kv,
                             head_dim, n_kv, scale, q_norm_w, k_norm_w, eps, pos, sin_tab, cos_tab,
                             n_ctx, status, workspace, workspace_bytes, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Decode without a caller workspace (for callers that cannot allocate: code
+// under stream capture, serving loops that forbid allocation). The split
+// partials and arrival counters live in a file-scope device array,
+// kNoAllocScratchBytes per device: every call on a device shares that
+// device's copy, so calls that overlap on one device race (order them on one
+// stream). Nothing is allocated or freed: the array's address on each device
+// is looked up on the first call there (hipGetSymbolAddress) and kept.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr size_t kNoAllocScratchBytes = IKV_DECODE_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on the current device (host code must not
+// use the symbol itself as a pointer).
+int scratch_ptr(void **out) {
+  int dev = 0;
+  if (const hipError_t e = hipGetDevice(&dev); e != hipSuccess) return static_cast<int>(e);
+  if (dev < 0 || dev >= kMaxDevices) return -ENODEV;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    if (const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)); e != hipSuccess)
+      return static_cast<int>(e);
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
+}  // namespace
+
+extern "C" int ikv_attn_decode_noalloc_f32(const float *q, float *k_cache, float *v_cache,
+                                           const float *k_new, const float *v_new, float *out,
+                                           int n_head, int n_head_kv, int head_dim, int64_t n_kv,
+                                           float scale, void *stream) {
+  if (const int rc = shape_status(n_head, n_head_kv, head_dim, n_kv)) return rc;
+  if (ikv_attn_decode_workspace_bytes(n_head, n_head_kv, head_dim, n_kv) > kNoAllocScratchBytes)
+    return -ENOSPC;
+  void *ws = nullptr;
+  if (const int rc = scratch_ptr(&ws)) return rc;
+  // The counters are cleared on every call: a call of another shape may have
+  // left split partials where this shape's counters sit.
+  return decode_common(q, k_cache, v_cache, k_new, v_new, out, n_head, n_head_kv, head_dim, n_kv,
+                       scale, ws, kNoAllocScratchBytes, nullptr, nullptr, stream,
+                       /*clear_counters=*/true);
 }

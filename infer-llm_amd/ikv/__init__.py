@@ -47,6 +47,11 @@ SIGNATURES = {
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
          _c_int, _c_int, _c_int, _c_int64, _c_float, _c_void_p, _c_size_t, _c_void_p],
     ),
+    "ikv_attn_decode_noalloc_f32": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+         _c_int, _c_int, _c_int, _c_int64, _c_float, _c_void_p],
+    ),
     "ikv_attn_decode_rope_f32": (
         _c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int,
@@ -256,6 +261,38 @@ def attn_decode(q, k_cache, v_cache, n_kv: int, *, k_new=None, v_new=None, out=N
         _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(k_new), _ptr(v_new), _ptr(out),
         n_head, n_head_kv, D, n_kv, scale, _ptr(workspace), workspace.numel() * 4, _stream(stream))
     _check("ikv_attn_decode_f32", rc)
+    return out
+
+
+# IKV_DECODE_NOALLOC_SCRATCH_BYTES (include/ikv.h): the device array that
+# attn_decode_noalloc keeps its split partials and counters in
+NOALLOC_SCRATCH_BYTES = 2 << 20
+
+
+def attn_decode_noalloc(q, k_cache, v_cache, n_kv: int, *, out, k_new=None, v_new=None,
+                        scale: float = 0.0, stream=None):
+    """attn_decode without a workspace: nothing is allocated (out is the
+    caller's). The library's per-device scratch array holds the split
+    partials, so calls on one device must be ordered on one stream."""
+    for name, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache), ("out", out)):
+        _need_f32_dev(name, t)
+    n_head, D = q.shape[-2], q.shape[-1]
+    n_head_kv = k_cache.shape[-2]
+    if k_cache.shape[0] < n_kv or v_cache.shape[0] < n_kv:
+        raise ValueError("cache shorter than n_kv")
+    if (k_new is None) != (v_new is None):
+        raise ValueError("k_new and v_new go together")
+    if k_new is not None:
+        _need_f32_dev("k_new", k_new)
+        _need_f32_dev("v_new", v_new)
+        if k_new.numel() != n_head_kv * D or v_new.numel() != n_head_kv * D:
+            raise ValueError("k_new/v_new must hold one token row")
+    if out.numel() != n_head * D:
+        raise ValueError("out must hold n_head rows")
+    rc = load().ikv_attn_decode_noalloc_f32(
+        _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(k_new), _ptr(v_new), _ptr(out),
+        n_head, n_head_kv, D, n_kv, scale, _stream(stream))
+    _check("ikv_attn_decode_noalloc_f32", rc)
     return out
 
 

@@ -3,6 +3,7 @@ include/ikv.h declares, and rejects bad arguments before touching a device.
 No kernel is launched here."""
 import ctypes
 import errno
+import re
 import subprocess
 
 import numpy as np
@@ -60,6 +61,31 @@ def test_decode_rejects_bad_arguments_without_launching():
     assert call(n_kv=4097) == -errno.EINVAL            # split-K needs a workspace
     need = ikv.decode_workspace_bytes(ok["n_head"], ok["n_head_kv"], 128, 4097)
     assert call(n_kv=4097, ws=P, wsb=need - 4) == -errno.EINVAL
+
+
+def test_noalloc_decode_rejects_shapes_before_touching_a_device():
+    P = 64
+    m = re.search(r"#define IKV_DECODE_NOALLOC_SCRATCH_BYTES \((\d+)u << (\d+)\)",
+                  (ikv.HEADER_DIR / "ikv.h").read_text())
+    assert m and int(m[1]) << int(m[2]) == ikv.NOALLOC_SCRATCH_BYTES
+
+    def call(n_head, n_head_kv, head_dim=128, n_kv=4097):
+        return _rc("ikv_attn_decode_noalloc_f32", P, P, P, None, None, P, n_head, n_head_kv,
+                   head_dim, n_kv, 0.0, None)
+
+    # 4096 query heads over 512 KV heads: 2.26 MB of partials, more than the array
+    assert ikv.decode_workspace_bytes(4096, 512, 128, 4097) > ikv.NOALLOC_SCRATCH_BYTES
+    assert call(4096, 512) == -errno.ENOSPC
+    assert call(12, 8) == -errno.EINVAL
+    assert call(16, 8, n_kv=0) == -errno.EINVAL
+    assert call(16, 8, head_dim=64) == -errno.ENOTSUP
+    assert call(24, 8) == -errno.ENOTSUP              # group of 3
+    assert call(16, 8, n_kv=2**31) == -errno.EOVERFLOW
+    # every supported group size of up to 128 KV heads fits, at any context
+    for hkv in (1, 8, 64, 128):
+        for G in (1, 2, 4, 8):
+            for n_kv in (129, 4097, 40960, 1 << 20):
+                assert ikv.decode_workspace_bytes(hkv * G, hkv, 128, n_kv) <= ikv.NOALLOC_SCRATCH_BYTES
 
 
 def test_prefill_and_rows_reject_bad_arguments():
