@@ -23,6 +23,9 @@
  *     hipError_t when a launch fails. The HIP backend maps negative codes to
  *     std::errc and positive ones to std::errc::io_error, as check_cuda does
  *     (reference include/cuda_util.hpp:7-16).
+ *   - Bad data inside a launch (a position, block entry or token id out of
+ *     range) never faults: the kernel ORs one IKV_STATUS_* bit into the
+ *     caller's device status word, when one is given, and carries on.
  */
 #ifndef IKV_H
 #define IKV_H
@@ -33,6 +36,11 @@
 #ifdef __cplusplus
 extern "C" {
 #endif
+
+/* Bits of the device status word (see the conventions above). */
+#define IKV_STATUS_POSITION 1 /* a RoPE position outside [0, n_ctx) */
+#define IKV_STATUS_BLOCK 2    /* a paged block-table entry outside the pool */
+#define IKV_STATUS_TOKEN 4    /* a get_rows id outside the table */
 
 /* Version string of the library, e.g. "ikv 0.1 gfx950". */
 const char *ikv_version(void);
@@ -116,7 +124,7 @@ int ikv_attn_decode_noalloc_f32(const float *q, float *k_cache, float *v_cache,
  * q_raw [n_head][head_dim], k_raw / v_new [n_head_kv][head_dim]; norm
  * weights [head_dim]; pos: device int32; sin/cos tables [n_ctx][head_dim/2]
  * as for ikv_rope_neox_f32. A position outside [0, n_ctx) does not fault:
- * q and k become zero rows and *status (device int, if non-NULL) is set to 1.
+ * q and k become zero rows and IKV_STATUS_POSITION is raised in *status.
  * Workspace and other arguments as for ikv_attn_decode_f32.
  * ------------------------------------------------------------------- */
 int ikv_attn_decode_rope_f32(const float *q_raw, const float *k_raw, const float *v_new,
@@ -151,8 +159,9 @@ int ikv_attn_prefill_f32(const float *q, const float *k, const float *v, float *
  * block_tokens must be a positive multiple of 64 (a tile of the kernels never
  * straddles two blocks). block_table is device memory with an entry for every
  * block the call touches; an entry outside [0, n_pool_blocks) does not fault:
- * block 0 is read (or written) instead and *status (device int, if non-NULL)
- * is set to 1.
+ * reads take block 0's rows instead, writes to that block are dropped (no
+ * other sequence's rows are touched), and IKV_STATUS_BLOCK is raised in
+ * *status (device int, if non-NULL).
  * ------------------------------------------------------------------- */
 typedef struct ikv_kv_pages {
     const int32_t *block_table;
@@ -222,7 +231,8 @@ int ikv_rope_sincos_table_f32(const float *theta_host, size_t count, float *sin_
  * c = cos_tab[p][j], s = sin_tab[p][j]  (src/backends/cpu_backend.cpp:
  * 443-523). Replaces CUDA_F32::compute_rope (src/kernels/cuda/kernel_f32.cu:
  * 242-301). A position outside [0, n_ctx) does not fault: its rows are
- * written as zeros and *status (if non-NULL, device int) is set to 1.
+ * written as zeros and IKV_STATUS_POSITION is raised in *status (device int,
+ * if non-NULL).
  * x may equal out.
  * ------------------------------------------------------------------- */
 int ikv_rope_neox_f32(const float *x, float *out, const int32_t *pos, int64_t n_tokens,

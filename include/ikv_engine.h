@@ -29,6 +29,10 @@ extern "C" {
 typedef struct ikv_qwen3_config {
     uint32_t n_layer, n_embd, n_head, n_head_kv, head_dim, n_ff, n_vocab, n_ctx_train;
     float rope_theta, rms_norm_eps;
+    /* 0: the logits use the token embedding (tied, as when a GGUF file has
+     * no "output.weight"); 1: a separate "output.weight" [n_vocab][n_embd]
+     * projects them (src/model.cpp:203-210). */
+    uint32_t untied_output;
 } ikv_qwen3_config;
 
 /* TTFT and TPOT as benchmarks/cpu/bench.cpp:239-281 defines them:
@@ -72,7 +76,8 @@ int ikv_qwen3_kv_stats(const ikv_qwen3 *m, ikv_qwen3_kv_counters *out);
 
 /* Weight tensors by GGUF name (ModelBase::load_weight, src/model.cpp:
  * 164-311): "token_embd.weight", "blk.<i>.attn_q.weight", ...,
- * "output_norm.weight"; the output projection is the tied token embedding.
+ * "output_norm.weight", then "output.weight" when the config is untied
+ * (otherwise the output projection is the tied token embedding).
  * Index order is the synthetic initialiser's draw order. */
 int ikv_qwen3_tensor_count(const ikv_qwen3 *m);
 const char *ikv_qwen3_tensor_name(const ikv_qwen3 *m, int index);

@@ -61,7 +61,8 @@ int ikv_gemv_swiglu_f32(const float *w_gate, const float *w_up, const float *x, 
  * get_rows: out[i][:] = table[ids[i]][:] for i < n_ids, rows of row_len
  * floats (CPUBackend::compute_get_rows, src/backends/cpu_backend.cpp:
  * 259-332; the token embedding). An id outside [0, n_rows) does not fault:
- * its output row is zeros and *status (device int, if non-NULL) is set to 1.
+ * its output row is zeros and IKV_STATUS_TOKEN (include/ikv.h) is raised in
+ * *status (device int, if non-NULL).
  * ------------------------------------------------------------------- */
 int ikv_get_rows_f32(const float *table, const int32_t *ids, float *out, int64_t n_ids,
                      int64_t row_len, int64_t n_rows, int *status, void *stream);

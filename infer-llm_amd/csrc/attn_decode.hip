@@ -397,7 +397,7 @@ __device__ __forceinline__ void qk_prologue(const Prologue &pro, ProStage<G> &st
     s[r][j] = o0;
     s[r][j + hd] = o1;
   }
-  if (!ok && tid == 0 && pro.status) *pro.status = 1;
+  if (!ok && tid == 0) ikv::raise_status(pro.status, IKV_STATUS_POSITION);
   __syncthreads();
 }
 
@@ -638,7 +638,9 @@ __global__ __launch_bounds__(WG, waves_per_simd(G)) void decode_kernel(
   // The append: the split holding the new token writes its K (rotated when
   // RoPE is folded in) and V rows into the caches, 16 bytes per lane of the
   // first half-wave.
-  if (new_row >= t_begin && new_row < t_end && wave == 0 && half == 0) {
+  bool append_here = new_row >= t_begin && new_row < t_end && wave == 0 && half == 0;
+  if constexpr (PAGED) append_here = append_here && ikv::page_ok(pages, new_row);
+  if (append_here) {
     const size_t off = static_cast<size_t>(new_row + shift_of(new_row)) * tok_stride + head_off;
     float4 kw;
     if constexpr (PRO)

@@ -100,6 +100,12 @@ __device__ __forceinline__ float rms_scale_strided(const float4 *row, int dim, f
   return static_cast<float>(1.0 / sqrt(s / static_cast<double>(dim) + static_cast<double>(eps)));
 }
 
+// ORs an IKV_STATUS_* bit into a caller's device status word (a vector
+// atomic; several kernels and error kinds may share one word).
+__device__ __forceinline__ void raise_status(int *status, int bit) {
+  if (status) atomicOr(status, bit);
+}
+
 // A paged KV cache as the kernels see it: logical token t lives in pool row
 // table[t / bt] * bt + t % bt (bt a multiple of 64).
 struct Pages {
@@ -111,16 +117,22 @@ struct Pages {
 
 // Offset that takes logical token t to its pool row (t + shift), shared by
 // every token of t's block. A table entry outside [0, n_blocks) maps to block
-// 0 and raises *status. t is uniform across the wave, so the entry is one
-// scalar load.
+// 0 (in bounds, for reads) and raises IKV_STATUS_BLOCK. t is uniform across
+// the wave, so the entry is one scalar load.
 __device__ __forceinline__ int64_t page_shift(const Pages &pg, int t) {
   const int b = t / pg.bt;
   int blk = pg.table[b];
   if (static_cast<unsigned>(blk) >= static_cast<unsigned>(pg.n_blocks)) {
-    if (pg.status) *pg.status = 1;
+    raise_status(pg.status, IKV_STATUS_BLOCK);
     blk = 0;
   }
   return static_cast<int64_t>(blk - b) * pg.bt;
+}
+
+// Whether logical token t's table entry names a pool block: writes to a
+// token whose entry does not are dropped.
+__device__ __forceinline__ bool page_ok(const Pages &pg, int64_t t) {
+  return static_cast<unsigned>(pg.table[t / pg.bt]) < static_cast<unsigned>(pg.n_blocks);
 }
 
 // Host check of a paged-cache descriptor: a table, blocks of a positive

@@ -40,10 +40,10 @@ __global__ __launch_bounds__(256) void scatter16_kernel(uint4 *__restrict__ pool
     const size_t c = u - i * per_row;
     const int64_t t = first + static_cast<int64_t>(i);
     const int64_t b = t / pg.bt;
-    int blk = pg.table[b];
+    const int blk = pg.table[b];
     if (static_cast<unsigned>(blk) >= static_cast<unsigned>(pg.n_blocks)) {
-      if (pg.status) *pg.status = 1;
-      blk = 0;
+      ikv::raise_status(pg.status, IKV_STATUS_BLOCK);  // dropped: no block to write
+      continue;
     }
     const size_t row = static_cast<size_t>(blk) * pg.bt + static_cast<size_t>(t - b * pg.bt);
     pool[row * per_row + c] = src[u];

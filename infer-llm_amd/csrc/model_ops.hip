@@ -31,7 +31,7 @@ __global__ __launch_bounds__(kThreads) void get_rows_kernel(const float *__restr
   const int32_t id = ids[i];
   float *dst = out + i * row_len;
   const bool ok = id >= 0 && id < n_rows;
-  if (!ok && threadIdx.x == 0 && status) atomicOr(status, 1);
+  if (!ok && threadIdx.x == 0) ikv::raise_status(status, IKV_STATUS_TOKEN);
   const float *src = table + static_cast<int64_t>(ok ? id : 0) * row_len;
   if (vec) {
     for (int64_t c = threadIdx.x; c < row_len / 4; c += kThreads) {

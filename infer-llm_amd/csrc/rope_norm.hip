@@ -235,7 +235,7 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(const float *__restric
     }
     float o0 = 0.0f, o1 = 0.0f;
     if (p < 0 || p >= n_ctx) {
-      if (status) *status = 1;
+      ikv::raise_status(status, IKV_STATUS_POSITION);
     } else {
       const float a = x0 * c;
       const float b = x1 * s;

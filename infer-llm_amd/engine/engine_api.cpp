@@ -57,6 +57,8 @@ int create(const ikv_qwen3_config *cfg, int device, int64_t max_ctx, const KVOpt
   hp.n_ctx_train = cfg->n_ctx_train;
   hp.rope_theta = cfg->rope_theta;
   hp.rms_norm_eps = cfg->rms_norm_eps;
+  if (cfg->untied_output > 1) return -EINVAL;
+  hp.untied_output = cfg->untied_output != 0;
   m->model = std::make_unique<Qwen3Model>(hp);
   if (auto r = m->model->alloc_weights(m->backend.get()); !r) return to_errno(r.error());
   m->runner = std::make_unique<Qwen3Runner>(*m->model, *hip(m.get()), size_t(max_ctx), kv);

@@ -249,7 +249,13 @@ infer::expected<void, std::error_code> HIPBackend::synchronize() {
   }
   if (status != 0) {
     (void)hipMemset(_status, 0, sizeof(int));
-    std::fprintf(stderr, "[hip] RoPE position outside the angle table\n");
+    if (status & IKV_STATUS_POSITION)
+      std::fprintf(stderr, "[hip] RoPE position outside the angle table\n");
+    if (status & IKV_STATUS_BLOCK)
+      std::fprintf(stderr, "[hip] paged block-table entry outside the pool (its rows were "
+                           "read from block 0 and its writes dropped)\n");
+    if (status & IKV_STATUS_TOKEN)
+      std::fprintf(stderr, "[hip] token id outside the embedding table\n");
     return infer::fail(std::errc::invalid_argument);
   }
   return {};
@@ -285,11 +291,17 @@ infer::expected<void, std::error_code> HIPBackend::reserve_decode_workspace(int 
                                                                            int head_dim,
                                                                            int64_t max_kv) {
   if (auto r = set_device(); !r) return r;
+  return ensure_workspace(decode_workspace_reservation(n_head, n_head_kv, head_dim, max_kv));
+}
+
+size_t HIPBackend::decode_workspace_reservation(int n_head, int n_head_kv, int head_dim,
+                                                int64_t max_kv) {
+  // The split count is not monotone in n_kv (it peaks where a split's tile
+  // count steps down), so every context is asked; a few ns each, once.
   size_t need = 0;
-  for (int64_t n = 1; n <= max_kv; n = n < 64 ? n + 1 : n * 2)  // workspace grows with n_kv
+  for (int64_t n = 1; n <= max_kv; ++n)
     need = std::max(need, ikv_attn_decode_workspace_bytes(n_head, n_head_kv, head_dim, n));
-  need = std::max(need, ikv_attn_decode_workspace_bytes(n_head, n_head_kv, head_dim, max_kv));
-  return ensure_workspace(need);
+  return need;
 }
 
 infer::expected<const HIPBackend::RopeTables *, std::error_code> HIPBackend::rope_tables(

@@ -48,8 +48,9 @@ class HIPBackend : public Backend {
   infer::expected<bool, std::error_code> copy_tensor_high(const Tensor *src,
                                                           Tensor *dst) const override;
   infer::expected<void, std::error_code> compute(Graph &sub_graph) override;
-  // Waits for the stream, then reports RoPE position errors recorded by the
-  // kernels since the last call (invalid_argument).
+  // Waits for the stream, then reports the data errors the kernels recorded
+  // since the last call (IKV_STATUS_* bits: RoPE positions, paged block
+  // entries, token ids), each by name, as invalid_argument.
   infer::expected<void, std::error_code> synchronize() override;
   bool accepts_host_src(const Tensor &node, int src_index) const override;
 
@@ -58,6 +59,10 @@ class HIPBackend : public Backend {
   // allocation happens inside compute() (e.g. under graph capture).
   infer::expected<void, std::error_code> reserve_decode_workspace(int n_head, int n_head_kv,
                                                                   int head_dim, int64_t max_kv);
+  // The bytes reserve_decode_workspace allocates: the largest decode
+  // workspace of any context of 1..max_kv keys (host arithmetic only).
+  static size_t decode_workspace_reservation(int n_head, int n_head_kv, int head_dim,
+                                             int64_t max_kv);
   void set_fusion(bool on) { _fusion = on; }
   struct Stats {
     int launches = 0;

@@ -39,6 +39,8 @@ Qwen3Model::Qwen3Model(const Qwen3Hparams &hp) : _hp(hp) {
     L.ffn_down = make(p + "ffn_down.weight", {F, E});
   }
   _output_norm = make("output_norm.weight", {E});
+  // last, so that a tied model's synthetic draw order does not depend on it
+  _output = hp.untied_output ? make("output.weight", {E, hp.n_vocab}) : _token_embd;
 }
 
 Qwen3Model::~Qwen3Model() {
@@ -162,7 +164,7 @@ infer::expected<Graph, std::error_code> Qwen3Model::build_graph(GraphContext &ct
   // prefill).
   Tensor *last = n_tokens > 1 ? OpFactory::view_rows(g, inpL, n_tokens - 1, 1, "result_last") : inpL;
   Tensor *final_norm = OpFactory::rms_norm(g, last, _output_norm, eps, "result_norm");
-  Tensor *logits = OpFactory::mul_mat(g, _token_embd, final_norm, "logits");  // tied output
+  Tensor *logits = OpFactory::mul_mat(g, _output, final_norm, "logits");
   g.mark_output(logits);
   return g;
 }

@@ -48,6 +48,9 @@ struct Qwen3Hparams {
   uint32_t n_ctx_train = 40960;
   float rope_theta = 1e6f;
   float rms_norm_eps = 1e-6f;
+  // A separate output projection "output.weight"; false ties the logits to
+  // the token embedding (src/model.cpp:203-210).
+  bool untied_output = false;
 };
 
 struct Qwen3LayerWeights {
@@ -90,6 +93,7 @@ class Qwen3Model {
   std::vector<std::unique_ptr<Tensor>> _tensors;
   std::unordered_map<std::string, Tensor *> _map;
   Tensor *_token_embd = nullptr, *_output_norm = nullptr;
+  Tensor *_output = nullptr;  // the token embedding when tied
   std::vector<Qwen3LayerWeights> _layers;
 };
 

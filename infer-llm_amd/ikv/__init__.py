@@ -264,6 +264,9 @@ def attn_decode(q, k_cache, v_cache, n_kv: int, *, k_new=None, v_new=None, out=N
     return out
 
 
+# IKV_STATUS_* bits (include/ikv.h) a kernel raises in a device status word
+STATUS_POSITION, STATUS_BLOCK, STATUS_TOKEN = 1, 2, 4
+
 # IKV_DECODE_NOALLOC_SCRATCH_BYTES (include/ikv.h): the device array that
 # attn_decode_noalloc keeps its split partials and counters in
 NOALLOC_SCRATCH_BYTES = 2 << 20

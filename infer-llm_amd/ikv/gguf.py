@@ -8,9 +8,11 @@ counts, metadata key/value pairs, tensor infos (name, dims innermost first,
 type, offset), padding to ``general.alignment`` (32 when absent), tensor data.
 The keys written are those ModelBase::load_hparams reads
 (src/model.cpp:60-163) and the tensor names those ModelBase::load_weight
-reads (src/model.cpp:164-311); ``output.weight`` is omitted, so the logits
-use the tied token embedding. A file written here therefore runs on the
-reference's CPU backend as well, e.g. for its config-0 benchmark.
+reads (src/model.cpp:164-311). ``output.weight`` is written only for a
+config with ``untied_output``; without it the logits use the tied token
+embedding, and a file that has one is read as untied (src/model.cpp:203-210).
+A file written here therefore runs on the reference's CPU backend as well,
+e.g. for its config-0 benchmark.
 
     python -m ikv.gguf write --config 0 --out qwen3-0.6b-synthetic.gguf
 
@@ -233,7 +235,8 @@ def qwen3_config(g: GGUFFile):
         n_ff=int(m[p + "feed_forward_length"]), n_vocab=len(m["tokenizer.ggml.tokens"]),
         n_ctx_train=int(m[p + "context_length"]),
         rope_theta=float(m.get(p + "rope.freq_base", 10000.0)),
-        rms_norm_eps=float(m.get(p + "attention.layer_norm_rms_epsilon", 1e-5)))
+        rms_norm_eps=float(m.get(p + "attention.layer_norm_rms_epsilon", 1e-5)),
+        untied_output=int("output.weight" in g.tensors))
 
 
 def load_qwen3(path, max_ctx: int, device: int = 0, **engine_kw):

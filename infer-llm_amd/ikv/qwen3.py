@@ -27,6 +27,7 @@ class Qwen3Config:
     n_ctx_train: int = 40960
     rope_theta: float = 1e6
     rms_norm_eps: float = 1e-6
+    untied_output: int = 0  # 1: a separate output.weight projects the logits
 
 
 QWEN3_0_6B = Qwen3Config()
@@ -36,7 +37,8 @@ QWEN3_8B = Qwen3Config(n_layer=36, n_embd=4096, n_head=32, n_head_kv=8, n_ff=122
 class _Config(ctypes.Structure):
     _fields_ = [(n, ctypes.c_uint32) for n in ("n_layer", "n_embd", "n_head", "n_head_kv",
                                                "head_dim", "n_ff", "n_vocab", "n_ctx_train")] + \
-               [("rope_theta", ctypes.c_float), ("rms_norm_eps", ctypes.c_float)]
+               [("rope_theta", ctypes.c_float), ("rms_norm_eps", ctypes.c_float),
+                ("untied_output", ctypes.c_uint32)]
 
 
 class Timing(ctypes.Structure):
@@ -103,6 +105,8 @@ def tensor_layout(cfg: Qwen3Config):
                 (p + "ffn_gate.weight", (F, E)), (p + "ffn_up.weight", (F, E)),
                 (p + "ffn_down.weight", (E, F))]
     out.append(("output_norm.weight", (E,)))
+    if cfg.untied_output:
+        out.append(("output.weight", (cfg.n_vocab, E)))
     return out
 
 

@@ -244,9 +244,12 @@ class Qwen3Oracle:
         tokens = np.ascontiguousarray(tokens, dtype=np.int32)
         logits = np.zeros((tokens.size, self.cfg.n_vocab), np.float32)
         emb = self.w["token_embd.weight"]
+        # output.weight when the model has one, else the tied embedding
+        # (src/model.cpp:203-210)
+        out_w = self.w.get("output.weight", emb)
         rc = _lib_model().oracle_qwen3_step(
             ctypes.byref(self.hp), self.layers, emb.ctypes.data,
-            self.w["output_norm.weight"].ctypes.data, emb.ctypes.data, self.theta.ctypes.data,
+            self.w["output_norm.weight"].ctypes.data, out_w.ctypes.data, self.theta.ctypes.data,
             tokens.ctypes.data, tokens.size, n_past, self.kp, self.vp, logits.ctypes.data,
             1 if last_row_only else 0)
         if rc != 0:

@@ -13,12 +13,14 @@
 // Prints one line per check; the exit status is the number of failures.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
 #include <memory>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "../../infer-llm_amd/engine/backend.hpp"
@@ -28,6 +30,7 @@
 #include "../../infer-llm_amd/engine/kvcache/offload_storage.hpp"
 #include "../../infer-llm_amd/engine/op_factory.hpp"
 #include "../../infer-llm_amd/engine/scheduler.hpp"
+#include "../../include/ikv.h"
 #include "../../oracle/oracle.h"
 
 static int g_fail = 0;
@@ -106,6 +109,30 @@ static void offload_cpu_tests();
 static void offload_gpu_tests(HIPBackend *hip);
 
 static void cpu_tests() {
+  {
+    // the decode workspace reserved up front covers every context: no
+    // allocation inside a decode step (host arithmetic, no device)
+    bool ok = true;
+    for (auto [hq, hkv] : {std::pair{16, 8}, {32, 8}, {64, 8}, {8, 8}, {16, 2}}) {
+      for (int64_t cap : {64, 130, 2560, 4352, 9000}) {
+        const size_t r = HIPBackend::decode_workspace_reservation(hq, hkv, 128, cap);
+        size_t most = 0;
+        for (int64_t n = 1; n <= cap; ++n) {
+          const size_t w = ikv_attn_decode_workspace_bytes(hq, hkv, 128, n);
+          ok = ok && w <= r;
+          most = std::max(most, w);
+        }
+        ok = ok && most == r;
+      }
+    }
+    // the Qwen3-0.6B shape peaks at 2049..2112 keys (33 splits), which a
+    // powers-of-two sampling misses
+    const size_t at2048 = ikv_attn_decode_workspace_bytes(16, 8, 128, 2048);
+    const size_t at2080 = ikv_attn_decode_workspace_bytes(16, 8, 128, 2080);
+    ok = ok && at2080 > at2048 &&
+         HIPBackend::decode_workspace_reservation(16, 8, 128, 2560) >= at2080;
+    CHECK(ok, "decode workspace reservation covers every context up to capacity");
+  }
   {
     infer::expected<int, std::error_code> a = 5;
     infer::expected<int, std::error_code> b = infer::fail(std::errc::invalid_argument);

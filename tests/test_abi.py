@@ -68,6 +68,9 @@ def test_noalloc_decode_rejects_shapes_before_touching_a_device():
     m = re.search(r"#define IKV_DECODE_NOALLOC_SCRATCH_BYTES \((\d+)u << (\d+)\)",
                   (ikv.HEADER_DIR / "ikv.h").read_text())
     assert m and int(m[1]) << int(m[2]) == ikv.NOALLOC_SCRATCH_BYTES
+    for name in ("POSITION", "BLOCK", "TOKEN"):
+        m = re.search(rf"#define IKV_STATUS_{name} (\d+)", (ikv.HEADER_DIR / "ikv.h").read_text())
+        assert m and int(m[1]) == getattr(ikv, f"STATUS_{name}")
 
     def call(n_head, n_head_kv, head_dim=128, n_kv=4097):
         return _rc("ikv_attn_decode_noalloc_f32", P, P, P, None, None, P, n_head, n_head_kv,

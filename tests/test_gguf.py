@@ -68,6 +68,28 @@ def test_round_trip_is_bit_exact(tiny_file):
         assert np.array_equal(got.view(np.uint32), arr.view(np.uint32)), name
 
 
+def test_untied_output_round_trips(tmp_path):
+    # a model with its own output projection (src/model.cpp:203-210): the
+    # writer emits output.weight, the reader sees it and marks the config
+    # untied, and the projection is drawn after every tied-model tensor, so
+    # the shared tensors equal the tied model's bit for bit
+    untied = dataclasses.replace(TINY, untied_output=1)
+    path = tmp_path / "untied.gguf"
+    gguf.write_qwen3_synthetic(path, untied, seed=1234, threads=2)
+    g = gguf.GGUFFile(path)
+    assert gguf.qwen3_config(g).untied_output == 1
+    assert g.tensors["output.weight"].shape == (TINY.n_vocab, TINY.n_embd)
+    assert [n for n, _ in qwen3.tensor_layout(untied)][-1] == "output.weight"
+    want = qwen3.synthetic_weights(untied, 1234, threads=2)
+    tied = qwen3.synthetic_weights(TINY, 1234, threads=2)
+    assert set(want) == set(tied) | {"output.weight"}
+    for name, arr in want.items():
+        assert np.array_equal(g.tensor(name).view(np.uint32), arr.view(np.uint32)), name
+        if name in tied:
+            assert np.array_equal(arr, tied[name]), name
+    assert not np.array_equal(want["output.weight"], want["token_embd.weight"])
+
+
 def test_malformed_files_are_rejected(tmp_path, tiny_file):
     raw = bytearray(tiny_file.read_bytes())
     bad = tmp_path / "bad_magic.gguf"

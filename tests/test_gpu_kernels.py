@@ -323,7 +323,7 @@ def test_rope_bad_position_sets_status_without_fault(dev):
     status = torch.zeros(1, dtype=torch.int32, device=dev)
     out = ikv.rope_neox(x, pos, s, c, status=status)
     torch.cuda.synchronize()
-    assert int(status.item()) == 1
+    assert int(status.item()) == ikv.STATUS_POSITION
     o = out.cpu().numpy()
     assert np.all(o[1] == 0) and np.all(o[0] != 0)
 

@@ -116,7 +116,7 @@ def test_get_rows_bit_exact_and_bad_id_zeroed(dev):
     bad = np.array([3, 1000, -1], np.int32)
     got = host(ikv.get_rows(dev_t(t, dev), dev_t(bad, dev), status=status))
     assert np.array_equal(got[0], t[3]) and not got[1:].any()
-    assert int(host(status)[0]) == 1
+    assert int(host(status)[0]) == ikv.STATUS_TOKEN
 
 
 @pytest.mark.parametrize("n", [1, 1000, 3072, 4097])
@@ -240,6 +240,26 @@ def test_other_group_sizes_greedy_tokens_match_oracle(dev, oracle_pool, n_head, 
     assert eng.generate(prompt, n_gen)[0] == ref
     eng.set_fusion(False)
     assert eng.generate(prompt, n_gen)[0] == ref
+    eng.close()
+
+
+def test_untied_gguf_model_uses_its_output_projection(dev, oracle_pool, tmp_path):
+    # a GGUF file with output.weight (src/model.cpp:203-210) loads untied and
+    # its logits come from that projection: the tokens equal the oracle's
+    # with output.weight, and differ from those of the tied embedding
+    from ikv import gguf
+    cfg = qwen3.Qwen3Config(n_layer=2, n_vocab=4096, n_ctx_train=4096, untied_output=1)
+    path = tmp_path / "untied.gguf"
+    gguf.write_qwen3_synthetic(path, cfg, seed=synth.config_seed(0, 50), std=0.05, threads=8)
+    w = qwen3.synthetic_weights(cfg, synth.config_seed(0, 50), std=0.05)
+    prompt = synth.uniform_ints(synth.config_seed(0, 51), 24, cfg.n_vocab)
+    ref = oracle.Qwen3Oracle(cfg, w, 64).generate(prompt, 32)
+    tied = {k: v for k, v in w.items() if k != "output.weight"}
+    ref_tied = oracle.Qwen3Oracle(cfg, tied, 64).generate(prompt, 32)
+    assert ref != ref_tied
+    eng = gguf.load_qwen3(path, 64)
+    assert eng.cfg.untied_output == 1 and eng.tensor_names()[-1] == "output.weight"
+    assert eng.generate(prompt, 32)[0] == ref
     eng.close()
 
 
@@ -377,7 +397,7 @@ def test_decode_with_qk_rope_bad_position_is_flagged(dev):
     ikv.attn_decode_rope(torch.ones((16, D), device=dev), torch.ones((8, D), device=dev),
                          torch.ones((8, D), device=dev), kc, vc, 11, ones, ones, 1e-6, pos,
                          dev_t(s, dev), dev_t(c, dev), status=status)
-    assert int(host(status)[0]) == 1
+    assert int(host(status)[0]) == ikv.STATUS_POSITION
     assert not host(kc)[10].any()       # the appended key row is zeros, not garbage
 
 

@@ -174,15 +174,34 @@ def test_bad_block_entry_is_flagged_not_faulted(dev):
     status = torch.zeros(1, dtype=torch.int32, device=dev)
     ikv.attn_decode_paged(q, kp, vp, table, bt, n_kv, status=status)
     torch.cuda.synchronize()
-    assert int(status.cpu()[0]) == 1
+    assert int(status.cpu()[0]) == ikv.STATUS_BLOCK
     status.zero_()
     ikv.attn_prefill_paged(rand(g, (n_kv, 16, D)), kp, vp, table, bt, 0, status=status)
     torch.cuda.synchronize()
-    assert int(status.cpu()[0]) == 1
+    assert int(status.cpu()[0]) == ikv.STATUS_BLOCK
+    # writes through a bad entry are dropped: block 0 (and every other pool
+    # row) keeps its contents, the rows of good entries land
     status.zero_()
-    ikv.append_paged(kp, rand(g, (n_kv, 8, D)), table, bt, 0, status=status)
+    before = kp.clone()
+    rows = rand(g, (n_kv, 8, D))
+    ikv.append_paged(kp, rows, table, bt, 0, status=status)
     torch.cuda.synchronize()
-    assert int(status.cpu()[0]) == 1
+    assert int(status.cpu()[0]) == ikv.STATUS_BLOCK
+    want = before.clone()
+    for t in range(n_kv):
+        blk = int(table[t // bt])
+        if blk < 6:
+            want[blk * bt + t % bt] = rows[t]
+    assert torch.equal(kp, want)
+    # the fused decode append through a bad entry is dropped too
+    status.zero_()
+    before_k, before_v = kp.clone(), vp.clone()
+    kn, vn = rand(g, (8, D)), rand(g, (8, D))
+    # token 2 * bt + 5 is in the table's third block, whose entry is bad
+    ikv.attn_decode_paged(q, kp, vp, table, bt, 2 * bt + 6, k_new=kn, v_new=vn, status=status)
+    torch.cuda.synchronize()
+    assert int(status.cpu()[0]) == ikv.STATUS_BLOCK
+    assert torch.equal(kp, before_k) and torch.equal(vp, before_v)
     # a good table raises nothing
     status.zero_()
     good = torch.tensor([0, 1, 2, 3, 4], dtype=torch.int32, device=dev)
