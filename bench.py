@@ -59,33 +59,38 @@ def prefill_flops(p, n_head=N_HEAD, d=D):
     return n_head * (p * (p + 1) // 2) * 4 * d
 
 
-class DecodeRig:
-    """28 layers of KV cache at one context length, launched through the C-ABI."""
+def seeded(ikv, config, index, shape):
+    """Host float32 N(0, 1) samples of stream config_seed(config, index): the
+    portable splitmix64 / Box-Muller stream of ikv.synth (multithreaded C++
+    form), the same numbers for the GPU and the CPU legs."""
+    from ikv import synth
+    return ikv.synth_normal(synth.config_seed(config, index), shape, threads=16)
 
-    def __init__(self, torch, ikv, ctx, n_layer=N_LAYER, seed=0x1F0000 + 1000 + 2, n_head=N_HEAD,
-                 block_tokens=0):
+
+class DecodeRig:
+    """n_layer layers of KV cache at one context length, launched through the
+    C-ABI. Config 1 inputs: layer i's K and V caches are streams
+    config_seed(1, 100 + i) and (1, 200 + i); q, k_new, v_new (the same for
+    every layer) are (1, 300), (1, 301), (1, 302)."""
+
+    def __init__(self, torch, ikv, ctx, n_layer=N_LAYER, n_head=N_HEAD, block_tokens=0):
         self.torch, self.ikv, self.ctx, self.n_layer = torch, ikv, ctx, n_layer
         self.n_head = n_head
         self.block_tokens = block_tokens  # > 0: paged pools with a shuffled block table
         dev = torch.device("cuda:0")
-        g = torch.Generator(device=dev)
-        g.manual_seed(seed)
+        q = torch.from_numpy(seeded(ikv, 1, 300, (n_head, D))).to(dev)
+        kn = torch.from_numpy(seeded(ikv, 1, 301, (N_HEAD_KV, D))).to(dev)
+        vn = torch.from_numpy(seeded(ikv, 1, 302, (N_HEAD_KV, D))).to(dev)
         self.layers = []
-        for _ in range(n_layer):
-            kc = torch.empty((ctx + 1, N_HEAD_KV, D), device=dev)
-            vc = torch.empty((ctx + 1, N_HEAD_KV, D), device=dev)
-            kc.normal_(generator=g)
-            vc.normal_(generator=g)
-            self.layers.append(dict(
-                kc=kc, vc=vc,
-                q=torch.randn((n_head, D), generator=g, device=dev),
-                kn=torch.randn((N_HEAD_KV, D), generator=g, device=dev),
-                vn=torch.randn((N_HEAD_KV, D), generator=g, device=dev),
-                out=torch.empty((n_head, D), device=dev)))
+        for i in range(n_layer):
+            kc = torch.from_numpy(seeded(ikv, 1, 100 + i, (ctx + 1, N_HEAD_KV, D))).to(dev)
+            vc = torch.from_numpy(seeded(ikv, 1, 200 + i, (ctx + 1, N_HEAD_KV, D))).to(dev)
+            self.layers.append(dict(kc=kc, vc=vc, q=q, kn=kn, vn=vn,
+                                    out=torch.empty((n_head, D), device=dev)))
         if block_tokens:
             import numpy as np
             n_blocks = (ctx + 1 + block_tokens - 1) // block_tokens
-            rng = np.random.default_rng(seed)
+            rng = np.random.default_rng(0x1F0000 + 1000 + block_tokens)
             for L in self.layers:
                 pool_blocks = n_blocks + 4
                 table = rng.permutation(pool_blocks)[:n_blocks].astype(np.int32)
@@ -166,13 +171,28 @@ class DecodeRig:
         return e0.elapsed_time(e1) / 1e3  # seconds
 
 
-def time_prefill(torch, ikv, p, reps):
+def prefill_inputs(torch, ikv, p):
+    """BASELINE config 2 inputs at prompt length p: raw Q, K, V from streams
+    config_seed(2, 10 + p), (2, 20 + p), (2, 30 + p); Q and K then go through
+    the qk-RMSNorm (weight 1.0, eps 1e-6) and RoPE (theta 1e6, positions
+    0..p-1) of a Qwen3 layer on the device, as the model feeds attention."""
+    import numpy as np
     dev = torch.device("cuda:0")
-    g = torch.Generator(device=dev)
-    g.manual_seed(0x1F0000 + 2000 + p)
-    q = torch.randn((p, N_HEAD, D), generator=g, device=dev)
-    k = torch.randn((p, N_HEAD_KV, D), generator=g, device=dev)
-    v = torch.randn((p, N_HEAD_KV, D), generator=g, device=dev)
+    q = torch.from_numpy(seeded(ikv, 2, 10 + p, (p, N_HEAD, D))).to(dev)
+    k = torch.from_numpy(seeded(ikv, 2, 20 + p, (p, N_HEAD_KV, D))).to(dev)
+    v = torch.from_numpy(seeded(ikv, 2, 30 + p, (p, N_HEAD_KV, D))).to(dev)
+    s, c = ikv.rope_sincos_table(ikv.rope_theta_table(1e6, D, p))
+    s, c = torch.from_numpy(s).to(dev), torch.from_numpy(c).to(dev)
+    pos = torch.from_numpy(np.arange(p, dtype=np.int32)).to(dev)
+    ones = torch.ones(D, device=dev)
+    q = ikv.qk_norm_rope(q, ones, pos, 1e-6, s, c)
+    k = ikv.qk_norm_rope(k, ones, pos, 1e-6, s, c)
+    torch.cuda.synchronize()
+    return q, k, v
+
+
+def time_prefill(torch, ikv, p, reps):
+    q, k, v = prefill_inputs(torch, ikv, p)
     out = torch.empty_like(q)
     for _ in range(3):
         ikv.attn_prefill(q, k, v, 0, out=out)
@@ -193,9 +213,7 @@ def prefill_only(torch, ikv, p, reps):
     each timed over `reps` launches per layer with HIP events."""
     dev = torch.device("cuda:0")
     t_pre = time_prefill(torch, ikv, p, reps)
-    g = torch.Generator(device=dev)
-    g.manual_seed(0x1F0000 + 2000 + p + 1)
-    rows = torch.randn((p, N_HEAD_KV, D), generator=g, device=dev)
+    rows = torch.from_numpy(seeded(ikv, 2, 20 + p, (p, N_HEAD_KV, D))).to(dev)
     caches = [torch.empty((p, N_HEAD_KV, D), device=dev) for _ in range(N_LAYER)]
     for c in caches:
         ikv.append(c, rows)
@@ -355,19 +373,14 @@ def model_bench(configs, cpu_tokens):
 
     res = {}
     gpu_tokens0 = None
-    runs = [(c, 0, False) for c in configs]
+    runs = [(c, 0) for c in configs]
     if 3 in configs:
-        runs.append((3, 256, False))  # config 3 again on a paged cache of 256-token blocks
-        # and on the HBM <-> host offload tier, HBM budget = every layer of the sequence: each
-        # new sequence's layers start in pinned host memory holding no rows, so nothing moves
-        runs.append((3, 0, True))
-    for c, bt, off in runs:
+        runs.append((3, 256))  # config 3 again on a paged cache of 256-token blocks
+    for c, bt in runs:
         arch, P, N = MODEL_CONFIGS[c]
         cfg = getattr(qwen3, arch)
-        layer_bytes = (P + N) * cfg.n_head_kv * cfg.head_dim * 4 * 2
         t0 = time.perf_counter()
-        eng = qwen3.Qwen3Engine(cfg, P + N, block_tokens=bt,
-                                offload_hbm_bytes=cfg.n_layer * layer_bytes if off else 0)
+        eng = qwen3.Qwen3Engine(cfg, P + N, block_tokens=bt)
         eng.init_synthetic(synth.config_seed(c, 1), threads=16)
         init_s = time.perf_counter() - t0
         prompt = synth.uniform_ints(synth.config_seed(c, 0), P, cfg.n_vocab)
@@ -376,9 +389,7 @@ def model_bench(configs, cpu_tokens):
         # (the library loads its kernels on first use)
         eng.generate(prompt, 4)
         # 3 timed runs, medians reported (benchmarks/cpu/bench.cpp:421-431)
-        kv0 = eng.kv_stats() if off else None
         runs3 = [eng.generate(prompt, N) for _ in range(3)]
-        kv1 = eng.kv_stats() if off else None
         toks = runs3[0][0]
         if any(r[0] != toks for r in runs3[1:]):
             raise RuntimeError(f"config {c}: repeated runs gave different tokens")
@@ -388,7 +399,7 @@ def model_bench(configs, cpu_tokens):
         eng.close()
         if c == 0:
             gpu_tokens0 = toks
-        key = f"config{c}" + (f"_paged{bt}" if bt else "") + ("_offload" if off else "")
+        key = f"config{c}" + (f"_paged{bt}" if bt else "")
         res[key] = {
             "model": arch.lower().replace("_", "-").replace("-0-6b", "-0.6b"),
             "prompt": P, "generated": N, "ttft_ms": round(ttft_med * 1e3, 3),
@@ -400,20 +411,9 @@ def model_bench(configs, cpu_tokens):
                                      for _, sh in qwen3.tensor_layout(cfg)) * 4 / 2**30, 2),
             "init_s": round(init_s, 1),
         }
-        if off:
-            # per timed run: the bytes uploaded host -> HBM, and the rate implied by the TTFT
-            # over the all-HBM run of the same config (the uploads sit in the prefill step)
-            per_run = {k: (kv1[k] - kv0[k]) // 3 for k in kv1}
-            r = res[key]
-            r["kv_per_run"] = per_run
-            base = res.get(f"config{c}")
-            if base and per_run["bytes_in"] > 0 and r["ttft_ms"] > base["ttft_ms"]:
-                r["page_in_gbs_vs_hbm_ttft"] = round(
-                    per_run["bytes_in"] / ((r["ttft_ms"] - base["ttft_ms"]) * 1e-3) / 1e9, 1)
-        tail = f", per run {res[key]['kv_per_run']}" if off else ""
-        log(f"[bench] model config {c}{f' paged {bt}' if bt else ''}{' offload' if off else ''} "
+        log(f"[bench] model config {c}{f' paged {bt}' if bt else ''} "
             f"({arch}, P={P}, N={N}): TTFT {ttft_med * 1e3:.2f} ms, TPOT {t.tpot_s * 1e3:.3f} ms "
-            f"(medians of 3){tail}")
+            f"(medians of 3)")
     if cpu_tokens and 0 in configs:
         import oracle
 
@@ -442,27 +442,84 @@ def model_bench(configs, cpu_tokens):
         log(f"[bench] cpu config 0: TPOT {res['cpu_config0']['tpot_ms']} ms on {threads} threads, "
             f"tokens equal GPU: {res['cpu_config0']['tokens_equal_gpu_prefix']}")
         del w, orc
+    if 3 in configs:
+        res["config3_offload_2seq"] = offload_bench()
     return res
+
+
+HOST_LINK_GBS = 64.0  # PCIe 5.0 x16, one direction (the MI355X host link)
+
+
+def offload_bench(n_gen=48):
+    """Two config-3 sequences (Qwen3-0.6B, 2048-token prompts) decoded in
+    turn, on the HBM <-> host offload tier with an HBM budget of ONE
+    sequence's 28 layers, and on the all-HBM cache: every turn of the
+    offloaded run writes back the other sequence's appended rows and uploads
+    this one's committed rows (the reference's OffloadKVStorage under two
+    sequences, include/kvcache/KVStorages/offloadKVStorage.hpp:57-179).
+    Reports the bytes per run and the paging rate implied by the extra time
+    per round over the all-HBM run, against the host link."""
+    from ikv import qwen3, synth
+
+    cfg = qwen3.QWEN3_0_6B
+    P = MODEL_CONFIGS[3][1]
+    cap = P + n_gen
+    prompts = [synth.uniform_ints(synth.config_seed(3, 0), P, cfg.n_vocab),
+               synth.uniform_ints(synth.config_seed(3, 2), P, cfg.n_vocab)]
+    layer_bytes = cap * cfg.n_head_kv * cfg.head_dim * 4 * 2
+    out = {"model": "qwen3-0.6b", "sequences": 2, "prompt": P, "generated": n_gen,
+           "hbm_budget_bytes": cfg.n_layer * layer_bytes,
+           "combined_layer_bytes": 2 * cfg.n_layer * layer_bytes}
+    toks = {}
+    for name, budget in (("hbm", 0), ("offload", cfg.n_layer * layer_bytes)):
+        eng = qwen3.Qwen3Engine(cfg, cap, offload_hbm_bytes=budget)
+        eng.init_synthetic(synth.config_seed(3, 1), threads=16)
+        eng.generate_interleaved(prompts, 4)  # warm-up
+        kv0 = eng.kv_stats()
+        runs = [eng.generate_interleaved(prompts, n_gen) for _ in range(3)]
+        kv1 = eng.kv_stats()
+        eng.close()
+        toks[name] = runs[0][0]
+        if any(r[0] != toks[name] for r in runs[1:]):
+            raise RuntimeError(f"offload bench ({name}): repeated runs gave different tokens")
+        t = sorted((r[1] for r in runs), key=lambda x: x.tpot_s)[1]
+        out[f"{name}_round_ms"] = round(t.tpot_s * 1e3, 3)
+        out[f"{name}_ttft_ms"] = round(sorted(r[1].ttft_s for r in runs)[1] * 1e3, 2)
+        if budget:
+            out["kv_per_run"] = {k: (kv1[k] - kv0[k]) // 3 for k in kv1}
+    if toks["hbm"] != toks["offload"]:
+        raise RuntimeError("offload bench: the offloaded run's tokens differ from the all-HBM run's")
+    kv = out["kv_per_run"]
+    rounds = n_gen - 1
+    extra_s = (out["offload_round_ms"] - out["hbm_round_ms"]) * 1e-3
+    moved = (kv["bytes_in"] + kv["bytes_out"]) / max(rounds, 1)  # per round, both turns
+    out["bytes_per_round"] = int(moved)
+    out["tokens_equal_hbm"] = True
+    if extra_s > 0:
+        out["paging_gbs"] = round(moved / extra_s / 1e9, 1)
+        out["paging_frac_host_link"] = round(moved / extra_s / 1e9 / HOST_LINK_GBS, 3)
+    log(f"[bench] offload, 2 config-3 sequences in one sequence's HBM: round "
+        f"{out['offload_round_ms']} ms vs {out['hbm_round_ms']} ms all-HBM, per run {kv}, "
+        f"{out.get('paging_gbs')} GB/s paging")
+    return out
 
 
 def cpu_baseline(ctx, seconds):
     """The oracle (restated reference CPU backend) on this host: the same
     decode step (append + attention) of one layer, rotated over 8 layers."""
-    import numpy as np
-
+    import ikv
     import oracle
-    from ikv import synth
 
     workers = min(oracle.default_workers(), 15)
     threads = oracle.set_workers(workers)
     layers = []
-    for i in range(8):
-        kc = synth.normal(synth.config_seed(1, 100 + i), ((ctx + 1), N_HEAD_KV, D))
-        vc = synth.normal(synth.config_seed(1, 200 + i), ((ctx + 1), N_HEAD_KV, D))
+    for i in range(8):  # the GPU rig's first 8 layer caches
+        kc = seeded(ikv, 1, 100 + i, ((ctx + 1), N_HEAD_KV, D))
+        vc = seeded(ikv, 1, 200 + i, ((ctx + 1), N_HEAD_KV, D))
         layers.append((kc, vc))
-    q = synth.normal(synth.config_seed(1, 300), (N_HEAD, D))
-    kn = synth.normal(synth.config_seed(1, 301), (N_HEAD_KV, D))
-    vn = synth.normal(synth.config_seed(1, 302), (N_HEAD_KV, D))
+    q = seeded(ikv, 1, 300, (N_HEAD, D))
+    kn = seeded(ikv, 1, 301, (N_HEAD_KV, D))
+    vn = seeded(ikv, 1, 302, (N_HEAD_KV, D))
     oracle.decode_append_attn(q, kn, vn, *layers[0], ctx)  # warm
     n, t0 = 0, time.perf_counter()
     while True:
@@ -491,8 +548,8 @@ def cpu_sweep():
     :414-431)."""
     import numpy as np
 
+    import ikv
     import oracle
-    from ikv import synth
 
     workers = min(oracle.default_workers(), 15)
     threads = oracle.set_workers(workers)
@@ -511,19 +568,28 @@ def cpu_sweep():
         return sorted(ts)[1]
 
     res = {"threads": threads, "decode_gbs": {}, "prefill_ms": {}, "prefill_gflops": {}}
-    q = synth.normal(synth.config_seed(1, 300), (N_HEAD, D))
-    kn = synth.normal(synth.config_seed(1, 301), (N_HEAD_KV, D))
-    vn = synth.normal(synth.config_seed(1, 302), (N_HEAD_KV, D))
+    q = seeded(ikv, 1, 300, (N_HEAD, D))
+    kn = seeded(ikv, 1, 301, (N_HEAD_KV, D))
+    vn = seeded(ikv, 1, 302, (N_HEAD_KV, D))
     for ctx in (256, 1024, 4096, 16384, 32768):
-        kc = synth.normal(synth.config_seed(1, 100), ((ctx + 1), N_HEAD_KV, D))
-        vc = synth.normal(synth.config_seed(1, 200), ((ctx + 1), N_HEAD_KV, D))
+        kc = seeded(ikv, 1, 100, ((ctx + 1), N_HEAD_KV, D))
+        vc = seeded(ikv, 1, 200, ((ctx + 1), N_HEAD_KV, D))
         t = median3(lambda: oracle.decode_append_attn(q, kn, vn, kc, vc, ctx))
         res["decode_gbs"][str(ctx)] = round(decode_bytes(ctx) / t / 1e9, 2)
         del kc, vc
     for P in (32, 64, 128, 256, 2048):
-        qp = synth.normal(synth.config_seed(2, 10 + P), (P, N_HEAD, D))
-        kp = synth.normal(synth.config_seed(2, 20 + P), (P, N_HEAD_KV, D))
-        vp = synth.normal(synth.config_seed(2, 30 + P), (P, N_HEAD_KV, D))
+        # the GPU leg's inputs: the same streams, Q and K through the oracle's
+        # qk-RMSNorm and RoPE (bit-identical to the device ops)
+        th = oracle.rope_theta_table(1e6, D, P)
+        pos = np.arange(P, dtype=np.int32)
+        ones = np.ones(D, np.float32)
+
+        def norm_rope(x):
+            n = oracle.rms_norm(x.reshape(-1, D), ones, 1e-6).reshape(x.shape)
+            return oracle.rope_neox(n, pos, th)
+        qp = norm_rope(seeded(ikv, 2, 10 + P, (P, N_HEAD, D)))
+        kp = norm_rope(seeded(ikv, 2, 20 + P, (P, N_HEAD_KV, D)))
+        vp = seeded(ikv, 2, 30 + P, (P, N_HEAD_KV, D))
         kcache = np.empty_like(kp)
         vcache = np.empty_like(vp)
 
@@ -716,7 +782,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic: K,V,q,k_new,v_new ~ N(0,1) F32 (torch.randn, fixed seed)",
+        "data": "synthetic: K,V,q,k_new,v_new ~ N(0,1) F32 from the portable splitmix64 "
+                "streams config_seed(1, 100+layer / 200+layer / 300..302), the CPU leg's data",
         "config": {
             "workload": "decode attention + fused KV append, Qwen3-0.6B layer shape "
                         f"(16 q heads, 8 KV heads, head_dim 128), n_past {args.ctx}, one step = "

@@ -217,6 +217,14 @@ int ikv_rms_norm_f32(const float *x, const float *w, float *out, int64_t rows, i
                      float eps, void *stream);
 
 /* ---------------------------------------------------------------------
+ * Host helper: the RoPE angle table [n_ctx][head_dim/2] of
+ * GraphContext::get_rope_theta_table (src/graph.cpp:92-135):
+ * freq_i = 1.0f / powf(theta_base, (2.0f*i) / head_dim) in float, widened
+ * to double; theta_host[pos][i] = (float)(pos * freq_i). head_dim even.
+ * ------------------------------------------------------------------- */
+int ikv_rope_theta_table_f32(float theta_base, int head_dim, int64_t n_ctx, float *theta_host);
+
+/* ---------------------------------------------------------------------
  * Host helper: sin/cos tables from a RoPE angle table (host memory).
  * sin_host[i] = sinf(theta_host[i]), cos_host[i] = cosf(theta_host[i]) —
  * the per-step computation of src/backends/cpu_backend.cpp:472-487, done

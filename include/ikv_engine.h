@@ -95,6 +95,20 @@ int ikv_qwen3_init_synthetic(ikv_qwen3 *m, uint64_t seed, double std, int thread
 int ikv_qwen3_generate(ikv_qwen3 *m, const int32_t *prompt, int64_t n_prompt, int64_t n_gen,
                        int32_t *tokens_out, ikv_qwen3_timing *timing);
 
+/* n_seq (1..4) sequences of one cache decoded in turn: every prompt's
+ * prefill, then n_gen - 1 rounds of one token per sequence. prompts is
+ * [n_seq][n_prompt], tokens_out [n_seq][n_gen]; each sequence's tokens are
+ * those ikv_qwen3_generate gives its prompt alone. On an offloaded cache
+ * whose HBM budget holds fewer layers than the sequences together, each
+ * turn pages the next sequence's layers in (and the last one's written
+ * rows out): the reference's multi-sequence offload tier
+ * (include/kvcache/KVStorages/offloadKVStorage.hpp:57-179) under load.
+ * timing->tpot_s is per round of all sequences; ttft_s ends with the first
+ * round. */
+int ikv_qwen3_generate_interleaved(ikv_qwen3 *m, const int32_t *prompts, int64_t n_seq,
+                                   int64_t n_prompt, int64_t n_gen, int32_t *tokens_out,
+                                   ikv_qwen3_timing *timing);
+
 /* Fusions taken and kernel launches in the last step. */
 typedef struct ikv_qwen3_stats {
     int launches, fused_norm_rope, fused_append_decode, fused_swiglu, fused_residual, fused_qkv,

@@ -42,6 +42,7 @@
 #include "../../include/ikv.h"
 
 #include <climits>
+#include <vector>
 
 namespace {
 
@@ -317,6 +318,28 @@ extern "C" int ikv_rms_norm_f32(const float *x, const float *w, float *out, int6
   if (dim > kLdsFloats - 1) return -ENOTSUP;
   return launch_rows<true, false>(x, w, out, nullptr, rows, static_cast<int>(dim), eps, 1, nullptr,
                                   nullptr, 0, nullptr, stream);
+}
+
+extern "C" int ikv_rope_theta_table_f32(float theta_base, int head_dim, int64_t n_ctx,
+                                        float *theta_host) {
+  if (head_dim <= 0 || (head_dim & 1) || n_ctx < 0) return -EINVAL;
+  if (n_ctx == 0) return 0;
+  if (!theta_host) return -EINVAL;
+  const int half = head_dim / 2;
+  // the exponent 2i/d and the reciprocal power are float operations (the
+  // reference's float arguments to std::pow select powf); the angle is the
+  // position times the widened frequency, rounded once to float
+  std::vector<double> freq(static_cast<size_t>(half));
+  for (int i = 0; i < half; ++i) {
+    const float e = (2.0f * static_cast<float>(i)) / static_cast<float>(head_dim);
+    freq[static_cast<size_t>(i)] = static_cast<double>(1.0f / powf(theta_base, e));
+  }
+  for (int64_t pos = 0; pos < n_ctx; ++pos) {
+    float *row = theta_host + pos * half;
+    for (int i = 0; i < half; ++i)
+      row[i] = static_cast<float>(static_cast<double>(pos) * freq[static_cast<size_t>(i)]);
+  }
+  return 0;
 }
 
 extern "C" int ikv_rope_sincos_table_f32(const float *theta_host, size_t count, float *sin_host,

@@ -135,6 +135,23 @@ extern "C" int ikv_qwen3_generate(ikv_qwen3 *m, const int32_t *prompt, int64_t n
   return 0;
 }
 
+extern "C" int ikv_qwen3_generate_interleaved(ikv_qwen3 *m, const int32_t *prompts, int64_t n_seq,
+                                              int64_t n_prompt, int64_t n_gen,
+                                              int32_t *tokens_out, ikv_qwen3_timing *timing) {
+  if (!m || !prompts || n_seq <= 0 || n_seq > Qwen3Runner::kMaxInterleaved || n_prompt <= 0 ||
+      n_gen <= 0 || !tokens_out)
+    return -EINVAL;
+  std::vector<std::vector<int32_t>> p(static_cast<size_t>(n_seq)), toks;
+  for (int64_t s = 0; s < n_seq; ++s) p[s].assign(prompts + s * n_prompt, prompts + (s + 1) * n_prompt);
+  GenerationTiming t;
+  auto r = m->runner->generate_interleaved(p, size_t(n_gen), toks, t);
+  if (!r) return to_errno(r.error());
+  for (int64_t s = 0; s < n_seq; ++s)
+    for (int64_t i = 0; i < n_gen; ++i) tokens_out[s * n_gen + i] = toks[s][i];
+  if (timing) *timing = {t.ttft_s, t.tpot_s, t.wall_s, t.build_s, t.execute_s, t.sample_s};
+  return 0;
+}
+
 extern "C" int ikv_qwen3_last_stats(const ikv_qwen3 *m, ikv_qwen3_stats *out) {
   if (!m || !out) return -EINVAL;
   const auto &s = static_cast<const HIPBackend *>(m->backend.get())->last_stats();

@@ -3,6 +3,8 @@
 #include <cmath>
 #include <new>
 
+#include "../../include/ikv.h"
+
 #include "kvcache/kvcache_manager.hpp"
 
 Tensor *Graph::add_node(std::unique_ptr<Tensor> t) {
@@ -55,16 +57,9 @@ infer::expected<Tensor *, std::error_code> GraphContext::get_rope_theta_table(fl
   std::unique_ptr<float[]> buf(new (std::nothrow) float[static_cast<size_t>(half) * n_ctx]);
   if (!buf) return infer::fail(std::errc::not_enough_memory);
   // freq_i = 1 / theta^(2i/d) evaluated in float (the exponent 2i/d too),
-  // widened to double; angle = float(double(pos) * freq_i).
-  std::vector<double> freq(half);
-  for (uint32_t i = 0; i < half; ++i) {
-    const float e = (2.0f * static_cast<float>(i)) / static_cast<float>(head_dim);
-    freq[i] = static_cast<double>(1.0f / std::pow(theta_base, e));
-  }
-  for (uint32_t pos = 0; pos < n_ctx; ++pos) {
-    float *row = buf.get() + static_cast<size_t>(pos) * half;
-    for (uint32_t i = 0; i < half; ++i) row[i] = static_cast<float>(static_cast<double>(pos) * freq[i]);
-  }
+  // widened to double; angle = float(double(pos) * freq_i)
+  if (ikv_rope_theta_table_f32(theta_base, int(head_dim), n_ctx, buf.get()) != 0)
+    return infer::fail(std::errc::invalid_argument);
   t->data = buf.get();
   _rope_buffers.push_back(std::move(buf));
   _rope_theta_cache[key] = t;

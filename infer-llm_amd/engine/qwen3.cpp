@@ -228,13 +228,13 @@ infer::expected<void, std::error_code> Qwen3Runner::init() {
     (void)hipGetLastError();
     return infer::fail(std::errc::not_enough_memory);
   };
-  if (hipMalloc(&_token_dev, 2 * sizeof(int32_t)) != hipSuccess) return fail_alloc();
+  if (hipMalloc(&_token_dev, kSlots * sizeof(int32_t)) != hipSuccess) return fail_alloc();
   if (hipMalloc(&_positions_dev, _capacity * sizeof(int32_t)) != hipSuccess) return fail_alloc();
   if (hipMalloc(&_argmax_ws, ikv_argmax_workspace_bytes()) != hipSuccess ||
       hipMemset(_argmax_ws, 0, ikv_argmax_workspace_bytes()) != hipSuccess)
     return fail_alloc();
   // Mapped and coherent: the sampler's store reaches host memory directly.
-  if (hipHostMalloc(&_token_host, 2 * sizeof(int32_t), hipHostMallocMapped | hipHostMallocCoherent) !=
+  if (hipHostMalloc(&_token_host, kSlots * sizeof(int32_t), hipHostMallocMapped | hipHostMallocCoherent) !=
           hipSuccess ||
       hipHostGetDevicePointer(reinterpret_cast<void **>(&_token_host_dev), _token_host, 0) !=
           hipSuccess)
@@ -250,7 +250,8 @@ infer::expected<void, std::error_code> Qwen3Runner::init() {
 }
 
 infer::expected<void, std::error_code> Qwen3Runner::enqueue_step(const int32_t *host_tokens,
-                                                                 int64_t n, int slot,
+                                                                 int64_t n, int in_slot,
+                                                                 int out_slot,
                                                                  GenerationTiming &timing) {
   using Clock = std::chrono::steady_clock;
   const auto t0 = Clock::now();
@@ -267,7 +268,7 @@ infer::expected<void, std::error_code> Qwen3Runner::enqueue_step(const int32_t *
     _tokens->device = DeviceType::CPU;
     _tokens->backend = nullptr;
   } else {  // the previous step's greedy token, already on the device
-    _tokens->data = _token_dev + (slot ^ 1);
+    _tokens->data = _token_dev + in_slot;
     _tokens->device = DeviceType::HIP;
     _tokens->backend = &_backend;
   }
@@ -291,9 +292,9 @@ infer::expected<void, std::error_code> Qwen3Runner::enqueue_step(const int32_t *
   hipStream_t s = _backend.stream();
   // The sampler writes the token to the device slot the next step embeds
   // and to the pinned host slot the host reads once the event has fired.
-  if (ikv_argmax_ws_f32(row, vocab, _token_dev + slot, _token_host_dev + slot, _argmax_ws,
+  if (ikv_argmax_ws_f32(row, vocab, _token_dev + out_slot, _token_host_dev + out_slot, _argmax_ws,
                         ikv_argmax_workspace_bytes(), s) != 0 ||
-      hipEventRecord(_ready[slot], s) != hipSuccess)
+      hipEventRecord(_ready[out_slot], s) != hipSuccess)
     return abort(std::make_error_code(std::errc::io_error));
   // The kernels of this step hold no host-side state: hand the layer
   // accesses back and commit the appended range now.
@@ -349,12 +350,81 @@ infer::expected<void, std::error_code> Qwen3Runner::generate(const std::vector<i
     return {};
   };
   // step i writes token slot i % 2 and reads slot (i - 1) % 2
-  if (auto r = enqueue_step(prompt.data(), int64_t(prompt.size()), 0, timing); !r) return finish(r);
+  if (auto r = enqueue_step(prompt.data(), int64_t(prompt.size()), 1, 0, timing); !r)
+    return finish(r);
   for (size_t i = 1; i < n_gen; ++i) {
-    if (auto r = enqueue_step(nullptr, 1, int(i & 1), timing); !r) return finish(r);
+    if (auto r = enqueue_step(nullptr, 1, int((i - 1) & 1), int(i & 1), timing); !r)
+      return finish(r);
     if (auto r = take(int((i - 1) & 1), i - 1); !r) return finish(r);
   }
   if (auto r = take(int((n_gen - 1) & 1), n_gen - 1); !r) return finish(r);
+  timing.wall_s = std::chrono::duration<double>(Clock::now() - start).count();
+  timing.ttft_s = std::chrono::duration<double>(first - start).count();
+  timing.tpot_s =
+      n_gen > 1 ? std::chrono::duration<double>(last - first).count() / double(n_gen - 1) : 0.0;
+  return finish({});
+}
+
+infer::expected<void, std::error_code> Qwen3Runner::generate_interleaved(
+    const std::vector<std::vector<int32_t>> &prompts, size_t n_gen,
+    std::vector<std::vector<int32_t>> &tokens_out, GenerationTiming &timing) {
+  using Clock = std::chrono::steady_clock;
+  const size_t n_seq = prompts.size();
+  if (n_seq == 0 || n_seq > size_t(kMaxInterleaved) || n_gen == 0)
+    return infer::fail(std::errc::invalid_argument);
+  for (const auto &p : prompts) {
+    if (p.empty()) return infer::fail(std::errc::invalid_argument);
+    if (p.size() + n_gen - 1 > _capacity) return infer::fail(std::errc::value_too_large);
+  }
+  if (!_kv) return infer::fail(std::errc::invalid_argument);
+  std::vector<SequenceId> seqs;
+  auto finish = [&](infer::expected<void, std::error_code> r) {
+    const auto sync = _backend.synchronize();
+    (void)_ctx->release_kv_access();
+    (void)_ctx->set_kv_cache(nullptr, kInvalidSequenceId);
+    for (SequenceId id : seqs) (void)_kv->release_sequence(id);
+    _seq = kInvalidSequenceId;
+    if (r && !sync) return sync;
+    return r;
+  };
+  for (size_t s = 0; s < n_seq; ++s) {
+    auto sid = _kv->create_sequence();
+    if (!sid) return finish(infer::unexpected(sid.error()));
+    seqs.push_back(*sid);
+  }
+  timing = GenerationTiming{};
+  tokens_out.assign(n_seq, {});
+  // sequence s, step i: writes slot 2s + i % 2, reads slot 2s + (i - 1) % 2
+  auto turn = [&](size_t s, size_t i) -> infer::expected<void, std::error_code> {
+    _seq = seqs[s];
+    if (auto r = _ctx->set_kv_cache(_kv.get(), _seq); !r) return r;
+    const int base = int(2 * s);
+    if (i == 0)
+      return enqueue_step(prompts[s].data(), int64_t(prompts[s].size()), base + 1, base, timing);
+    return enqueue_step(nullptr, 1, base + int((i - 1) & 1), base + int(i & 1), timing);
+  };
+  const auto start = Clock::now();
+  Clock::time_point first{}, last{};
+  auto take_round = [&](size_t i) -> infer::expected<void, std::error_code> {
+    const auto t0 = Clock::now();
+    for (size_t s = 0; s < n_seq; ++s) {
+      auto tok = collect(int(2 * s) + int(i & 1));
+      if (!tok) return infer::unexpected(tok.error());
+      tokens_out[s].push_back(*tok);
+    }
+    const auto ready = Clock::now();
+    timing.sample_s += std::chrono::duration<double>(ready - t0).count();
+    if (i == 0) first = ready;
+    last = ready;
+    return {};
+  };
+  for (size_t i = 0; i < n_gen; ++i) {
+    for (size_t s = 0; s < n_seq; ++s)
+      if (auto r = turn(s, i); !r) return finish(r);
+    if (i > 0)
+      if (auto r = take_round(i - 1); !r) return finish(r);
+  }
+  if (auto r = take_round(n_gen - 1); !r) return finish(r);
   timing.wall_s = std::chrono::duration<double>(Clock::now() - start).count();
   timing.ttft_s = std::chrono::duration<double>(first - start).count();
   timing.tpot_s =

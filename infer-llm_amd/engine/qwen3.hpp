@@ -130,14 +130,28 @@ class Qwen3Runner {
   infer::expected<void, std::error_code> generate(const std::vector<int32_t> &prompt, size_t n_gen,
                                                   std::vector<int32_t> &tokens_out,
                                                   GenerationTiming &timing);
+  // Up to kMaxInterleaved sequences decoded in turn, one step each per
+  // round: prefill of every prompt, then n_gen - 1 rounds of one token per
+  // sequence. Each sequence's tokens are those generate() gives it alone; on
+  // an offloaded cache whose HBM budget holds fewer layers than the
+  // sequences have, every turn pages the next sequence's layers in.
+  // Timing: ttft = first round done - start, tpot = (last round - first
+  // round) / (n_gen - 1), per round of all sequences.
+  static constexpr int kMaxInterleaved = 4;
+  infer::expected<void, std::error_code> generate_interleaved(
+      const std::vector<std::vector<int32_t>> &prompts, size_t n_gen,
+      std::vector<std::vector<int32_t>> &tokens_out, GenerationTiming &timing);
   // Page-in / write-back counts of an offloaded cache (zeros otherwise).
   OffloadStats offload_stats() const;
 
  private:
-  // Enqueues one step; its greedy token lands in token slot `slot` (device)
-  // and, once event `slot` has fired, in _token_host[slot].
+  // Enqueues one step of sequence _seq: its input is the host prompt, or
+  // (host_tokens NULL) the token in device slot in_slot; its greedy token
+  // lands in device slot out_slot and, once event out_slot has fired, in
+  // _token_host[out_slot].
   infer::expected<void, std::error_code> enqueue_step(const int32_t *host_tokens, int64_t n,
-                                                      int slot, GenerationTiming &timing);
+                                                      int in_slot, int out_slot,
+                                                      GenerationTiming &timing);
   infer::expected<int32_t, std::error_code> collect(int slot);
 
   Qwen3Model &_model;
@@ -151,10 +165,11 @@ class Qwen3Runner {
   SequenceId _seq = kInvalidSequenceId;
   Tensor *_tokens = nullptr, *_pos = nullptr;
   std::vector<int32_t> _input;
-  int32_t *_token_dev = nullptr;    // [2] sampled-token slots
-  int32_t *_token_host = nullptr;   // [2] pinned read-back slots
+  static constexpr int kSlots = 2 * kMaxInterleaved;
+  int32_t *_token_dev = nullptr;    // [kSlots] sampled-token slots, two per sequence
+  int32_t *_token_host = nullptr;   // [kSlots] pinned read-back slots
   int32_t *_token_host_dev = nullptr;  // the same slots as the device addresses them
   int32_t *_positions_dev = nullptr;  // [capacity]: 0, 1, 2, ...
   void *_argmax_ws = nullptr;         // the multi-workgroup sampler's workspace (zeroed once)
-  hipEvent_t _ready[2] = {nullptr, nullptr};
+  hipEvent_t _ready[kSlots] = {};
 };

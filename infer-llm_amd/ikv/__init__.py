@@ -83,6 +83,7 @@ SIGNATURES = {
     ),
     "ikv_rms_norm_f32": (
         _c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int64, _c_int64, _c_float, _c_void_p]),
+    "ikv_rope_theta_table_f32": (_c_int, [_c_float, _c_int, _c_int64, _c_void_p]),
     "ikv_rope_sincos_table_f32": (_c_int, [_c_void_p, _c_size_t, _c_void_p, _c_void_p]),
     "ikv_rope_neox_f32": (
         _c_int,
@@ -444,6 +445,16 @@ def rms_norm(x, w, eps: float, out=None, stream=None):
     rows = x.numel() // dim
     _check("ikv_rms_norm_f32",
            load().ikv_rms_norm_f32(_ptr(x), _ptr(w), _ptr(out), rows, dim, eps, _stream(stream)))
+    return out
+
+
+def rope_theta_table(theta_base: float, head_dim: int, n_ctx: int):
+    """Host RoPE angle table [n_ctx][head_dim/2] (numpy float32), the
+    engine's own (GraphContext::get_rope_theta_table)."""
+    import numpy as np
+    out = np.empty((n_ctx, head_dim // 2), dtype=np.float32)
+    _check("ikv_rope_theta_table_f32",
+           load().ikv_rope_theta_table_f32(theta_base, head_dim, n_ctx, out.ctypes.data))
     return out
 
 

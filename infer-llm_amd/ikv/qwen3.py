@@ -73,6 +73,8 @@ ENGINE_SIGNATURES = {
     "ikv_qwen3_init_synthetic": (ctypes.c_int, [_P, ctypes.c_uint64, ctypes.c_double, ctypes.c_int]),
     "ikv_qwen3_generate": (ctypes.c_int, [_P, _P, ctypes.c_int64, ctypes.c_int64, _P,
                                           ctypes.POINTER(Timing)]),
+    "ikv_qwen3_generate_interleaved": (ctypes.c_int, [_P, _P, ctypes.c_int64, ctypes.c_int64,
+                                                      ctypes.c_int64, _P, ctypes.POINTER(Timing)]),
     "ikv_qwen3_last_stats": (ctypes.c_int, [_P, ctypes.POINTER(Stats)]),
     "ikv_qwen3_set_fusion": (ctypes.c_int, [_P, ctypes.c_int]),
     "ikv_qwen3_destroy": (None, [_P]),
@@ -191,6 +193,17 @@ class Qwen3Engine:
         t = Timing()
         _check("ikv_qwen3_generate", _lib().ikv_qwen3_generate(
             self._h, p.ctypes.data, p.size, n_gen, out.ctypes.data, ctypes.byref(t)))
+        return out.tolist(), t
+
+    def generate_interleaved(self, prompts, n_gen: int):
+        """Greedy tokens of several equal-length prompts decoded in turn (one
+        step each per round): a list of token lists, and Timing per round."""
+        p = np.ascontiguousarray(np.stack([np.asarray(x, np.int32) for x in prompts]))
+        out = np.empty((p.shape[0], n_gen), np.int32)
+        t = Timing()
+        _check("ikv_qwen3_generate_interleaved", _lib().ikv_qwen3_generate_interleaved(
+            self._h, p.ctypes.data, p.shape[0], p.shape[1], n_gen, out.ctypes.data,
+            ctypes.byref(t)))
         return out.tolist(), t
 
     def last_stats(self):

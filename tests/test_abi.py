@@ -140,6 +140,17 @@ def test_sincos_table_is_bitwise_glibc():
     assert np.array_equal(s.view(np.uint32), sin_ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("base,hd,n_ctx", [(1e6, 128, 40960), (1e4, 64, 300), (5e5, 2, 17)])
+def test_theta_table_equals_the_oracle_bitwise(base, hd, n_ctx):
+    # the product's angle table (the engine and the benchmark build theirs
+    # with it) against the oracle's restatement of src/graph.cpp:92-135
+    got = ikv.rope_theta_table(base, hd, n_ctx)
+    want = oracle.rope_theta_table(base, hd, n_ctx)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert _rc("ikv_rope_theta_table_f32", 1e6, 127, 10, None) == -errno.EINVAL
+    assert _rc("ikv_rope_theta_table_f32", 1e6, 128, 0, None) == 0
+
+
 def test_paged_entry_points_reject_bad_descriptors():
     P = 64
     good = ikv.KvPages(P, 64, 10, None)

@@ -196,6 +196,34 @@ def test_prefill_causal_qwen3_06b(dev, P):
     assert_attn_close(out, want, f"P={P}")
 
 
+@pytest.mark.parametrize("P", [32, 64, 128, 256, 2048])
+def test_prefill_config2_inputs_after_qk_norm_rope(dev, P):
+    """BASELINE config 2 as the benchmark feeds it: Q and K are the seeded
+    streams config_seed(2, 10 + P) / (2, 20 + P) after the layer's
+    qk-RMSNorm (weight 1, eps 1e-6) and RoPE (theta 1e6, positions 0..P-1);
+    V is (2, 30 + P). The device-side preparation equals the oracle's bit for
+    bit, and the prefill output matches the oracle's attention on it."""
+    th = ikv.rope_theta_table(1e6, D, P)
+    s, c = ikv.rope_sincos_table(th)
+    s, c = torch.from_numpy(s).to(dev), torch.from_numpy(c).to(dev)
+    pos = np.arange(P, dtype=np.int32)
+    ones = np.ones(D, np.float32)
+    raw = {n: ikv.synth_normal(synth.config_seed(2, i + P), (P, h, D), threads=8)
+           for n, i, h in (("q", 10, 16), ("k", 20, 8), ("v", 30, 8))}
+    dev_in = {n: ikv.qk_norm_rope(torch.from_numpy(raw[n]).to(dev), torch.ones(D, device=dev),
+                                  torch.from_numpy(pos).to(dev), 1e-6, s, c) for n in ("q", "k")}
+    host_in = {n: oracle.rope_neox(oracle.rms_norm(raw[n].reshape(-1, D), ones, 1e-6)
+                                   .reshape(raw[n].shape), pos, oracle.rope_theta_table(1e6, D, P))
+               for n in ("q", "k")}
+    for n in ("q", "k"):
+        assert np.array_equal(bits(dev_in[n].cpu().numpy()), bits(host_in[n])), n
+    v = torch.from_numpy(raw["v"]).to(dev)
+    out = ikv.attn_prefill(dev_in["q"], dev_in["k"], v, 0)
+    torch.cuda.synchronize()
+    want = oracle.flash_attn(host_in["q"], host_in["k"], raw["v"], 0)
+    assert_attn_close(out.cpu().numpy(), want, f"config 2 P={P}")
+
+
 @pytest.mark.parametrize("n_q,n_past", [(17, 100), (64, 1000), (3, 4093), (128, 128), (1999, 77)])
 def test_prefill_with_history(dev, n_q, n_past):
     out, want = run_prefill_case(dev, n_q, n_past, seed=2)

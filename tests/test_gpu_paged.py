@@ -285,3 +285,37 @@ def test_offload_engine_matches_hbm_cache(dev, oracle_pool):
         small.generate(prompt, 5)
     for e in (flat, off, small):
         e.close()
+
+
+@pytest.mark.parametrize("budget_layers", [3, 4])
+def test_offload_interleaved_sequences_page_and_keep_tokens(dev, oracle_pool, budget_layers):
+    """Two sequences decoded in turn on a cache whose HBM budget holds one
+    sequence's 3 layers (or 4 of the 6): every turn evicts the other
+    sequence's layers (writing back the rows it appended) and uploads this
+    one's committed rows, and each sequence's tokens stay those it gets
+    alone, which the oracle pins."""
+    from ikv import qwen3
+    cfg = qwen3.Qwen3Config(n_layer=3, n_vocab=8192, n_ctx_train=4096)
+    w = qwen3.synthetic_weights(cfg, synth.config_seed(0, 32))
+    prompts = [synth.uniform_ints(synth.config_seed(0, 33 + i), 40, cfg.n_vocab) for i in range(2)]
+    P, N, cap = 40, 24, 64
+    want = [oracle.Qwen3Oracle(cfg, w, cap).generate(p, N) for p in prompts]
+    flat = qwen3.Qwen3Engine(cfg, cap)
+    flat.set_weights(w)
+    assert [flat.generate(p, N)[0] for p in prompts] == want
+    assert flat.generate_interleaved(prompts, N)[0] == want
+    layer_bytes = cap * 8 * 128 * 4 * 2
+    off = qwen3.Qwen3Engine(cfg, cap, offload_hbm_bytes=budget_layers * layer_bytes)
+    off.set_weights(w)
+    toks, t = off.generate_interleaved(prompts, N)
+    assert toks == want
+    st = off.kv_stats()
+    # every decode turn after the first round pages the sequence back in
+    assert st["page_ins"] >= (N - 1) * (6 - budget_layers) and st["evictions"] > 0
+    assert st["bytes_in"] > 0 and st["bytes_out"] > 0
+    # the rows moved are the committed ones: at most the whole sequence per layer
+    assert st["bytes_in"] <= st["page_ins"] * (P + N) * 8 * 128 * 4 * 2
+    assert t.tpot_s > 0
+    for e in (flat, off):
+        e.close()
+
