@@ -203,14 +203,13 @@ int ikv_attn_prefill_paged_f32(const float *q, const float *k_pool, const float 
  * RMS norm over rows of `dim` floats: out = (x * s) * w with
  * s = float(1 / sqrt(sum_d double(x_d*x_d) / dim + eps)) — the arithmetic of
  * CPUBackend::compute_rms_norm (src/backends/cpu_backend.cpp:335-382).
- * Rows shorter than 512 floats (head rows) take the double sum in index
- * order, so results are bit-identical to the reference. Rows of 512 or more
- * floats with dim % 256 == 0 (model-width rows) take it in a fixed
- * lane-strided order (lane l of a wavefront adds elements 256*j + 4*l + c,
- * then an xor butterfly): the float scale equals the reference's unless the
- * two double sums straddle a float rounding boundary (about 2^-27 of rows),
- * and equals that of the norm folded into ikv_gemv3_f32 /
- * ikv_gemv_swiglu_f32 bit for bit.
+ * The double sum is taken in parallel and the float scale is certified
+ * against the reference's index-order sum: when the parallel sum's double
+ * scale lies farther from a float rounding midpoint than the two sums can
+ * differ, both round to the same float; otherwise (about 2^-16 of rows) the
+ * row is summed again in index order. Results are bit-identical to the
+ * reference for every row, and to the norm folded into ikv_gemv3_f32 /
+ * ikv_gemv_swiglu_f32.
  * Replaces CUDA_F32::compute_rms_norm (src/kernels/cuda/kernel_f32.cu:16-90).
  * ------------------------------------------------------------------- */
 int ikv_rms_norm_f32(const float *x, const float *w, float *out, int64_t rows, int64_t dim,

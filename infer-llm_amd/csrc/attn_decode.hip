@@ -348,30 +348,29 @@ __device__ __forceinline__ void qk_prologue(const Prologue &pro, ProStage<G> &st
     if (i < S::n_el) s[i / D][i - (i / D) * D] = st.el[u];
   }
   __syncthreads();
-  if (tid <= G) {
-    // In index order, as the reference's loop. The row's next 8 floats are
-    // read from LDS while the current 8 are added, so the chain of dependent
-    // double adds is not broken up by LDS round trips.
-    const float4 *row = reinterpret_cast<const float4 *>(&s[tid][0]);
-    double sum = 0.0;
-    float4 a = row[0], b = row[1];
+  {
+    // Row r's sum of squares by half-wave r: lane c adds the squares of
+    // elements 4c..4c+3, a xor butterfly over the half-wave adds the lanes
+    // (8 roundings on any term's path), and the scale is certified against
+    // the reference's index-order sum (127 roundings); lane 0 redoes the sum
+    // in index order when it is not certain. The ordered sum alone is a
+    // chain of 128 dependent double adds, about 1.1 us on MI355X.
+    static_assert((G + 1) * 32 <= WG, "a half-wave per row");
+    const int r = tid >> 5;
+    const int c = tid & 31;
+    if (r <= G) {
+      const float4 v = *reinterpret_cast<const float4 *>(&s[r][4 * c]);
+      const float a = v.x * v.x, b = v.y * v.y, e = v.z * v.z, f = v.w * v.w;
+      double part = static_cast<double>(a);
+      part += static_cast<double>(b);
+      part += static_cast<double>(e);
+      part += static_cast<double>(f);
 #pragma unroll
-    for (int c = 0; c < D / 8; ++c) {
-      float4 na = a, nb = b;
-      if (c + 1 < D / 8) {
-        na = row[2 * c + 2];
-        nb = row[2 * c + 3];
-      }
-      const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float sq = v[e] * v[e];
-        sum += static_cast<double>(sq);
-      }
-      a = na;
-      b = nb;
+      for (int o = 16; o > 0; o >>= 1) part += __shfl_xor(part, o, 64);
+      float sc = 0.f;
+      const bool certain = ikv::certified_rms_scale(part, D, pro.eps, (D - 1) + 8, sc);
+      if (c == 0) scl[r] = certain ? sc : ikv::ordered_rms_scale(&s[r][0], D, pro.eps);
     }
-    scl[tid] = static_cast<float>(1.0 / sqrt(sum / static_cast<double>(D) + static_cast<double>(pro.eps)));
   }
   __syncthreads();
 #pragma unroll

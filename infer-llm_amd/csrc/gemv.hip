@@ -91,7 +91,8 @@ __device__ __forceinline__ float rms_scale_from_first(const float4 (&first)[kBat
     s += static_cast<double>(d);
   }
   for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
-  return static_cast<float>(1.0 / sqrt(s / static_cast<double>(dim) + static_cast<double>(eps)));
+  return ikv::certified_or_ordered_scale(s, reinterpret_cast<const float *>(row), dim, eps,
+                                         (dim - 1) + dim / 64 + 5, lane);
 }
 
 // Sums of NR rows (row r at rows[r], K columns, K % 1024 == 0) dotted with

@@ -80,11 +80,67 @@ __device__ __forceinline__ float4 scale4(float s, const float4 v) {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// The reference's RMSNorm scale is float(1 / sqrt(S / dim + eps)), S the
+// row's float squares summed in double in index order
+// (src/backends/cpu_backend.cpp:335-382): a chain of dim dependent double
+// adds. A kernel that sums the same squares in another order (in parallel)
+// gets S' with |S' - S| <= n_err * 2^-53 * S', n_err the longest chain of
+// roundings of the two orders together (dim - 1 for the index order plus the
+// other order's). The doubles computed from S and S' by the same four
+// correctly rounded operations then differ by at most
+// (n_err / 2 + 8) * 2^-53 relative. This returns the float scale from S'
+// when every double within 64 times that of its value rounds to the same
+// float, which makes it the reference's float bit for bit; it returns false
+// (about 2^-16 of rows; also for zero, infinite and NaN values) when the
+// caller must sum in index order instead.
+__device__ __forceinline__ bool certified_rms_scale(double s_any, int dim, float eps, int n_err,
+                                                    float &scale) {
+  const double t = 1.0 / sqrt(s_any / static_cast<double>(dim) + static_cast<double>(eps));
+  if (!(t > 1e-30) || !(t < 1e30)) return false;
+  const float f = static_cast<float>(t);
+  const double fd = static_cast<double>(f);
+  const unsigned bits = __float_as_uint(f);
+  // the float next to f on t's side, and the rounding midpoint between them
+  // (exact in double: two adjacent floats)
+  const double nb = static_cast<double>(__uint_as_float(t >= fd ? bits + 1u : bits - 1u));
+  const double mid = 0.5 * (fd + nb);
+  const double rel = (0.5 * n_err + 8.0) * 0x1p-53;
+  if (fabs(mid - t) <= 64.0 * rel * t) return false;
+  scale = f;
+  return true;
+}
+
+// The reference's scale from its index-order sum of the row's float squares.
+__device__ __forceinline__ float ordered_rms_scale(const float *row, int dim, float eps) {
+  double sum = 0.0;
+  for (int i = 0; i < dim; ++i) {
+    const float x = row[i];
+    const float sq = x * x;
+    sum += static_cast<double>(sq);
+  }
+  return static_cast<float>(1.0 / sqrt(sum / static_cast<double>(dim) + static_cast<double>(eps)));
+}
+
+// certified_rms_scale for a sum that every lane of the wave holds, else the
+// index-order sum by lane 0, broadcast (wave-uniform control flow).
+__device__ __forceinline__ float certified_or_ordered_scale(double s_any, const float *row,
+                                                            int dim, float eps, int n_err,
+                                                            int lane) {
+  float scale = 0.f;
+  if (certified_rms_scale(s_any, dim, eps, n_err, scale)) return scale;
+  float seq = 0.f;
+  if (lane == 0) seq = ordered_rms_scale(row, dim, eps);
+  return __shfl(seq, 0, 64);
+}
+
 // RMSNorm scale float(1 / sqrt(sum/dim + eps)) of a row of dim floats
-// (dim % 256 == 0, row 16-byte aligned) for one wavefront: lane l adds in
-// double, in this order, the float squares of elements 256*j + 4*l + c
-// (j ascending, c = 0..3); the 64 lane sums combine in a fixed xor butterfly
-// (32, 16, ..., 1), so every lane of every wave gets the same bits.
+// (dim % 256 == 0, row 16-byte aligned) for one wavefront, equal to the
+// reference's bit for bit: lane l adds in double the float squares of
+// elements 256*j + 4*l + c (j ascending, c = 0..3), the 64 lane sums combine
+// in a xor butterfly (32, 16, ..., 1; every lane gets the same bits), and the
+// scale is certified against the index-order sum (certified_rms_scale); when
+// it is not certain, lane 0 sums the row in index order (about 9 us for 1024
+// floats; rare) and every lane takes that.
 __device__ __forceinline__ float rms_scale_strided(const float4 *row, int dim, float eps, int lane) {
   double s = 0.0;
 #pragma unroll 4
@@ -97,7 +153,8 @@ __device__ __forceinline__ float rms_scale_strided(const float4 *row, int dim, f
     s += static_cast<double>(d);
   }
   for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
-  return static_cast<float>(1.0 / sqrt(s / static_cast<double>(dim) + static_cast<double>(eps)));
+  return certified_or_ordered_scale(s, reinterpret_cast<const float *>(row), dim, eps,
+                                    (dim - 1) + dim / 64 + 5, lane);
 }
 
 // ORs an IKV_STATUS_* bit into a caller's device status word (a vector

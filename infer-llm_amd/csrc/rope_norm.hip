@@ -13,26 +13,28 @@
 // Contraction into FMA is disabled in this file so every product and sum
 // rounds exactly as the reference's separate float operations do.
 //
-// Two sums of squares:
-//  * rows shorter than kLongRow (the head_dim rows of qk-norm): one lane per
-//    row adds the float squares in index order in double — exactly the
-//    reference's loop, so outputs are bit-identical to it;
+// Sums of squares: the reference adds a row's float squares in index order in
+// double, a chain of dim dependent double adds (about 1.1 us for 128 on
+// MI355X). The kernels add them in parallel instead and certify the float
+// scale against the index-order sum (ikv::certified_rms_scale): the two sums
+// differ by a bounded amount, and when the double scale is farther than that
+// from a float rounding midpoint, both round to the same float. When it is
+// not (about 2^-16 of rows), one lane redoes the sum in index order. Every
+// scale is therefore the reference's bit for bit.
+//  * rows shorter than kLongRow (the head_dim rows of qk-norm): half-wave per
+//    row, lane c adds elements c, c + 32, ..., then a xor butterfly;
 //  * rows of kLongRow or more floats, a multiple of 256 (the model-width
 //    rows of attn_norm / ffn_norm / output_norm): one wavefront per row; lane
-//    l adds, in double and in this order, the squares of elements
-//    256*j + 4*l + c (j ascending, c = 0..3), then the 64 lane sums combine
-//    in a fixed xor butterfly (32, 16, ..., 1). The double sum differs from
-//    the sequential one only in its last bits, and the float scale derived
-//    from it is the same unless the two straddle a float rounding boundary
-//    (about 2^-27 of rows). The GEMV kernels that fold this norm into their
-//    input (ikv_model.h) use the same order, so fused and unfused paths agree
-//    bit for bit.
+//    l adds the squares of elements 256*j + 4*l + c (j ascending,
+//    c = 0..3), then the 64 lane sums combine in a xor butterfly
+//    (ikv::rms_scale_strided). The GEMV kernels that fold this norm into
+//    their input (ikv_model.h) use the same scale.
 //
 // Short rows: each workgroup is 4 wavefronts owning up to 16 rows. It issues
 // all of its row loads at once (coalesced, float4 when aligned) together with
 // the positions, norm weights and sin/cos rows of its first RoPE pairs, then
 // stages the rows in LDS (row stride dim+1 floats, so the per-lane row walks
-// are bank-conflict free); lane r sums row r while the RoPE inputs land; then
+// are bank-conflict free); half-wave r sums row r while the RoPE inputs land; then
 // every thread takes elements (or RoPE pairs) of the block in turn, so
 // weights, sin/cos and outputs move coalesced. A block stages all its rows
 // before writing any output, so x == out (in place) is safe.
@@ -65,43 +67,6 @@ int rows_per_block(int dim) {
 }
 
 bool long_row(int64_t dim) { return dim >= kLongRow && dim % 256 == 0; }
-
-// The reference's ordered sum of one row's float squares in double
-// (cpu_backend.cpp:369), reading the row from LDS eight floats ahead of the
-// adds so that the chain of dependent double adds is not broken up by LDS
-// round trips.
-__device__ __forceinline__ double ordered_sq_sum(const float *rp, int dim) {
-  double sum = 0.0;
-  int c = 0;
-  float a[8];
-  if (dim >= 8) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) a[e] = rp[e];
-  }
-  for (; c + 8 <= dim; c += 8) {
-    float b[8];
-    const bool more = c + 16 <= dim;
-    if (more) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) b[e] = rp[c + 8 + e];
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float sq = a[e] * a[e];
-      sum += static_cast<double>(sq);
-    }
-    if (more) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) a[e] = b[e];
-    }
-  }
-  for (; c < dim; ++c) {
-    const float xv = rp[c];
-    const float sq = xv * xv;
-    sum += static_cast<double>(sq);
-  }
-  return sum;
-}
 
 // Short rows (head_dim rows of qk-norm and RoPE, rows shorter than kLongRow).
 // A block of 4 wavefronts owns up to kMaxRows rows. Every load the block needs
@@ -202,10 +167,30 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(const float *__restric
   }
   __syncthreads();
 
-  if (NORM && tid < nr) {
-    const double sum = ordered_sq_sum(&lds[tid * stride], dim);
-    s_scale[tid] =
-        static_cast<float>(1.0 / sqrt(sum / static_cast<double>(dim) + static_cast<double>(eps)));
+  if (NORM) {
+    // Row r's sum by half-wave r % 8 (rows r and r + 8 for 16 rows): lane c
+    // adds the squares of elements c, c + 32, ... in double, a xor butterfly
+    // adds the lanes, and the scale is certified against the reference's
+    // index-order sum; lane 0 sums in index order when it is not certain.
+    // The index-order sum alone is a chain of dim dependent double adds
+    // (about 1.1 us for 128).
+    const int hw = tid >> 5;
+    const int c = tid & 31;
+    for (int r = hw; r < nr; r += kRowThreads / 32) {
+      const float *rp = &lds[r * stride];
+      double part = 0.0;
+      for (int i = c; i < dim; i += 32) {
+        const float xv = rp[i];
+        const float sq = xv * xv;
+        part += static_cast<double>(sq);
+      }
+#pragma unroll
+      for (int o = 16; o > 0; o >>= 1) part += __shfl_xor(part, o, 64);
+      float sc = 0.f;
+      const bool certain =
+          ikv::certified_rms_scale(part, dim, eps, (dim - 1) + (dim + 31) / 32 + 4, sc);
+      if (c == 0) s_scale[r] = certain ? sc : ikv::ordered_rms_scale(rp, dim, eps);
+    }
   }
   __syncthreads();
 

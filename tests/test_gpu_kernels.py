@@ -284,6 +284,52 @@ def test_rms_norm_bit_exact(dev, rows, dim):
     assert np.array_equal(bits(got.cpu().numpy()), bits(oracle.rms_norm(x, w, 1e-6)))
 
 
+def near_midpoint_rows(dim, n, seed, k, eps=1e-6):
+    """Rows (of n seeded candidates) whose RMSNorm scale, as a double, lies
+    closest to a float rounding midpoint: the rows on which a parallel sum of
+    squares cannot be certified and the kernels fall back to the index-order
+    sum. Returns up to k rows and how many fall inside the kernels' window."""
+    x = ikv.synth_normal(seed, (n, dim), threads=8)
+    margins = np.empty(n)
+    for a in range(0, n, 65536):
+        xb = x[a:a + 65536]
+        S = (xb * xb).astype(np.float64).sum(axis=1)
+        t = 1.0 / np.sqrt(S / dim + np.float64(np.float32(eps)))
+        f = t.astype(np.float32)
+        fd = f.astype(np.float64)
+        nb = np.where(t >= fd, np.nextafter(f, np.float32(np.inf)),
+                      np.nextafter(f, np.float32(0))).astype(np.float64)
+        margins[a:a + 65536] = np.abs(0.5 * (fd + nb) - t) / t
+    # the kernels' window for the longest of their sums (lane strides of 32)
+    window = 64 * (0.5 * ((dim - 1) + dim / 32 + 5) + 8) * 2.0 ** -53
+    order = np.argsort(margins)[:k]
+    return np.ascontiguousarray(x[order]), int((margins < window).sum())
+
+
+@pytest.mark.parametrize("dim,n", [(128, 1 << 20), (1024, 1 << 18)])
+def test_rms_norm_rows_near_rounding_midpoints_bit_exact(dev, dim, n):
+    """The parallel sums' certification and its index-order fallback: rows
+    chosen for scales within the kernels' window of a float rounding midpoint
+    still give the reference's float scale bit for bit."""
+    rows, inside = near_midpoint_rows(dim, n, 4242 + dim, 48)
+    assert inside >= 3, "the candidate set should reach the fallback window"
+    w = synth.normal(200 + dim, (dim,))
+    got = ikv.rms_norm(torch.from_numpy(rows).to(dev), torch.from_numpy(w).to(dev), 1e-6)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(got.cpu().numpy()), bits(oracle.rms_norm(rows, w, 1e-6)))
+    if dim == 128:
+        # the fused qk-norm + RoPE (half-wave sums) on the same rows as heads
+        th, s, c = sincos_dev(dev, 64)
+        x = torch.from_numpy(rows.reshape(-1, 8, dim)).to(dev)
+        pos = torch.arange(x.shape[0], dtype=torch.int32, device=dev) % 64
+        wd = torch.from_numpy(w).to(dev)
+        got = ikv.qk_norm_rope(x, wd, pos, 1e-6, s, c)
+        torch.cuda.synchronize()
+        want = oracle.rope_neox(oracle.rms_norm(rows, w, 1e-6).reshape(-1, 8, dim),
+                                pos.cpu().numpy(), th)
+        assert np.array_equal(bits(got.cpu().numpy()), bits(want))
+
+
 def sincos_dev(dev, n_ctx=40960):
     th = oracle.rope_theta_table(1e6, D, n_ctx)
     s, c = ikv.rope_sincos_table(th)

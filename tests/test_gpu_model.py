@@ -346,9 +346,14 @@ def test_staged_swiglu_folded_equals_separate_norm(dev):
     assert np.array_equal(sep.view(np.uint32), fused.view(np.uint32))
 
 
-@pytest.mark.parametrize("Hq,Hkv,ctx", [(16, 8, 0), (16, 8, 37), (16, 8, 4096), (32, 8, 1000),
-                                        (8, 8, 300), (64, 8, 129)])
-def test_decode_with_qk_rope_equals_separate_ops(dev, oracle_pool, Hq, Hkv, ctx):
+@pytest.mark.parametrize("Hq,Hkv,ctx,near", [(16, 8, 0, False), (16, 8, 37, False),
+                                             (16, 8, 4096, False), (32, 8, 1000, False),
+                                             (8, 8, 300, False), (64, 8, 129, False),
+                                             (16, 8, 37, True), (32, 8, 1000, True)])
+def test_decode_with_qk_rope_equals_separate_ops(dev, oracle_pool, Hq, Hkv, ctx, near):
+    """near: q and k rows whose norm scales sit closest to float rounding
+    midpoints, so that the folded prologue's certified sum falls back to the
+    index-order one."""
     import torch
     D = 128
     th = oracle.rope_theta_table(1e6, D, 8192)
@@ -358,6 +363,10 @@ def test_decode_with_qk_rope_equals_separate_ops(dev, oracle_pool, Hq, Hkv, ctx)
     kn_w = 1 + 0.3 * synth.normal(31, (D,))
     q_raw = synth.normal(32 + ctx, (Hq, D)) * 2
     k_raw = synth.normal(33 + ctx, (Hkv, D)) * 2
+    if near:
+        from test_gpu_kernels import near_midpoint_rows
+        rows, _ = near_midpoint_rows(D, 1 << 20, 777 + ctx, Hq + Hkv)
+        q_raw, k_raw = rows[:Hq].copy(), rows[Hq:].copy()
     v_new = synth.normal(34 + ctx, (Hkv, D))
     hist_k = synth.normal(35 + ctx, (ctx + 1, Hkv, D))
     hist_v = synth.normal(36 + ctx, (ctx + 1, Hkv, D))
