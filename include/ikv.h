@@ -135,6 +135,31 @@ int ikv_attn_decode_rope_f32(const float *q_raw, const float *k_raw, const float
                              int *status, void *workspace, size_t workspace_bytes, void *stream);
 
 /* ---------------------------------------------------------------------
+ * The whole attention input side of one Qwen3 layer for one token, in one
+ * launch: the q/k/v projections of x (attn_norm folded in when attn_norm_w is
+ * not NULL, as for ikv_gemv3_f32, include/ikv_model.h) written to q_out
+ * [n_head][head_dim], k_out and v_out [n_head_kv][head_dim], then
+ * ikv_attn_decode_rope_f32 on them (qk-RMSNorm + RoPE at pos[0], append at
+ * row n_kv-1, attention) — the MUL_MAT x3 -> RMS_NORM -> ROPE -> CPY -> VIEW
+ * -> FLASH_ATTN_EXT chain of src/models/Qwen3.cpp:53-88. For short contexts
+ * only (one decode split, n_kv <= 128): -ENOTSUP otherwise, and for n_embd
+ * not a multiple of 1024, and the caller makes the two launches. Outputs and
+ * cache rows are bit-identical to ikv_gemv3_f32 followed by
+ * ikv_attn_decode_rope_f32. w_q [n_head*head_dim][n_embd], w_k and w_v
+ * [n_head_kv*head_dim][n_embd], x [n_embd]; the workspace is a decode
+ * workspace (ikv_attn_decode_workspace_bytes, zero-filled once): its
+ * arrival counters, which every launch leaves at zero again.
+ * ------------------------------------------------------------------- */
+int ikv_qkv_attn_decode_f32(const float *w_q, const float *w_k, const float *w_v, const float *x,
+                            const float *attn_norm_w, float attn_eps, float *q_out, float *k_out,
+                            float *v_out, int64_t n_embd, float *k_cache, float *v_cache,
+                            float *out, int n_head, int n_head_kv, int head_dim, int64_t n_kv,
+                            float scale, const float *q_norm_w, const float *k_norm_w, float eps,
+                            const int32_t *pos, const float *sin_tab, const float *cos_tab,
+                            int64_t n_ctx, int *status, void *workspace, size_t workspace_bytes,
+                            void *stream);
+
+/* ---------------------------------------------------------------------
  * Prefill / general attention, n_q >= 1 query tokens, causal: key j is
  * visible to query t iff j <= n_past + t (src/backends/cpu_backend.cpp:578,
  * src/kernels/cuda/kernel_f32.cu:346). F32 MFMA tiles; K/V tiles staged in

@@ -113,6 +113,7 @@ int ikv_qwen3_generate_interleaved(ikv_qwen3 *m, const int32_t *prompts, int64_t
 typedef struct ikv_qwen3_stats {
     int launches, fused_norm_rope, fused_append_decode, fused_swiglu, fused_residual, fused_qkv,
         fused_norm_mm, fused_rope_decode;
+    int fused_qkv_decode; /* decodes run inside their q/k/v launch (short contexts) */
 } ikv_qwen3_stats;
 int ikv_qwen3_last_stats(const ikv_qwen3 *m, ikv_qwen3_stats *out);
 /* 0 disables the HIP backend's graph fusions (every node its own launch). */

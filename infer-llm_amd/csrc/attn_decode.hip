@@ -43,6 +43,7 @@
 // cache is bit-identical to the one the separate ops produce. The prologue's
 // loads are issued first and the first tile's K/V loads right after them, so
 // the prologue's arithmetic runs while the tile is in flight.
+#include "gemv_dev.hpp"
 #include "ikv_common.hpp"
 #include "../../include/ikv.h"
 
@@ -197,6 +198,11 @@ __device__ __forceinline__ float4 load4_agent(__amdgpu_buffer_rsrc_t r, unsigned
   const f4v v = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kCpolSc1);
   return make_float4(v.x, v.y, v.z, v.w);
 }
+// One float stored by another workgroup of this launch (on any XCD) before
+// it was counted: an agent-coherent load.
+__device__ __forceinline__ float load_agent(const float *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // Loads the K and V rows of tile `base` for this lane: row r of the lane is
 // token base + r*2*NWAVE + 2*wave + half. Rows past the split (t > t_last)
@@ -206,6 +212,11 @@ __device__ __forceinline__ float4 load4_agent(__amdgpu_buffer_rsrc_t r, unsigned
 // token's row comes from k_new / v_new. Token t is read from cache row
 // t + shift (shift = 0 for a contiguous cache; a paged cache's block offset,
 // the same for the whole tile).
+//
+// With COH (k_new / v_new written by other workgroups of the same launch)
+// the new token's row is loaded from the cache like the others (stale, in
+// bounds) and the caller substitutes the new row it loaded coherently.
+template <bool COH = false>
 __device__ __forceinline__ void load_tile(float4 (&kr)[R], float4 (&vr)[R], int base, int t_last,
                                           int wave, int half, int new_row, const float *kc,
                                           const float *vc, const float *k_new, const float *v_new,
@@ -213,7 +224,7 @@ __device__ __forceinline__ void load_tile(float4 (&kr)[R], float4 (&vr)[R], int 
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int t = min(base + r * (NWAVE * 2) + wave * 2 + half, t_last);
-    const bool fresh = (t == new_row);
+    const bool fresh = !COH && (t == new_row);
     const size_t row = static_cast<size_t>(t + shift) * tok_stride + head_off;
     const float *kp = fresh ? k_new + head_off : kc + row;
     const float *vp = fresh ? v_new + head_off : vc + row;
@@ -274,7 +285,7 @@ struct ProStage {
   int spec;
 };
 
-template <int G>
+template <int G, bool COH>
 __device__ __forceinline__ void qk_prologue_load(const Prologue &pro, const float *q, const float *k_new,
                                                  int g, int n_kv, ProStage<G> &st) {
   using S = ProStage<G>;
@@ -285,7 +296,12 @@ __device__ __forceinline__ void qk_prologue_load(const Prologue &pro, const floa
     if (i < S::n_el) {
       const int r = i / D;
       const int d = i - r * D;
-      st.el[u] = r < G ? q[static_cast<size_t>(g * G + r) * D + d] : k_new[static_cast<size_t>(g) * D + d];
+      const float *p = r < G ? q + static_cast<size_t>(g * G + r) * D + d
+                             : k_new + static_cast<size_t>(g) * D + d;
+      if constexpr (COH)
+        st.el[u] = load_agent(p);
+      else
+        st.el[u] = *p;
     }
   }
   st.spec = min(n_kv - 1, static_cast<int>(min(pro.n_ctx, static_cast<int64_t>(INT_MAX))) - 1);
@@ -506,19 +522,22 @@ __device__ __forceinline__ void merge_splits(const float *part_ml, const float *
   }
 }
 
-template <int G, bool PRO, bool PAGED>
-__global__ __launch_bounds__(WG, waves_per_simd(G)) void decode_kernel(
-    const float *__restrict__ q, float *kc, float *vc, const float *k_new, const float *v_new,
+// One workgroup's share of a decode: KV head g, split `split`. COH: q, k_new
+// and v_new were written by other workgroups of the same launch (the folded
+// q/k/v projection) and are read with agent-coherent loads.
+template <int G, bool PRO, bool PAGED, bool COH>
+__device__ __forceinline__ void decode_body(
+    const float *q, float *kc, float *vc, const float *k_new, const float *v_new,
     float *__restrict__ out, int *counters, float *part_ml, float *part_o, int n_head_kv, int n_kv,
-    int tokens_per_split, int n_splits, float scale_log2, Prologue pro, ikv::Pages pages) {
+    int tokens_per_split, int n_splits, float scale_log2, const Prologue &pro,
+    const ikv::Pages &pages, int g, int split) {
+  static_assert(!COH || PRO, "the coherent form is the one with the prologue folded in");
   // Arrays read or written as float4 are declared 16-byte aligned.
   __shared__ __attribute__((aligned(16))) float s_acc[NWAVE][G][D];
   __shared__ float s_m[NWAVE][G];
   __shared__ float s_l[NWAVE][G];
   __shared__ __attribute__((aligned(16))) MergeLds s_merge;
 
-  const int g = blockIdx.x % n_head_kv;
-  const int split = blockIdx.x / n_head_kv;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -544,9 +563,15 @@ __global__ __launch_bounds__(WG, waves_per_simd(G)) void decode_kernel(
   // is scored from the other.
   float4 ka[R], va[R], kb[R], vb[R];
   ProStage<G> st;
-  if constexpr (PRO) qk_prologue_load<G>(pro, q, k_new, g, n_kv, st);
-  load_tile(ka, va, t_begin, t_end - 1, wave, half, new_row, kc, vc, k_new, v_new, tok_stride,
-            head_off, shift_of(t_begin));
+  if constexpr (PRO) qk_prologue_load<G, COH>(pro, q, k_new, g, n_kv, st);
+  // the new token's V piece of this lane, when it cannot be read with the tiles
+  float4 vnew = make_float4(0.f, 0.f, 0.f, 0.f);
+  if constexpr (COH) {
+    const float *p = v_new + head_off;
+    vnew = make_float4(load_agent(p), load_agent(p + 1), load_agent(p + 2), load_agent(p + 3));
+  }
+  load_tile<COH>(ka, va, t_begin, t_end - 1, wave, half, new_row, kc, vc, k_new, v_new, tok_stride,
+                 head_off, shift_of(t_begin));
 
   float4 qv[G];
   float4 knew_rot = make_float4(0.f, 0.f, 0.f, 0.f);  // this lane's piece of rope(norm(k_new))
@@ -575,7 +600,7 @@ __global__ __launch_bounds__(WG, waves_per_simd(G)) void decode_kernel(
   // Scores and accumulates one tile. Branch-free: masked rows are -inf
   // scores, and with the folded RoPE the new token's key is swapped for the
   // rotated one by a select.
-  auto process = [&](float4 (&kr)[R], const float4 (&vr)[R], int base) {
+  auto process = [&](float4 (&kr)[R], float4 (&vr)[R], int base) {
     if constexpr (PRO) {
 #pragma unroll
       for (int r = 0; r < R; ++r) {
@@ -584,6 +609,12 @@ __global__ __launch_bounds__(WG, waves_per_simd(G)) void decode_kernel(
         kr[r].y = fresh ? knew_rot.y : kr[r].y;
         kr[r].z = fresh ? knew_rot.z : kr[r].z;
         kr[r].w = fresh ? knew_rot.w : kr[r].w;
+        if constexpr (COH) {
+          vr[r].x = fresh ? vnew.x : vr[r].x;
+          vr[r].y = fresh ? vnew.y : vr[r].y;
+          vr[r].z = fresh ? vnew.z : vr[r].z;
+          vr[r].w = fresh ? vnew.w : vr[r].w;
+        }
       }
     }
 #pragma unroll
@@ -622,15 +653,15 @@ __global__ __launch_bounds__(WG, waves_per_simd(G)) void decode_kernel(
       process(ka, va, base);
       break;
     }
-    load_tile(kb, vb, base + TILE, t_end - 1, wave, half, new_row, kc, vc, k_new, v_new,
-              tok_stride, head_off, shift_of(base + TILE));
+    load_tile<COH>(kb, vb, base + TILE, t_end - 1, wave, half, new_row, kc, vc, k_new, v_new,
+                   tok_stride, head_off, shift_of(base + TILE));
     process(ka, va, base);
     if (base + 2 * TILE >= t_end) {
       process(kb, vb, base + TILE);
       break;
     }
-    load_tile(ka, va, base + 2 * TILE, t_end - 1, wave, half, new_row, kc, vc, k_new, v_new,
-              tok_stride, head_off, shift_of(base + 2 * TILE));
+    load_tile<COH>(ka, va, base + 2 * TILE, t_end - 1, wave, half, new_row, kc, vc, k_new, v_new,
+                   tok_stride, head_off, shift_of(base + 2 * TILE));
     process(kb, vb, base + TILE);
   }
 
@@ -647,7 +678,10 @@ __global__ __launch_bounds__(WG, waves_per_simd(G)) void decode_kernel(
     else
       kw = *reinterpret_cast<const float4 *>(k_new + head_off);
     *reinterpret_cast<float4 *>(kc + off) = kw;
-    *reinterpret_cast<float4 *>(vc + off) = *reinterpret_cast<const float4 *>(v_new + head_off);
+    if constexpr (COH)
+      *reinterpret_cast<float4 *>(vc + off) = vnew;
+    else
+      *reinterpret_cast<float4 *>(vc + off) = *reinterpret_cast<const float4 *>(v_new + head_off);
   }
 
   // Merge the two half-waves (they saw different tokens).
@@ -716,6 +750,100 @@ __global__ __launch_bounds__(WG, waves_per_simd(G)) void decode_kernel(
   __syncthreads();
   if (!s_last) return;
   merge_splits<G>(part_ml, part_o, out, g, n_splits, s_merge);
+}
+
+template <int G, bool PRO, bool PAGED>
+__global__ __launch_bounds__(WG, waves_per_simd(G)) void decode_kernel(
+    const float *__restrict__ q, float *kc, float *vc, const float *k_new, const float *v_new,
+    float *__restrict__ out, int *counters, float *part_ml, float *part_o, int n_head_kv, int n_kv,
+    int tokens_per_split, int n_splits, float scale_log2, Prologue pro, ikv::Pages pages) {
+  decode_body<G, PRO, PAGED, false>(q, kc, vc, k_new, v_new, out, counters, part_ml, part_o,
+                                    n_head_kv, n_kv, tokens_per_split, n_splits, scale_log2, pro,
+                                    pages, static_cast<int>(blockIdx.x) % n_head_kv,
+                                    static_cast<int>(blockIdx.x) / n_head_kv);
+}
+
+// ---------------------------------------------------------------------------
+// The q/k/v projection of a one-token step with the short-context decode
+// folded in (ikv_qkv_attn_decode_f32). Every workgroup first computes 16 rows
+// of [q | k | v] = [w_q | w_k | w_v] x (with the attn_norm of x folded in),
+// 2 per wave, exactly as the q/k/v product ikv_gemv3_f32 does (the same
+// device code), and stores them agent-coherently. The 16 rows of a workgroup
+// belong to one KV head g (D and the group's G * D q rows are multiples of
+// 16); a per-head arrival counter finds the last of the head's workgroups to
+// finish, and that workgroup runs the head's decode (qk-norm + RoPE + append
+// + attention over n_kv <= 2 * TILE keys, one split) with the decode kernel's
+// device code, reading the head's q, k and v rows back coherently. The
+// outputs are bit-identical to the separate launches; the decode's launch,
+// its ramp and its wait for the projection's last wave are gone.
+constexpr int kQkvRpw = 2;                        // rows per wave
+constexpr int kQkvRowsPerWg = NWAVE * kQkvRpw;    // 16
+static_assert(D % kQkvRowsPerWg == 0, "a workgroup's rows stay within one head");
+
+// Built for 2 waves per SIMD (256 VGPRs): the projection's and the decode's
+// registers together do not fit 128, and one 8-wave workgroup per CU is the
+// launch's occupancy anyway at the widths it serves (Qwen3-0.6B: 256
+// workgroups).
+template <int G>
+__global__ __launch_bounds__(WG, 2) void qkv_attn_kernel(
+    const float *__restrict__ wq, const float *__restrict__ wk, const float *__restrict__ wv,
+    const float *__restrict__ x, const float *attn_norm_w, float attn_eps, float *q_out,
+    float *k_out, float *v_out, int K, float *kc, float *vc, float *out, int *counters,
+    int n_head_kv, int n_kv, int tokens_per_split, float scale_log2, Prologue pro) {
+  const int n0 = n_head_kv * G * D;  // q rows
+  const int n1 = n_head_kv * D;      // k rows, v rows
+  const int lane = threadIdx.x & 63;
+  const int wg_row0 = static_cast<int>(blockIdx.x) * kQkvRowsPerWg;
+  int row0 = wg_row0 + (static_cast<int>(threadIdx.x) >> 6) * kQkvRpw;
+  const float *w;
+  float *o;
+  int g;
+  if (wg_row0 < n0) {
+    w = wq;
+    o = q_out;
+    g = wg_row0 / (G * D);
+  } else if (wg_row0 < n0 + n1) {
+    w = wk;
+    o = k_out;
+    row0 -= n0;
+    g = (wg_row0 - n0) / D;
+  } else {
+    w = wv;
+    o = v_out;
+    row0 -= n0 + n1;
+    g = (wg_row0 - n0 - n1) / D;
+  }
+  const float *rows[kQkvRpw];
+#pragma unroll
+  for (int r = 0; r < kQkvRpw; ++r) rows[r] = w + static_cast<size_t>(row0 + r) * K;
+  float sums[kQkvRpw];
+  ikv::gemv::wave_dots<kQkvRpw>(rows, x, K, sums, attn_norm_w, attn_eps);
+  if (lane < kQkvRpw) {
+    float v = sums[0];
+#pragma unroll
+    for (int r = 1; r < kQkvRpw; ++r)
+      if (lane == r) v = sums[r];
+    store_agent(o + row0 + lane, v);
+  }
+  // Publish: the row stores have completed (vmcnt counts stores) before the
+  // workgroup's arrival is counted.
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __syncthreads();
+  __shared__ int s_last_qkv;
+  if (threadIdx.x == 0) {
+    constexpr int per_head = (G + 2) * D / kQkvRowsPerWg;
+    int *ctr = counters + static_cast<size_t>(g) * kCounterStride;
+    const int before = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last_qkv = (before == per_head - 1);
+    if (s_last_qkv) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!s_last_qkv) return;
+  decode_body<G, true, false, true>(q_out, kc, vc, k_out, v_out, out, counters, nullptr, nullptr,
+                                    n_head_kv, n_kv, tokens_per_split, 1, scale_log2, pro,
+                                    ikv::Pages{}, g, 0);
 }
 
 bool supported_group(int G) { return G == 1 || G == 2 || G == 4 || G == 8; }
@@ -886,6 +1014,61 @@ extern "C" int ikv_attn_decode_rope_paged_f32(
   return decode_rope_common(q_raw, k_raw, v_new, k_pool, v_pool, pages, out, n_head, n_head_kv,
                             head_dim, n_kv, scale, q_norm_w, k_norm_w, eps, pos, sin_tab, cos_tab,
                             n_ctx, status, workspace, workspace_bytes, stream);
+}
+
+extern "C" int ikv_qkv_attn_decode_f32(
+    const float *w_q, const float *w_k, const float *w_v, const float *x, const float *attn_norm_w,
+    float attn_eps, float *q_out, float *k_out, float *v_out, int64_t n_embd, float *k_cache,
+    float *v_cache, float *out, int n_head, int n_head_kv, int head_dim, int64_t n_kv, float scale,
+    const float *q_norm_w, const float *k_norm_w, float eps, const int32_t *pos,
+    const float *sin_tab, const float *cos_tab, int64_t n_ctx, int *status, void *workspace,
+    size_t workspace_bytes, void *stream) {
+  if (const int rc = shape_status(n_head, n_head_kv, head_dim, n_kv)) return rc;
+  if (n_embd <= 0 || n_embd > INT_MAX) return -EINVAL;
+  // one split: the short contexts this launch is for; longer ones take the
+  // projection and the split decode as two launches
+  const Plan p = plan_for(n_head, n_head_kv, n_kv);
+  if (p.n_splits != 1 || n_embd % ikv::gemv::kBatchCols != 0) return -ENOTSUP;
+  if (!w_q || !w_k || !w_v || !x || !q_out || !k_out || !v_out || !k_cache || !v_cache || !out ||
+      !q_norm_w || !k_norm_w || !pos || !sin_tab || !cos_tab || n_ctx <= 0 || !workspace)
+    return -EINVAL;
+  if (!ikv::aligned16(w_q) || !ikv::aligned16(w_k) || !ikv::aligned16(w_v) || !ikv::aligned16(x) ||
+      !ikv::aligned16(k_cache) || !ikv::aligned16(v_cache) || !ikv::aligned16(out) ||
+      !ikv::aligned16(q_out) || !ikv::aligned16(k_out) || !ikv::aligned16(v_out) ||
+      (attn_norm_w && !ikv::aligned16(attn_norm_w)) || !ikv::aligned16(workspace))
+    return -EINVAL;
+  // the arrival counters, at the start of a decode workspace
+  if (workspace_bytes < ws_layout(n_head, n_head_kv, 1).part_ml) return -EINVAL;
+  Prologue pro;
+  pro.q_norm_w = q_norm_w;
+  pro.k_norm_w = k_norm_w;
+  pro.eps = eps;
+  pro.pos = pos;
+  pro.sin_tab = sin_tab;
+  pro.cos_tab = cos_tab;
+  pro.n_ctx = n_ctx;
+  pro.status = status;
+  if (!(scale > 0.0f)) scale = 1.0f / sqrtf(static_cast<float>(head_dim));
+  const float sl2 = scale * ikv::kLog2e;
+  const int G = n_head / n_head_kv;
+  const int total_rows = (G + 2) * n_head_kv * D;
+  const unsigned grid = static_cast<unsigned>(total_rows / kQkvRowsPerWg);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int *counters = static_cast<int *>(workspace);
+  const int K = static_cast<int>(n_embd);
+  const int nk = static_cast<int>(n_kv);
+#define IKV_QKV_ATTN(GG)                                                                          \
+  qkv_attn_kernel<GG><<<grid, WG, 0, s>>>(w_q, w_k, w_v, x, attn_norm_w, attn_eps, q_out, k_out,   \
+                                          v_out, K, k_cache, v_cache, out, counters, n_head_kv,   \
+                                          nk, p.tokens_per_split, sl2, pro)
+  switch (G) {
+    case 1: IKV_QKV_ATTN(1); break;
+    case 2: IKV_QKV_ATTN(2); break;
+    case 4: IKV_QKV_ATTN(4); break;
+    default: IKV_QKV_ATTN(8); break;
+  }
+#undef IKV_QKV_ATTN
+  return ikv::launch_status();
 }
 
 // ---------------------------------------------------------------------------

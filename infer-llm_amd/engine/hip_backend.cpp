@@ -383,6 +383,8 @@ infer::expected<void, std::error_code> HIPBackend::compute(Graph &graph) {
   _qkv.clear();
   _norm_into_mm.clear();
   _rope_into_attn.clear();
+  _qkv_attn.clear();
+  _attn_done.clear();
   _skip.clear();
 
   if (_fusion) {
@@ -565,6 +567,89 @@ void HIPBackend::plan_model_fusions(Graph &graph, std::unordered_map<const Tenso
     _rope_into_attn[attn] = {qr, kr};
     _skip[qr] = _skip[kr] = true;
   }
+  // A q/k/v group whose three outputs are exactly that decode's q, k and v
+  // inputs (contiguous cache): the decode may run inside the q/k/v launch.
+  for (const auto &[attn, ropes] : _rope_into_attn) {
+    const Tensor *k = attn->src[1], *v = attn->src[2];
+    if (!k || !v || is_paged(k) || is_paged(v)) continue;
+    const Tensor *qsrc = _norm_into_rope[ropes.first]->src[0];
+    const Tensor *ksrc = _norm_into_rope[ropes.second]->src[0];
+    const Tensor *vsrc = _append_into_attn[attn].second;
+    for (const auto &[first, group] : _qkv) {
+      if (group[0]->data == qsrc->data && group[1]->data == ksrc->data &&
+          group[2]->data == vsrc->data) {
+        _qkv_attn[first] = attn;
+        break;
+      }
+    }
+  }
+}
+
+infer::expected<HIPBackend::DecodeRopeArgs, std::error_code> HIPBackend::decode_rope_args(
+    const Tensor *attn) {
+  const auto rf = _rope_into_attn.find(attn);
+  const auto ap = _append_into_attn.find(attn);
+  if (rf == _rope_into_attn.end() || ap == _append_into_attn.end())
+    return infer::fail(std::errc::invalid_argument);
+  const Tensor *qr = rf->second.first, *kr = rf->second.second;
+  const Tensor *qn = _norm_into_rope[qr], *kn = _norm_into_rope[kr];
+  const Tensor *pos = qr->src[1];
+  if (!pos || !pos->data || pos->dataType != GGML_TYPE_I32 || !qr->src[2])
+    return infer::fail(std::errc::invalid_argument);
+  auto tab = rope_tables(*qr->src[2]);
+  if (!tab) return infer::unexpected(tab.error());
+  DecodeRopeArgs a;
+  a.q_raw = static_cast<const float *>(qn->src[0]->data);
+  a.k_raw = static_cast<const float *>(kn->src[0]->data);
+  a.v_new = static_cast<const float *>(ap->second.second->data);
+  a.q_norm_w = static_cast<const float *>(qn->src[1]->data);
+  a.k_norm_w = static_cast<const float *>(kn->src[1]->data);
+  std::memcpy(&a.eps, &qn->op_params[0], sizeof(a.eps));
+  a.pos = static_cast<const int32_t *>(pos->data);
+  a.tab = *tab;
+  return a;
+}
+
+infer::expected<void, std::error_code> HIPBackend::dispatch_qkv_decode(const Tensor *first,
+                                                                       const Tensor *attn) {
+  const auto g = _qkv.find(first);
+  if (g == _qkv.end()) return infer::fail(std::errc::invalid_argument);
+  const Tensor *a = g->second[0], *b = g->second[1], *c = g->second[2];
+  const Tensor *q = attn->src[0], *k = attn->src[1], *v = attn->src[2];
+  AttnParams p;
+  std::memcpy(&p, attn->op_params, sizeof(p));
+  const int64_t D = q->dims[0], Hq = q->dims[1], nkv = k->dims[2], Hkv = k->dims[1];
+  if (q->dims[2] != 1 || nkv != static_cast<int64_t>(p.n_ctx) + 1 || !attn->data)
+    return infer::fail(std::errc::not_supported);
+  const Tensor *xin = first->src[1], *nw = nullptr;
+  float attn_eps = 0.f;
+  if (const auto f = _norm_into_mm.find(first); f != _norm_into_mm.end()) {
+    xin = f->second->src[0];
+    nw = f->second->src[1];
+    std::memcpy(&attn_eps, &f->second->op_params[0], sizeof(attn_eps));
+  }
+  auto args = decode_rope_args(attn);
+  if (!args) return infer::unexpected(args.error());
+  const size_t need = ikv_attn_decode_workspace_bytes(int(Hq), int(Hkv), int(D), nkv);
+  if (auto r = ensure_workspace(need); !r) return r;
+  const int rc = ikv_qkv_attn_decode_f32(
+      static_cast<const float *>(a->src[0]->data), static_cast<const float *>(b->src[0]->data),
+      static_cast<const float *>(c->src[0]->data), static_cast<const float *>(xin->data),
+      nw ? static_cast<const float *>(nw->data) : nullptr, attn_eps, static_cast<float *>(a->data),
+      static_cast<float *>(b->data), static_cast<float *>(c->data), first->src[0]->dims[0],
+      static_cast<float *>(k->data), static_cast<float *>(v->data),
+      static_cast<float *>(attn->data), int(Hq), int(Hkv), int(D), nkv, p.scale,
+      args->q_norm_w, args->k_norm_w, args->eps, args->pos, args->tab->sin, args->tab->cos,
+      args->tab->n_ctx, _status, _workspace, _workspace_bytes, _stream);
+  if (rc == -ENOTSUP) return infer::fail(std::errc::not_supported);
+  if (auto r = check_ikv(rc, "qkv_attn_decode"); !r) return r;
+  _attn_done[attn] = true;
+  ++_stats.fused_qkv;
+  ++_stats.fused_qkv_decode;
+  ++_stats.fused_rope_decode;
+  ++_stats.fused_append_decode;
+  if (nw) ++_stats.fused_norm_mm;
+  return {};
 }
 
 infer::expected<void, std::error_code> HIPBackend::dispatch(Tensor *node) {
@@ -659,6 +744,7 @@ infer::expected<void, std::error_code> HIPBackend::dispatch(Tensor *node) {
       if (k->dims[0] != D || v->dims[0] != D || v->dims[1] != Hkv || v->dims[2] != nkv || Hkv <= 0 ||
           Hq % Hkv != 0)
         return infer::fail(std::errc::invalid_argument);
+      if (_attn_done.count(node)) return {};  // ran inside its q/k/v launch
       ++_stats.launches;
       if (nq == 1 && nkv == static_cast<int64_t>(p.n_ctx) + 1) {
         const auto fused = _append_into_attn.find(node);
@@ -672,39 +758,25 @@ infer::expected<void, std::error_code> HIPBackend::dispatch(Tensor *node) {
         if (auto r = ensure_workspace(need); !r) return r;
         const bool paged = is_paged(k) && is_paged(v);
         const ikv_kv_pages pg = paged ? pages_of(k, _status) : ikv_kv_pages{};
-        if (const auto rf = _rope_into_attn.find(node); rf != _rope_into_attn.end()) {
-          const Tensor *qr = rf->second.first, *kr = rf->second.second;
-          const Tensor *qn = _norm_into_rope[qr], *kn = _norm_into_rope[kr];
-          const Tensor *pos = qr->src[1];
-          if (!pos || !pos->data || pos->dataType != GGML_TYPE_I32 || !qr->src[2])
-            return infer::fail(std::errc::invalid_argument);
-          auto tab = rope_tables(*qr->src[2]);
-          if (!tab) return infer::unexpected(tab.error());
-          float eps;
-          std::memcpy(&eps, &qn->op_params[0], sizeof(eps));
+        if (_rope_into_attn.count(node)) {
+          auto a = decode_rope_args(node);
+          if (!a) return infer::unexpected(a.error());
+          const RopeTables *tab = a->tab;
           ++_stats.fused_rope_decode;
           if (paged)
             return check_ikv(ikv_attn_decode_rope_paged_f32(
-                                 static_cast<const float *>(qn->src[0]->data),
-                                 static_cast<const float *>(kn->src[0]->data),
-                                 static_cast<const float *>(vn), static_cast<float *>(k->data),
+                                 a->q_raw, a->k_raw, a->v_new, static_cast<float *>(k->data),
                                  static_cast<float *>(v->data), &pg, static_cast<float *>(node->data),
-                                 int(Hq), int(Hkv), int(D), nkv, p.scale,
-                                 static_cast<const float *>(qn->src[1]->data),
-                                 static_cast<const float *>(kn->src[1]->data), eps,
-                                 static_cast<const int32_t *>(pos->data), (*tab)->sin, (*tab)->cos,
-                                 (*tab)->n_ctx, _status, _workspace, _workspace_bytes, s),
+                                 int(Hq), int(Hkv), int(D), nkv, p.scale, a->q_norm_w, a->k_norm_w,
+                                 a->eps, a->pos, tab->sin, tab->cos, tab->n_ctx, _status, _workspace,
+                                 _workspace_bytes, s),
                              "attn_decode_rope_paged");
           return check_ikv(ikv_attn_decode_rope_f32(
-                               static_cast<const float *>(qn->src[0]->data),
-                               static_cast<const float *>(kn->src[0]->data),
-                               static_cast<const float *>(vn), static_cast<float *>(k->data),
+                               a->q_raw, a->k_raw, a->v_new, static_cast<float *>(k->data),
                                static_cast<float *>(v->data), static_cast<float *>(node->data),
-                               int(Hq), int(Hkv), int(D), nkv, p.scale,
-                               static_cast<const float *>(qn->src[1]->data),
-                               static_cast<const float *>(kn->src[1]->data), eps,
-                               static_cast<const int32_t *>(pos->data), (*tab)->sin, (*tab)->cos,
-                               (*tab)->n_ctx, _status, _workspace, _workspace_bytes, s),
+                               int(Hq), int(Hkv), int(D), nkv, p.scale, a->q_norm_w, a->k_norm_w,
+                               a->eps, a->pos, tab->sin, tab->cos, tab->n_ctx, _status, _workspace,
+                               _workspace_bytes, s),
                            "attn_decode_rope");
         }
         if (paged)
@@ -758,6 +830,11 @@ infer::expected<void, std::error_code> HIPBackend::dispatch(Tensor *node) {
       const Tensor *w = node->src[0], *x = node->src[1];
       ++_stats.launches;
       if (const auto g = _qkv.find(node); g != _qkv.end()) {
+        if (const auto qa = _qkv_attn.find(node); qa != _qkv_attn.end()) {
+          auto r = dispatch_qkv_decode(node, qa->second);
+          if (r) return r;
+          if (r.error() != std::make_error_code(std::errc::not_supported)) return r;
+        }
         const Tensor *a = g->second[0], *b = g->second[1], *c = g->second[2];
         const Tensor *xin = x, *nw = nullptr;
         float eps = 0.f;

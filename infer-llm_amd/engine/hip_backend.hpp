@@ -73,6 +73,7 @@ class HIPBackend : public Backend {
     int fused_qkv = 0;
     int fused_norm_mm = 0;      // RMSNorm folded into q/k/v or SwiGLU
     int fused_rope_decode = 0;  // qk-norm + RoPE folded into the decode launch
+    int fused_qkv_decode = 0;   // short-context decode folded into the q/k/v launch
   };
   const Stats &last_stats() const { return _stats; }
 
@@ -86,6 +87,17 @@ class HIPBackend : public Backend {
   infer::expected<const RopeTables *, std::error_code> rope_tables(const Tensor &theta);
   infer::expected<void, std::error_code> ensure_workspace(size_t bytes);
   infer::expected<void, std::error_code> dispatch(Tensor *node);
+  // The arguments of a one-token decode with qk-norm + RoPE folded in.
+  struct DecodeRopeArgs {
+    const float *q_raw, *k_raw, *v_new, *q_norm_w, *k_norm_w;
+    float eps;
+    const int32_t *pos;
+    const RopeTables *tab;
+  };
+  infer::expected<DecodeRopeArgs, std::error_code> decode_rope_args(const Tensor *attn);
+  // The q/k/v group `first` with its layer's decode folded in, when the
+  // context allows (else not_supported and nothing was launched).
+  infer::expected<void, std::error_code> dispatch_qkv_decode(const Tensor *first, const Tensor *attn);
   void plan_model_fusions(Graph &graph, std::unordered_map<const Tensor *, int> &uses);
   infer::expected<void, std::error_code> set_device() const;
 
@@ -107,6 +119,8 @@ class HIPBackend : public Backend {
   std::unordered_map<const Tensor *, std::array<const Tensor *, 3>> _qkv;  // first mm -> group
   std::unordered_map<const Tensor *, const Tensor *> _norm_into_mm;  // qkv first mm / swiglu mul -> norm
   std::unordered_map<const Tensor *, std::pair<const Tensor *, const Tensor *>> _rope_into_attn;  // attn -> q, k rope
+  std::unordered_map<const Tensor *, const Tensor *> _qkv_attn;  // qkv first mm -> the decode it feeds
+  std::unordered_map<const Tensor *, bool> _attn_done;           // decodes run by a q/k/v launch
   std::unordered_map<const Tensor *, bool> _skip;
 };
 

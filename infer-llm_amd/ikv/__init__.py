@@ -58,6 +58,13 @@ SIGNATURES = {
          _c_int64, _c_float, _c_void_p, _c_void_p, _c_float, _c_void_p, _c_void_p, _c_void_p,
          _c_int64, _c_void_p, _c_void_p, _c_size_t, _c_void_p],
     ),
+    "ikv_qkv_attn_decode_f32": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_float, _c_void_p, _c_void_p,
+         _c_void_p, _c_int64, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int64,
+         _c_float, _c_void_p, _c_void_p, _c_float, _c_void_p, _c_void_p, _c_void_p, _c_int64,
+         _c_void_p, _c_void_p, _c_size_t, _c_void_p],
+    ),
     "ikv_attn_prefill_f32": (
         _c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int,
@@ -298,6 +305,39 @@ def attn_decode_noalloc(q, k_cache, v_cache, n_kv: int, *, out, k_new=None, v_ne
         n_head, n_head_kv, D, n_kv, scale, _stream(stream))
     _check("ikv_attn_decode_noalloc_f32", rc)
     return out
+
+
+def qkv_attn_decode(w_q, w_k, w_v, x, k_cache, v_cache, n_kv: int, q_norm_w, k_norm_w,
+                    eps: float, pos, sin_tab, cos_tab, *, attn_norm_w=None, attn_eps: float = 0.0,
+                    q_out=None, k_out=None, v_out=None, out=None, scale: float = 0.0, status=None,
+                    workspace=None, stream=None):
+    """One token's q/k/v projections (attn_norm folded in when attn_norm_w is
+    given) and its decode (qk-norm + RoPE + append + attention) in one launch,
+    for contexts of one decode split. Returns (out, q_out, k_out, v_out)."""
+    torch = _torch()
+    n_embd = x.numel()
+    D = k_cache.shape[-1]
+    n_head_kv = k_cache.shape[-2]
+    n_head = w_q.shape[0] // D
+    dev = x.device
+    if q_out is None:
+        q_out = torch.empty((n_head, D), dtype=torch.float32, device=dev)
+    if k_out is None:
+        k_out = torch.empty((n_head_kv, D), dtype=torch.float32, device=dev)
+    if v_out is None:
+        v_out = torch.empty((n_head_kv, D), dtype=torch.float32, device=dev)
+    if out is None:
+        out = torch.empty((n_head, D), dtype=torch.float32, device=dev)
+    if workspace is None:
+        workspace = decode_workspace(n_head, n_head_kv, D, n_kv, device=dev)
+    rc = load().ikv_qkv_attn_decode_f32(
+        _ptr(w_q), _ptr(w_k), _ptr(w_v), _ptr(x), _ptr(attn_norm_w), attn_eps, _ptr(q_out),
+        _ptr(k_out), _ptr(v_out), n_embd, _ptr(k_cache), _ptr(v_cache), _ptr(out), n_head,
+        n_head_kv, D, n_kv, scale, _ptr(q_norm_w), _ptr(k_norm_w), eps, _ptr(pos), _ptr(sin_tab),
+        _ptr(cos_tab), sin_tab.shape[0], _ptr(status), _ptr(workspace), workspace.numel() * 4,
+        _stream(stream))
+    _check("ikv_qkv_attn_decode_f32", rc)
+    return out, q_out, k_out, v_out
 
 
 def attn_decode_rope(q_raw, k_raw, v_new, k_cache, v_cache, n_kv: int, q_norm_w, k_norm_w,

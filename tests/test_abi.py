@@ -91,6 +91,23 @@ def test_noalloc_decode_rejects_shapes_before_touching_a_device():
                 assert ikv.decode_workspace_bytes(hkv * G, hkv, 128, n_kv) <= ikv.NOALLOC_SCRATCH_BYTES
 
 
+def test_qkv_attn_rejects_bad_arguments_without_launching():
+    P = 64
+
+    def call(n_head=16, n_head_kv=8, head_dim=128, n_kv=100, n_embd=1024, ptr=P, ws=P):
+        return _rc("ikv_qkv_attn_decode_f32", ptr, P, P, P, None, 0.0, P, P, P, n_embd, P, P, P,
+                   n_head, n_head_kv, head_dim, n_kv, 0.0, P, P, 1e-6, P, P, P, 10, None, ws,
+                   1 << 20, None)
+
+    assert call(n_kv=129) == -errno.ENOTSUP          # more than one decode split
+    assert call(n_embd=1000) == -errno.ENOTSUP       # not a multiple of 1024
+    assert call(ptr=None) == -errno.EINVAL
+    assert call(ws=None) == -errno.EINVAL
+    assert call(n_head=24) == -errno.ENOTSUP
+    assert call(head_dim=64) == -errno.ENOTSUP
+    assert call(n_kv=0) == -errno.EINVAL
+
+
 def test_prefill_and_rows_reject_bad_arguments():
     P = 64
     assert _rc("ikv_attn_prefill_f32", P, P, P, P, 16, 8, 128, 0, 10, 0, 0.0, None) == 0  # n_q=0

@@ -6,6 +6,8 @@ Bars: gathers, adds, products and the sampler bit-exact; projections within
 dropped or misplaced term is ~1/K of that sum, above the bar for K <= 4096);
 silu within 1e-6 relative; the model: identical greedy token streams.
 """
+import errno
+
 import numpy as np
 import pytest
 
@@ -207,14 +209,15 @@ def test_small_model_greedy_tokens_match_oracle(dev, oracle_pool):
     stats = eng.last_stats()
     ref = oracle.Qwen3Oracle(SMALL, w, 128).generate(prompt, 48)
     assert toks == ref
-    # a decode step took every fusion: per layer attn_norm + q/k/v, qk-norm +
-    # RoPE + append + decode, o_proj + residual, ffn_norm + SwiGLU, down +
-    # residual: 5 launches per layer
+    # a decode step took every fusion: per layer attn_norm + q/k/v with the
+    # qk-norm + RoPE + append + decode folded in (a short context), o_proj +
+    # residual, ffn_norm + SwiGLU, down + residual: 4 launches per layer
     L = SMALL.n_layer
     assert stats["fused_rope_decode"] == L and stats["fused_append_decode"] == L
     assert stats["fused_qkv"] == L and stats["fused_swiglu"] == L and stats["fused_residual"] == 2 * L
     assert stats["fused_norm_mm"] == 2 * L and stats["fused_norm_rope"] == 0
-    assert stats["launches"] == 5 * L + 3  # + embedding, final norm, logits
+    assert stats["fused_qkv_decode"] == L
+    assert stats["launches"] == 4 * L + 3  # + embedding, final norm, logits
     assert t.ttft_s > 0 and t.tpot_s > 0
     # unfused graph (every node its own kernel) gives the same tokens
     eng.set_fusion(False)
@@ -391,6 +394,59 @@ def test_decode_with_qk_rope_equals_separate_ops(dev, oracle_pool, Hq, Hkv, ctx,
     assert np.array_equal(host(kc2).view(np.uint32), hk.view(np.uint32))
     got = host(out2).astype(np.float64)
     assert np.all(np.abs(got - want) <= 1e-5 + 1e-4 * np.abs(want))
+
+
+@pytest.mark.parametrize("Hq,Hkv,K,n_kv,norm", [(16, 8, 1024, 1, True), (16, 8, 1024, 33, True),
+                                               (16, 8, 1024, 64, True), (16, 8, 1024, 65, False),
+                                               (16, 8, 1024, 128, True), (32, 8, 2048, 100, True),
+                                               (8, 8, 1024, 77, True), (64, 8, 1024, 50, True)])
+def test_qkv_attn_folded_equals_separate_launches(dev, oracle_pool, Hq, Hkv, K, n_kv, norm):
+    """ikv_qkv_attn_decode_f32 (q/k/v projection with the short-context decode
+    folded in) against ikv_gemv3_f32 followed by ikv_attn_decode_rope_f32:
+    the projections, the output and both caches bit for bit, twice in a row
+    (the arrival counters must come back to zero)."""
+    import torch
+    D = 128
+    th = oracle.rope_theta_table(1e6, D, 4096)
+    s, c = ikv.rope_sincos_table(th)
+    sd, cd = dev_t(s, dev), dev_t(c, dev)
+    seed = 600 + Hq + n_kv + K
+    wq = dev_t(synth.normal(seed, (Hq * D, K), 0.02), dev)
+    wk = dev_t(synth.normal(seed + 1, (Hkv * D, K), 0.02), dev)
+    wv = dev_t(synth.normal(seed + 2, (Hkv * D, K), 0.02), dev)
+    x = dev_t(synth.normal(seed + 3, (K,)), dev)
+    an = dev_t(1 + 0.2 * synth.normal(seed + 4, (K,)), dev) if norm else None
+    qn_w = dev_t(1 + 0.3 * synth.normal(seed + 5, (D,)), dev)
+    kn_w = dev_t(1 + 0.3 * synth.normal(seed + 6, (D,)), dev)
+    hist_k = synth.normal(seed + 7, (n_kv, Hkv, D))
+    hist_v = synth.normal(seed + 8, (n_kv, Hkv, D))
+    pos = torch.tensor([n_kv - 1], dtype=torch.int32, device=dev)
+    ws = ikv.decode_workspace(Hq, Hkv, D, n_kv, device=dev)
+    for rep in range(2):
+        q, k, v = ikv.gemv3(wq, wk, wv, x, norm_w=an, eps=1e-6)
+        kc1, vc1 = dev_t(hist_k, dev), dev_t(hist_v, dev)
+        out1 = ikv.attn_decode_rope(q.view(Hq, D), k.view(Hkv, D), v.view(Hkv, D), kc1, vc1, n_kv,
+                                    qn_w, kn_w, 1e-6, pos, sd, cd, workspace=ws)
+        kc2, vc2 = dev_t(hist_k, dev), dev_t(hist_v, dev)
+        out2, q2, k2, v2 = ikv.qkv_attn_decode(wq, wk, wv, x, kc2, vc2, n_kv, qn_w, kn_w, 1e-6, pos,
+                                               sd, cd, attn_norm_w=an, attn_eps=1e-6, workspace=ws)
+        for a, b, what in ((q, q2, "q"), (k, k2, "k"), (v, v2, "v"), (out1, out2, "out"),
+                           (kc1, kc2, "K cache"), (vc1, vc2, "V cache")):
+            assert np.array_equal(host(a).reshape(-1).view(np.uint32),
+                                  host(b).reshape(-1).view(np.uint32)), f"rep {rep}: {what}"
+    assert not host(ws)[:Hkv * 64].any()  # every arrival counter back at zero
+
+
+def test_qkv_attn_rejects_long_contexts(dev):
+    import torch
+    D = 128
+    t = torch.zeros(1 << 20, device=dev)
+    with pytest.raises(ikv.IkvError) as e:
+        ikv.qkv_attn_decode(t.view(-1, 1024)[:2048], t.view(-1, 1024)[:1024], t.view(-1, 1024)[:1024],
+                            t[:1024], t.view(-1, 8, D)[:200], t.view(-1, 8, D)[:200], 129, t[:D],
+                            t[:D], 1e-6, torch.zeros(1, dtype=torch.int32, device=dev),
+                            t.view(-1, 64)[:10], t.view(-1, 64)[:10])
+    assert e.value.rc == -errno.ENOTSUP
 
 
 def test_decode_with_qk_rope_bad_position_is_flagged(dev):
