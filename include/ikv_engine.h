@@ -114,6 +114,7 @@ typedef struct ikv_qwen3_stats {
     int launches, fused_norm_rope, fused_append_decode, fused_swiglu, fused_residual, fused_qkv,
         fused_norm_mm, fused_rope_decode;
     int fused_qkv_decode; /* decodes run inside their q/k/v launch (short contexts) */
+    int fused_append;     /* cache appends written by their producer (prefill K and V) */
 } ikv_qwen3_stats;
 int ikv_qwen3_last_stats(const ikv_qwen3 *m, ikv_qwen3_stats *out);
 /* 0 disables the HIP backend's graph fusions (every node its own launch). */

@@ -157,7 +157,7 @@ extern "C" int ikv_qwen3_last_stats(const ikv_qwen3 *m, ikv_qwen3_stats *out) {
   const auto &s = static_cast<const HIPBackend *>(m->backend.get())->last_stats();
   *out = {s.launches,       s.fused_norm_rope, s.fused_append_decode, s.fused_swiglu,
           s.fused_residual, s.fused_qkv,       s.fused_norm_mm,       s.fused_rope_decode,
-          s.fused_qkv_decode};
+          s.fused_qkv_decode, s.fused_append};
   return 0;
 }
 

@@ -385,6 +385,7 @@ infer::expected<void, std::error_code> HIPBackend::compute(Graph &graph) {
   _rope_into_attn.clear();
   _qkv_attn.clear();
   _attn_done.clear();
+  _out_into_cpy.clear();
   _skip.clear();
 
   if (_fusion) {
@@ -583,6 +584,26 @@ void HIPBackend::plan_model_fusions(Graph &graph, std::unordered_map<const Tenso
       }
     }
   }
+  // A cache append (CPY into a contiguous cache view) whose source is a RoPE
+  // output or a product, through aliasing reshapes, and read by nothing else:
+  // the producer writes the cache rows itself (src/model.cpp:602-625's CPY
+  // folded into the k RoPE and the v projection of a prefill).
+  for (Tensor *c : graph.nodes()) {
+    if (c->op != OperationType::GGML_OP_CPY || _skip.count(c) || is_paged(c) || !c->is_contiguous())
+      continue;
+    const Tensor *p = c->src[0];
+    bool sole = p && uses[p] == 1;
+    while (sole && p->op == OperationType::GGML_OP_RESHAPE && p->src[0] && p->data == p->src[0]->data) {
+      p = p->src[0];
+      sole = uses[p] == 1;
+    }
+    if (!sole || _skip.count(p) || p->byte_size() != c->byte_size() || !p->is_contiguous()) continue;
+    const bool rope = p->op == OperationType::GGML_OP_ROPE;
+    const bool plain_mm = is_mm(p) && !_qkv.count(p) && mm_operands_ok(p);
+    if (!rope && !plain_mm) continue;
+    _out_into_cpy[p] = c;
+    _skip[c] = true;
+  }
 }
 
 infer::expected<HIPBackend::DecodeRopeArgs, std::error_code> HIPBackend::decode_rope_args(
@@ -712,21 +733,24 @@ infer::expected<void, std::error_code> HIPBackend::dispatch(Tensor *node) {
       if (!tab) return infer::unexpected(tab.error());
       const RopeTables &t = **tab;
       ++_stats.launches;
+      float *rope_out = static_cast<float *>(node->data);
+      if (const auto oc = _out_into_cpy.find(node); oc != _out_into_cpy.end()) {
+        rope_out = static_cast<float *>(oc->second->data);
+        ++_stats.fused_append;
+      }
       if (fused != _norm_into_rope.end()) {
         const Tensor *w = fused->second->src[1];
         float eps;
         std::memcpy(&eps, &fused->second->op_params[0], sizeof(eps));
         ++_stats.fused_norm_rope;
         return check_ikv(ikv_qk_norm_rope_f32(static_cast<const float *>(x->data),
-                                              static_cast<const float *>(w->data),
-                                              static_cast<float *>(node->data),
+                                              static_cast<const float *>(w->data), rope_out,
                                               static_cast<const int32_t *>(pos->data), x->dims[2],
                                               static_cast<int>(x->dims[1]), static_cast<int>(x->dims[0]),
                                               eps, t.sin, t.cos, t.n_ctx, _status, s),
                          "qk_norm_rope");
       }
-      return check_ikv(ikv_rope_neox_f32(static_cast<const float *>(x->data),
-                                         static_cast<float *>(node->data),
+      return check_ikv(ikv_rope_neox_f32(static_cast<const float *>(x->data), rope_out,
                                          static_cast<const int32_t *>(pos->data), x->dims[2],
                                          static_cast<int>(x->dims[1]), static_cast<int>(x->dims[0]),
                                          t.sin, t.cos, t.n_ctx, _status, s),
@@ -855,10 +879,14 @@ infer::expected<void, std::error_code> HIPBackend::dispatch(Tensor *node) {
                           nw ? static_cast<const float *>(nw->data) : nullptr, eps, s),
             "gemv3");
       }
+      float *mm_out = static_cast<float *>(node->data);
+      if (const auto oc = _out_into_cpy.find(node); oc != _out_into_cpy.end()) {
+        mm_out = static_cast<float *>(oc->second->data);
+        ++_stats.fused_append;
+      }
       return check_ikv(ikv_mul_mat_f32(static_cast<const float *>(w->data),
-                                       static_cast<const float *>(x->data),
-                                       static_cast<float *>(node->data), w->dims[1], w->dims[0],
-                                       x->dims[1], nullptr, s),
+                                       static_cast<const float *>(x->data), mm_out, w->dims[1],
+                                       w->dims[0], x->dims[1], nullptr, s),
                        "mul_mat");
     }
 

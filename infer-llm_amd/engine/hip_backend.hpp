@@ -74,6 +74,7 @@ class HIPBackend : public Backend {
     int fused_norm_mm = 0;      // RMSNorm folded into q/k/v or SwiGLU
     int fused_rope_decode = 0;  // qk-norm + RoPE folded into the decode launch
     int fused_qkv_decode = 0;   // short-context decode folded into the q/k/v launch
+    int fused_append = 0;       // cache appends written by their producer (prefill K and V)
   };
   const Stats &last_stats() const { return _stats; }
 
@@ -121,6 +122,7 @@ class HIPBackend : public Backend {
   std::unordered_map<const Tensor *, std::pair<const Tensor *, const Tensor *>> _rope_into_attn;  // attn -> q, k rope
   std::unordered_map<const Tensor *, const Tensor *> _qkv_attn;  // qkv first mm -> the decode it feeds
   std::unordered_map<const Tensor *, bool> _attn_done;           // decodes run by a q/k/v launch
+  std::unordered_map<const Tensor *, const Tensor *> _out_into_cpy;  // rope / mul_mat -> the cache copy it writes
   std::unordered_map<const Tensor *, bool> _skip;
 };
 

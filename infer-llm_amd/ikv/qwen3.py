@@ -50,7 +50,7 @@ class Stats(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in ("launches", "fused_norm_rope", "fused_append_decode",
                                             "fused_swiglu", "fused_residual", "fused_qkv",
                                             "fused_norm_mm", "fused_rope_decode",
-                                            "fused_qkv_decode")]
+                                            "fused_qkv_decode", "fused_append")]
 
 
 _P = ctypes.c_void_p

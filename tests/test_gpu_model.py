@@ -225,6 +225,23 @@ def test_small_model_greedy_tokens_match_oracle(dev, oracle_pool):
     eng.close()
 
 
+def test_prefill_appends_are_written_by_their_producers(dev, oracle_pool):
+    """A prefill step writes its K rows from the qk-norm + RoPE launch and its
+    V rows from the v projection straight into the cache: no copy launches,
+    and the tokens (which read those rows back in every later step) stay the
+    oracle's, for a skinny-GEMM prompt (20 tokens) and a library-GEMM one (70)."""
+    cfg = qwen3.Qwen3Config(n_layer=2, n_vocab=4096, n_ctx_train=4096)
+    w = qwen3.synthetic_weights(cfg, synth.config_seed(0, 60), std=0.05)
+    for P in (20, 70):
+        prompt = synth.uniform_ints(synth.config_seed(0, 61 + P), P, cfg.n_vocab)
+        eng = engine_with(cfg, w, P + 16)
+        eng.generate(prompt, 1)  # the prefill step alone
+        st = eng.last_stats()
+        assert st["fused_append"] == 2 * cfg.n_layer
+        assert eng.generate(prompt, 16)[0] == oracle.Qwen3Oracle(cfg, w, P + 16).generate(prompt, 16)
+        eng.close()
+
+
 @pytest.mark.parametrize("n_head,n_head_kv,prompt_len,n_gen", [(32, 8, 70, 64), (8, 8, 20, 40)])
 def test_other_group_sizes_greedy_tokens_match_oracle(dev, oracle_pool, n_head, n_head_kv,
                                                       prompt_len, n_gen):
