@@ -192,19 +192,33 @@ def prefill_inputs(torch, ikv, p):
 
 
 def time_prefill(torch, ikv, p, reps):
+    """Seconds per prefill launch: `reps` launches captured in one HIP graph
+    and replayed (a Python launch loop is host-bound below ~10 us a launch)."""
     q, k, v = prefill_inputs(torch, ikv, p)
     out = torch.empty_like(q)
-    for _ in range(3):
-        ikv.attn_prefill(q, k, v, 0, out=out)
+
+    def launches():
+        for _ in range(reps):
+            ikv.attn_prefill(q, k, v, 0, out=out)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        launches()  # warm (and load the kernels) outside the capture
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        launches()
+    g.replay()
     torch.cuda.synchronize()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record()
-    for _ in range(reps):
-        ikv.attn_prefill(q, k, v, 0, out=out)
+    for _ in range(5):
+        g.replay()
     e1.record()
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / 1e3 / reps
+    return e0.elapsed_time(e1) / 1e3 / (5 * reps)
 
 
 def prefill_only(torch, ikv, p, reps):

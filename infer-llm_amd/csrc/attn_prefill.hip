@@ -80,7 +80,7 @@ __device__ __forceinline__ float row_sum4(float x) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-template <int G, int NW, bool PAGED>
+template <int G, int NW, int NG, bool PAGED>
 __global__ __launch_bounds__(NW * 64) void prefill_kernel(const float *__restrict__ q,
                                                           const float *__restrict__ k,
                                                           const float *__restrict__ v,
@@ -88,10 +88,13 @@ __global__ __launch_bounds__(NW * 64) void prefill_kernel(const float *__restric
                                                           int n_q, int n_kv, int n_past,
                                                           int n_blocks, int paired,
                                                           float scale_log2, ikv::Pages pages) {
-  // NW = 8: two groups of 4 waves hold the same query rows and take
+  // NG = 2: two groups of NW / 2 waves hold the same query rows and take
   // alternate key tiles (group r: tiles r, r + 2, ...), merging their softmax
-  // states at the end, so that each SIMD runs two waves.
-  constexpr int NG = NW == 8 ? 2 : 1;  // wave groups
+  // states at the end: with 8 waves so that each SIMD runs two, with 2 so
+  // that a short prompt's longest causal rows take half the serial MFMA
+  // steps.
+  static_assert(NG == 1 || NG == 2, "one or two wave groups");
+  static_assert(NW % NG == 0, "whole groups");
   constexpr int WPG = NW / NG;         // waves per group
   constexpr int BQ = WPG * 16 / G;
   // [group][buffer][K | V]; K rows hold 16-byte chunk c at slot c ^ (key & 15)
@@ -325,18 +328,18 @@ __global__ __launch_bounds__(NW * 64) void prefill_kernel(const float *__restric
   }
 }
 
-template <int G, int NW>
+template <int G, int NW, int NG>
 void launch_nw(const float *q, const float *k, const float *v, float *out, int n_head_kv, int n_q,
                int n_kv, int n_past, float scale_log2, int paired, const ikv::Pages *pg,
                hipStream_t s) {
-  constexpr int BQ = (NW == 8 ? 4 : NW) * 16 / G;
+  constexpr int BQ = (NW / NG) * 16 / G;
   const int n_blocks = (n_q + BQ - 1) / BQ;
   const int items = paired ? (n_blocks + 1) / 2 : n_blocks;
   if (pg)
-    prefill_kernel<G, NW, true><<<n_head_kv * items, NW * 64, 0, s>>>(
+    prefill_kernel<G, NW, NG, true><<<n_head_kv * items, NW * 64, 0, s>>>(
         q, k, v, out, n_head_kv, n_q, n_kv, n_past, n_blocks, paired, scale_log2, *pg);
   else
-    prefill_kernel<G, NW, false><<<n_head_kv * items, NW * 64, 0, s>>>(
+    prefill_kernel<G, NW, NG, false><<<n_head_kv * items, NW * 64, 0, s>>>(
         q, k, v, out, n_head_kv, n_q, n_kv, n_past, n_blocks, paired, scale_log2, ikv::Pages{});
 }
 
@@ -349,6 +352,13 @@ void launch(const float *q, const float *k, const float *v, float *out, int n_he
             int n_kv, int n_past, float scale_log2, const ikv::Pages *pg, hipStream_t s) {
   int nw = IKV_PREFILL_NW;
   auto blocks = [&](int w) { return (n_q + w * 16 / G - 1) / (w * 16 / G); };
+  // Short prompts: one 16-row block per workgroup, its key tiles split
+  // between two one-wave groups, when that still fits one workgroup per CU
+  // (its two double buffers take 128 KB of LDS).
+  if (nw == 0 && IKV_PREFILL_SPLIT && blocks(1) * n_head_kv <= kCUs) {
+    launch_nw<G, 2, 2>(q, k, v, out, n_head_kv, n_q, n_kv, n_past, scale_log2, 0, pg, s);
+    return;
+  }
   if (nw == 0) nw = blocks(4) * n_head_kv >= IKV_PREFILL_PAIR_MIN_WGS ? 4 : 2;
   const int nb = blocks(nw);
   const int paired = (nb >= 2 && (nb + 1) / 2 * n_head_kv >= IKV_PREFILL_PAIR_MIN_WGS) ? 1 : 0;
@@ -356,11 +366,11 @@ void launch(const float *q, const float *k, const float *v, float *out, int n_he
   // give every block a second wave group instead (NW = 8).
   if (nw == 4 && IKV_PREFILL_SPLIT && n_head_kv * (paired ? (nb + 1) / 2 : nb) <= kCUs) nw = 8;
   if (nw == 8)
-    launch_nw<G, 8>(q, k, v, out, n_head_kv, n_q, n_kv, n_past, scale_log2, paired, pg, s);
+    launch_nw<G, 8, 2>(q, k, v, out, n_head_kv, n_q, n_kv, n_past, scale_log2, paired, pg, s);
   else if (nw == 4)
-    launch_nw<G, 4>(q, k, v, out, n_head_kv, n_q, n_kv, n_past, scale_log2, paired, pg, s);
+    launch_nw<G, 4, 1>(q, k, v, out, n_head_kv, n_q, n_kv, n_past, scale_log2, paired, pg, s);
   else
-    launch_nw<G, 2>(q, k, v, out, n_head_kv, n_q, n_kv, n_past, scale_log2, paired, pg, s);
+    launch_nw<G, 2, 1>(q, k, v, out, n_head_kv, n_q, n_kv, n_past, scale_log2, paired, pg, s);
 }
 
 }  // namespace
