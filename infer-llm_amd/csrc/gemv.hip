@@ -28,12 +28,16 @@
 #include <climits>
 #include <mutex>
 
+#include "gemm.hpp"
 #include "gemv_dev.hpp"
 #include "ikv_common.hpp"
 #include "../../include/ikv_model.h"
 
 namespace {
 
+#ifndef IKV_GEMM_OWN
+#define IKV_GEMM_OWN 1  // m >= 2048: this library's MFMA product (gemm.hip), else rocBLAS
+#endif
 #ifndef IKV_GEMV_WAVES
 #define IKV_GEMV_WAVES 4
 #endif
@@ -454,6 +458,11 @@ extern "C" int ikv_mul_mat_f32(const float *w, const float *x, float *out, int64
                                                                   int(k), int(m), n_tiles);
     return ikv::launch_status();
   }
+#if IKV_GEMM_OWN
+  if (m >= ikv::kGemmMinTokens && ikv::gemm_nt_supported(n_out, k, m) && ikv::aligned16(w) &&
+      ikv::aligned16(x))
+    return ikv::gemm_nt_f32(w, x, out, residual, n_out, k, m, s);
+#endif
   rocblas_handle h = blas_handle();
   if (!h) return static_cast<int>(hipErrorNotInitialized);
   if (rocblas_set_stream(h, s) != rocblas_status_success) return static_cast<int>(hipErrorUnknown);

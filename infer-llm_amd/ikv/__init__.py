@@ -105,6 +105,8 @@ SIGNATURES = {
     # include/ikv_model.h
     "ikv_mul_mat_f32": (
         _c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int64, _c_int64, _c_int64, _c_void_p, _c_void_p]),
+    "ikv_gemm_nt_f32": (
+        _c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int64, _c_int64, _c_int64, _c_void_p, _c_void_p]),
     "ikv_gemv3_f32": (
         _c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
@@ -553,6 +555,23 @@ def mul_mat(w, x, out=None, residual=None, stream=None):
     if out is None:
         out = torch.empty((m, n_out) if x.dim() > 1 else (n_out,), device=x.device)
     _check("ikv_mul_mat_f32", load().ikv_mul_mat_f32(_ptr(w), _ptr(x), _ptr(out), n_out, k, m,
+                                                      _ptr(residual), _stream(stream)))
+    return out
+
+
+def gemm_nt(w, x, out=None, residual=None, stream=None):
+    """The MFMA GEMM of mul_mat for any number of tokens: out[m, n] =
+    x[m, :] . w[n, :] (+ residual); n_out % 64 == 0 and k % 64 == 0."""
+    torch = _torch()
+    _need_f32_dev("w", w)
+    _need_f32_dev("x", x)
+    n_out, k = w.shape
+    m = x.numel() // k
+    if x.numel() != m * k:
+        raise ValueError("x length must be a multiple of k")
+    if out is None:
+        out = torch.empty((m, n_out), device=x.device)
+    _check("ikv_gemm_nt_f32", load().ikv_gemm_nt_f32(_ptr(w), _ptr(x), _ptr(out), n_out, k, m,
                                                       _ptr(residual), _stream(stream)))
     return out
 

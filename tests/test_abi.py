@@ -108,6 +108,23 @@ def test_qkv_attn_rejects_bad_arguments_without_launching():
     assert call(n_kv=0) == -errno.EINVAL
 
 
+def test_gemm_rejects_bad_arguments_without_launching():
+    P, U = 64, 68  # 16-byte aligned, unaligned addresses
+
+    def call(n_out=128, k=128, m=100, w=P, x=P, out=P):
+        return _rc("ikv_gemm_nt_f32", w, x, out, n_out, k, m, None, None)
+
+    assert call(n_out=100) == -errno.ENOTSUP      # n_out % 64
+    assert call(k=96) == -errno.ENOTSUP           # k % 64
+    assert call(k=0) == -errno.ENOTSUP
+    assert call(w=U) == -errno.EINVAL             # unaligned weights
+    assert call(x=U) == -errno.EINVAL
+    assert call(out=None) == -errno.EINVAL
+    assert call(m=-1) == -errno.EINVAL
+    assert call(m=0) == 0 and call(n_out=0) == 0  # nothing to do
+    assert call(m=2**40) == -errno.EOVERFLOW
+
+
 def test_prefill_and_rows_reject_bad_arguments():
     P = 64
     assert _rc("ikv_attn_prefill_f32", P, P, P, P, 16, 8, 128, 0, 10, 0, 0.0, None) == 0  # n_q=0

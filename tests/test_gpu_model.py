@@ -48,7 +48,9 @@ def test_gemv_matches_oracle(dev, oracle_pool, n_out, k):
 
 
 @pytest.mark.parametrize("n_out,k,m", [(2048, 1024, 37), (1024, 3072, 5), (300, 200, 2), (3072, 1024, 64),
-                                        (16, 256, 2), (4096, 4096, 17), (1024, 2048, 65)])
+                                        (16, 256, 2), (4096, 4096, 17), (1024, 2048, 65),
+                                        (2048, 1024, 300), (3072, 1024, 2048), (1024, 3072, 129),
+                                        (4096, 4096, 100), (192, 64, 70), (300, 200, 100)])
 def test_mul_mat_multi_token_matches_oracle(dev, oracle_pool, n_out, k, m):
     w = synth.normal(300 + m, (n_out, k), 0.02)
     x = synth.normal(400 + m, (m, k))
@@ -68,6 +70,52 @@ def test_mul_mat_few_tokens_residual_in_place(dev, oracle_pool):
     buf = dev_t(r, dev)
     ikv.mul_mat(dev_t(w, dev), dev_t(x, dev), out=buf, residual=buf)
     assert proj_close(host(buf), w, x, oracle.mul_mat(w, x).astype(np.float64) + r)
+
+
+def test_mul_mat_many_tokens_residual_in_place(dev, oracle_pool):
+    # out = out + W x for 200 tokens (rocBLAS with beta = 1) and 2048 (the
+    # MFMA GEMM of prefill projections)
+    for m in (200, 2048):
+        _many_tokens_residual_in_place(dev, m)
+
+
+def _many_tokens_residual_in_place(dev, m):
+    n_out, k = 1024, 2048
+    w = synth.normal(620, (n_out, k), 0.02)
+    x = synth.normal(621, (m, k))
+    r = synth.normal(622, (m, n_out))
+    buf = dev_t(r, dev)
+    ikv.mul_mat(dev_t(w, dev), dev_t(x, dev), out=buf, residual=buf)
+    assert proj_close(host(buf), w, x, oracle.mul_mat(w, x).astype(np.float64) + r)
+
+
+@pytest.mark.parametrize("n_out,k,m", [
+    (128, 64, 1), (192, 128, 65), (1024, 256, 200), (256, 2048, 129),  # 64 x 64 tiles, ragged m
+    (8192, 64, 2048), (8192, 128, 2047), (8192, 64, 2100),             # 128 x 128 tiles (>= 4 rounds)
+    (3072, 1024, 2048),                                               # a Qwen3-0.6B prefill shape
+])
+def test_gemm_matches_oracle(dev, oracle_pool, n_out, k, m):
+    # the MFMA GEMM through its own entry, at token counts below the mul_mat
+    # threshold too; both tile shapes and tokens past the last whole tile
+    w = synth.normal(700 + m, (n_out, k), 0.02)
+    x = synth.normal(701 + m, (m, k))
+    r = synth.normal(702 + m, (m, n_out))
+    ref = oracle.mul_mat(w, x)
+    got = host(ikv.gemm_nt(dev_t(w, dev), dev_t(x, dev)))
+    assert proj_close(got, w, x, ref)
+    buf = dev_t(r, dev)
+    ikv.gemm_nt(dev_t(w, dev), dev_t(x, dev), out=buf, residual=buf)
+    assert proj_close(host(buf), w, x, ref.astype(np.float64) + r)
+
+
+def test_gemm_is_deterministic_and_mul_mat_uses_it(dev):
+    # at 2048 tokens mul_mat runs the GEMM: same bits as the direct entry,
+    # and the same bits on every call
+    w = dev_t(synth.normal(710, (1024, 1024), 0.02), dev)
+    x = dev_t(synth.normal(711, (2048, 1024)), dev)
+    a = host(ikv.gemm_nt(w, x))
+    assert np.array_equal(a, host(ikv.gemm_nt(w, x)))
+    assert np.array_equal(a, host(ikv.mul_mat(w, x)))
 
 
 def test_gemv_residual_in_place(dev, oracle_pool):
