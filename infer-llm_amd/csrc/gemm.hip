@@ -312,13 +312,13 @@ int gemm_nt_f32(const float *w, const float *x, float *out, const float *residua
   if (!gemm_nt_supported(n_out, k, m)) return -ENOTSUP;
   if (!aligned16(w) || !aligned16(x)) return -EINVAL;
   const int n = static_cast<int>(n_out), kk = static_cast<int>(k), mm = static_cast<int>(m);
-  // 128 x 128 tiles (one workgroup per CU: 128 KB of LDS) when they make at
-  // least four rounds over the CUs; else 64 x 64 (two per CU, which hides
-  // more latency and fills the chip with fewer tokens). Measured on the
-  // Qwen3 projections at 2048 and 4096 tokens: each choice within 1% of the
-  // best of 128x128, 64x128, 128x64 and 64x64.
+  // 128 x 128 tiles (one workgroup per CU: 128 KB of LDS) when they make
+  // whole rounds over the CUs or at least four (a small last round); else
+  // 64 x 64 (two per CU, finer rounds). Measured on the Qwen3 projections
+  // at 1024-4096 tokens: each choice within 2% of the best of 128x128,
+  // 64x128, 128x64 and 64x64.
   const int64_t big_tiles = int64_t((mm + 127) / 128) * (n / 128);
-  if (n % 128 == 0 && big_tiles >= 4 * kCUs)
+  if (n % 128 == 0 && (big_tiles % kCUs == 0 || big_tiles >= 4 * kCUs))
     return launch<4, 4, 2, 2>(w, x, out, residual, n, kk, mm, s);
   return launch<2, 2, 2, 2>(w, x, out, residual, n, kk, mm, s);
 }
