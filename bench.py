@@ -250,6 +250,78 @@ def prefill_only(torch, ikv, p, reps):
                        "frac": round(nbytes / t_app / 1e9 / HBM_PEAK_GBS, 4)}}
 
 
+# The projections of one prefill layer at BASELINE configs 3 and 4 (n_out, k,
+# tokens): q, k/v, o, gate/up, down of Qwen3-0.6B at 2048 prompt tokens and
+# of Qwen3-8B at 4096.
+GEMM_SHAPES = [
+    ("0.6B q", 2048, 1024, 2048), ("0.6B k/v", 1024, 1024, 2048), ("0.6B o", 1024, 2048, 2048),
+    ("0.6B gate/up", 3072, 1024, 2048), ("0.6B down", 1024, 3072, 2048),
+    ("8B q/o", 4096, 4096, 4096), ("8B k/v", 1024, 4096, 4096), ("8B gate/up", 12288, 4096, 4096),
+    ("8B down", 4096, 12288, 4096),
+]
+
+
+def gemm_table(torch, ikv):
+    """ikv.mul_mat (the MFMA GEMM from 2048 tokens on) against torch.mm (the
+    vendor BLAS) at GEMM_SHAPES: each timed as a HIP graph of several
+    launches, best of three alternated rounds, after ~2 s of large products
+    to bring the clocks up (the first product timed cold ran ~10% slow)."""
+    import time
+    dev = torch.device("cuda:0")
+    a = torch.randn(4096, 4096, device=dev)
+    t0 = time.time()
+    while time.time() - t0 < 2.0:
+        for _ in range(20):
+            torch.mm(a, a)
+        torch.cuda.synchronize()
+    del a
+
+    def graph_us(fn, reps):
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(reps):
+                fn()
+        g.replay()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(3):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / (3 * reps)
+
+    rows = {}
+    for name, n, k, m in GEMM_SHAPES:
+        w = torch.randn(n, k, device=dev) * 0.02
+        x = torch.randn(m, k, device=dev)
+        out = torch.empty(m, n, device=dev)
+        ref = torch.empty(m, n, device=dev)
+        reps = 10 if n * k * m < 1e10 else 3
+        ours, blas = [], []
+        for _ in range(3):
+            ours.append(graph_us(lambda: ikv.mul_mat(w, x, out=out), reps))
+            blas.append(graph_us(lambda: torch.mm(x, w.t(), out=ref), reps))
+        o, b = min(ours), min(blas)
+        tf = 2 * n * k * m / o / 1e6
+        rows[name] = {"n_out": n, "k": k, "tokens": m, "us": round(o, 1), "tflops": round(tf, 1),
+                      "mfma_frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4),
+                      "blas_us": round(b, 1), "vs_blas": round(o / b, 3),
+                      "bit_equal_blas": bool(torch.equal(out, ref))}
+        log(f"[bench] gemm {name}: {o:.1f} us ({tf:.1f} TF/s), torch.mm {b:.1f} us, "
+            f"ratio {o / b:.3f}")
+        del w, x, out, ref
+        torch.cuda.empty_cache()
+    return rows
+
+
 def hbm_probes(torch, ikv):
     """What this box sustains, measured in the same run: a long streaming read
     (897 MiB per kernel), a streaming read of one decode layer's size (33.6 MB
@@ -641,6 +713,9 @@ def main():
     ap.add_argument("--prefill-only", type=int, default=0, metavar="P",
                     help="only the prefill attention and the KV append of P prompt tokens "
                          "(BASELINE config 2 shape); prints their JSON (for counter runs)")
+    ap.add_argument("--gemm-only", action="store_true",
+                    help="only the prefill projection GEMMs of configs 3 and 4 against the "
+                         "vendor BLAS; prints their JSON")
     ap.add_argument("--probes-only", action="store_true",
                     help="only the HBM / launch probes; prints their JSON")
     ap.add_argument("--pmc-calibrate", action="store_true",
@@ -677,6 +752,9 @@ def main():
     if args.probes_only:
         print(json.dumps(hbm_probes(torch, ikv)), flush=True)
         return
+    if args.gemm_only:
+        print(json.dumps({"prefill_gemm": gemm_table(torch, ikv)}), flush=True)
+        return
     if args.prefill_only:
         print(json.dumps(prefill_only(torch, ikv, args.prefill_only, args.steps)), flush=True)
         return
@@ -707,7 +785,8 @@ def main():
 
     extra = {"repeats": None, "eager_gbs": None, "ctx_sweep_gbs": {}, "short_ctx_us": {},
              "g4_ctx4096": None, "paged_ctx4096_gbs": {},
-             "mall_hot_gbs": None, "prefill": {}, "hbm_probes": None, "model": None,
+             "mall_hot_gbs": None, "prefill": {}, "prefill_gemm": None, "hbm_probes": None,
+             "model": None,
              "cpu_sweep": None}
     if not args.no_extra:
         # Five more timed regions of the same K steps (no warmup between them):
@@ -770,6 +849,7 @@ def main():
             extra["prefill"][str(p)] = {"us": round(t * 1e6, 2), "tflops": round(tf, 2),
                                         "mfma_frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)}
             log(f"[bench] prefill P={p}: {t * 1e6:.1f} us, {tf:.2f} TFLOP/s")
+        extra["prefill_gemm"] = gemm_table(torch, ikv)
 
     configs = [int(c) for c in args.model_configs.split(",") if c.strip()]
     if configs and not args.no_extra:
