@@ -160,6 +160,43 @@ int ikv_qkv_attn_decode_f32(const float *w_q, const float *w_k, const float *w_v
                             void *stream);
 
 /* ---------------------------------------------------------------------
+ * Replay forms, for a decode step recorded once (a captured HIP graph) and
+ * replayed at successive positions; they have no counterpart in the
+ * reference, whose step is rebuilt and relaunched every token
+ * (src/model.cpp:164-311). The context is not an argument: every launch
+ * reads pos[0] on the device and attends over n_kv = pos[0] + 1 keys,
+ * appending at row pos[0]. The launch is planned for n_kv_max keys (its
+ * grid and workspace); for every n_kv in [n, ikv_attn_decode_replay_limit(
+ * ..., n, width)] a launch planned for that limit gives bit-identical
+ * results to ikv_attn_decode_rope_f32 / ikv_qkv_attn_decode_f32 at n_kv
+ * (it only adds empty splits). pos[0] outside [0, n_kv_max) raises
+ * IKV_STATUS_POSITION in *status and the launch runs as n_kv_max keys
+ * (results invalid, accesses in bounds: the caches must hold n_kv_max
+ * rows). Contiguous caches only.
+ * ------------------------------------------------------------------- */
+int ikv_attn_decode_rope_replay_f32(const float *q_raw, const float *k_raw, const float *v_new,
+                                    float *k_cache, float *v_cache, float *out, int n_head,
+                                    int n_head_kv, int head_dim, int64_t n_kv_max, float scale,
+                                    const float *q_norm_w, const float *k_norm_w, float eps,
+                                    const int32_t *pos, const float *sin_tab,
+                                    const float *cos_tab, int64_t n_ctx, int *status,
+                                    void *workspace, size_t workspace_bytes, void *stream);
+int ikv_qkv_attn_decode_replay_f32(const float *w_q, const float *w_k, const float *w_v,
+                                   const float *x, const float *attn_norm_w, float attn_eps,
+                                   float *q_out, float *k_out, float *v_out, int64_t n_embd,
+                                   float *k_cache, float *v_cache, float *out, int n_head,
+                                   int n_head_kv, int head_dim, int64_t n_kv_max, float scale,
+                                   const float *q_norm_w, const float *k_norm_w, float eps,
+                                   const int32_t *pos, const float *sin_tab, const float *cos_tab,
+                                   int64_t n_ctx, int *status, void *workspace,
+                                   size_t workspace_bytes, void *stream);
+/* The largest m in [n_kv, n_kv + width - 1] such that a replay launch
+ * planned for m keys is bit-identical to the per-context launch at every
+ * context in [n_kv, m]; 0 for a shape the decode rejects or width < 1. */
+int64_t ikv_attn_decode_replay_limit(int n_head, int n_head_kv, int head_dim, int64_t n_kv,
+                                     int64_t width);
+
+/* ---------------------------------------------------------------------
  * Prefill / general attention, n_q >= 1 query tokens, causal: key j is
  * visible to query t iff j <= n_past + t (src/backends/cpu_backend.cpp:578,
  * src/kernels/cuda/kernel_f32.cu:346). F32 MFMA tiles; K/V tiles staged in

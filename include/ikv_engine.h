@@ -115,10 +115,21 @@ typedef struct ikv_qwen3_stats {
         fused_norm_mm, fused_rope_decode;
     int fused_qkv_decode; /* decodes run inside their q/k/v launch (short contexts) */
     int fused_append;     /* cache appends written by their producer (prefill K and V) */
+    /* over the last ikv_qwen3_generate: decode steps captured as a HIP graph,
+     * and decode steps launched from one (captured ones included) */
+    int step_captures, step_replays;
 } ikv_qwen3_stats;
 int ikv_qwen3_last_stats(const ikv_qwen3 *m, ikv_qwen3_stats *out);
 /* 0 disables the HIP backend's graph fusions (every node its own launch). */
 int ikv_qwen3_set_fusion(ikv_qwen3 *m, int on);
+/* 1 (the default): the decode steps of ikv_qwen3_generate are captured as a
+ * HIP graph once per range of contexts the decode's split plan allows (up to
+ * 256 tokens) and replayed, the position advancing on the device, so that a
+ * step costs the host one graph launch and one sampler launch; the tokens are
+ * those of the eager steps. Taken with a contiguous cache and fusions on.
+ * 0: every step is built and launched from the host (the reference's way,
+ * src/model.cpp:164-311). No counterpart in the reference. */
+int ikv_qwen3_set_step_replay(ikv_qwen3 *m, int on);
 
 void ikv_qwen3_destroy(ikv_qwen3 *m);
 

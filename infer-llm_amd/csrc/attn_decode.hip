@@ -108,7 +108,22 @@ struct Prologue {
   const float *sin_tab = nullptr, *cos_tab = nullptr;
   int64_t n_ctx = 0;
   int *status = nullptr;
+  // > 0: a launch recorded once and replayed at successive positions; the
+  // context is pos[0] + 1, read on the device, and the launch was planned
+  // for dyn_max keys (splits past pos[0] + 1 are empty).
+  int dyn_max = 0;
 };
+
+// The context of a launch: n_kv, or with pro.dyn_max, pos[0] + 1. A
+// position outside [0, dyn_max) raises IKV_STATUS_POSITION and runs as
+// dyn_max keys, inside the planned splits.
+__device__ __forceinline__ int launch_n_kv(const Prologue &pro, int n_kv) {
+  if (pro.dyn_max <= 0) return n_kv;
+  const int p = pro.pos[0];
+  if (p >= 0 && p < pro.dyn_max) return p + 1;
+  if (threadIdx.x == 0) ikv::raise_status(pro.status, IKV_STATUS_POSITION);
+  return pro.dyn_max;
+}
 
 #ifndef IKV_DECODE_MIN_SPLIT_TOKENS
 #define IKV_DECODE_MIN_SPLIT_TOKENS 64
@@ -757,6 +772,7 @@ __global__ __launch_bounds__(WG, waves_per_simd(G)) void decode_kernel(
     const float *__restrict__ q, float *kc, float *vc, const float *k_new, const float *v_new,
     float *__restrict__ out, int *counters, float *part_ml, float *part_o, int n_head_kv, int n_kv,
     int tokens_per_split, int n_splits, float scale_log2, Prologue pro, ikv::Pages pages) {
+  if constexpr (PRO) n_kv = launch_n_kv(pro, n_kv);
   decode_body<G, PRO, PAGED, false>(q, kc, vc, k_new, v_new, out, counters, part_ml, part_o,
                                     n_head_kv, n_kv, tokens_per_split, n_splits, scale_log2, pro,
                                     pages, static_cast<int>(blockIdx.x) % n_head_kv,
@@ -842,8 +858,8 @@ __global__ __launch_bounds__(WG, 2) void qkv_attn_kernel(
   __syncthreads();
   if (!s_last_qkv) return;
   decode_body<G, true, false, true>(q_out, kc, vc, k_out, v_out, out, counters, nullptr, nullptr,
-                                    n_head_kv, n_kv, tokens_per_split, 1, scale_log2, pro,
-                                    ikv::Pages{}, g, 0);
+                                    n_head_kv, launch_n_kv(pro, n_kv), tokens_per_split, 1,
+                                    scale_log2, pro, ikv::Pages{}, g, 0);
 }
 
 bool supported_group(int G) { return G == 1 || G == 2 || G == 4 || G == 8; }
@@ -974,7 +990,7 @@ int decode_rope_common(const float *q_raw, const float *k_raw, const float *v_ne
                        const float *q_norm_w, const float *k_norm_w, float eps,
                        const int32_t *pos, const float *sin_tab, const float *cos_tab,
                        int64_t n_ctx, int *status, void *workspace, size_t workspace_bytes,
-                       void *stream) {
+                       void *stream, bool replay = false) {
   if (!k_raw || !v_new || !q_norm_w || !k_norm_w || !pos || !sin_tab || !cos_tab || n_ctx <= 0)
     return -EINVAL;
   Prologue pro;
@@ -986,6 +1002,10 @@ int decode_rope_common(const float *q_raw, const float *k_raw, const float *v_ne
   pro.cos_tab = cos_tab;
   pro.n_ctx = n_ctx;
   pro.status = status;
+  if (replay) {
+    if (n_kv <= 0 || n_kv > INT_MAX - 2 * TILE) return n_kv <= 0 ? -EINVAL : -EOVERFLOW;
+    pro.dyn_max = static_cast<int>(n_kv);
+  }
   return decode_common(q_raw, k_cache, v_cache, k_raw, v_new, out, n_head, n_head_kv, head_dim,
                        n_kv, scale, workspace, workspace_bytes, &pro, pages, stream);
 }
@@ -1016,13 +1036,15 @@ extern "C" int ikv_attn_decode_rope_paged_f32(
                             n_ctx, status, workspace, workspace_bytes, stream);
 }
 
-extern "C" int ikv_qkv_attn_decode_f32(
+namespace {
+
+int qkv_attn_common(
     const float *w_q, const float *w_k, const float *w_v, const float *x, const float *attn_norm_w,
     float attn_eps, float *q_out, float *k_out, float *v_out, int64_t n_embd, float *k_cache,
     float *v_cache, float *out, int n_head, int n_head_kv, int head_dim, int64_t n_kv, float scale,
     const float *q_norm_w, const float *k_norm_w, float eps, const int32_t *pos,
     const float *sin_tab, const float *cos_tab, int64_t n_ctx, int *status, void *workspace,
-    size_t workspace_bytes, void *stream) {
+    size_t workspace_bytes, void *stream, bool replay) {
   if (const int rc = shape_status(n_head, n_head_kv, head_dim, n_kv)) return rc;
   if (n_embd <= 0 || n_embd > INT_MAX) return -EINVAL;
   // one split: the short contexts this launch is for; longer ones take the
@@ -1048,6 +1070,7 @@ extern "C" int ikv_qkv_attn_decode_f32(
   pro.cos_tab = cos_tab;
   pro.n_ctx = n_ctx;
   pro.status = status;
+  if (replay) pro.dyn_max = static_cast<int>(n_kv);
   if (!(scale > 0.0f)) scale = 1.0f / sqrtf(static_cast<float>(head_dim));
   const float sl2 = scale * ikv::kLog2e;
   const int G = n_head / n_head_kv;
@@ -1069,6 +1092,66 @@ extern "C" int ikv_qkv_attn_decode_f32(
   }
 #undef IKV_QKV_ATTN
   return ikv::launch_status();
+}
+
+// Whether launches planned for m keys give, at n keys, the results of the
+// launch planned for n: one split for both, or splits of the same length
+// (the launch for m then only adds empty splits, whose zero weights leave
+// every sum unchanged).
+bool replay_compatible(int n_head, int n_head_kv, int64_t n, int64_t m) {
+  const Plan a = plan_for(n_head, n_head_kv, n), b = plan_for(n_head, n_head_kv, m);
+  if (a.n_splits == 1 || b.n_splits == 1) return a.n_splits == 1 && b.n_splits == 1;
+  return a.tokens_per_split == b.tokens_per_split;
+}
+
+}  // namespace
+
+extern "C" int ikv_qkv_attn_decode_f32(
+    const float *w_q, const float *w_k, const float *w_v, const float *x, const float *attn_norm_w,
+    float attn_eps, float *q_out, float *k_out, float *v_out, int64_t n_embd, float *k_cache,
+    float *v_cache, float *out, int n_head, int n_head_kv, int head_dim, int64_t n_kv, float scale,
+    const float *q_norm_w, const float *k_norm_w, float eps, const int32_t *pos,
+    const float *sin_tab, const float *cos_tab, int64_t n_ctx, int *status, void *workspace,
+    size_t workspace_bytes, void *stream) {
+  return qkv_attn_common(w_q, w_k, w_v, x, attn_norm_w, attn_eps, q_out, k_out, v_out, n_embd,
+                         k_cache, v_cache, out, n_head, n_head_kv, head_dim, n_kv, scale, q_norm_w,
+                         k_norm_w, eps, pos, sin_tab, cos_tab, n_ctx, status, workspace,
+                         workspace_bytes, stream, false);
+}
+
+extern "C" int ikv_qkv_attn_decode_replay_f32(
+    const float *w_q, const float *w_k, const float *w_v, const float *x, const float *attn_norm_w,
+    float attn_eps, float *q_out, float *k_out, float *v_out, int64_t n_embd, float *k_cache,
+    float *v_cache, float *out, int n_head, int n_head_kv, int head_dim, int64_t n_kv_max,
+    float scale, const float *q_norm_w, const float *k_norm_w, float eps, const int32_t *pos,
+    const float *sin_tab, const float *cos_tab, int64_t n_ctx, int *status, void *workspace,
+    size_t workspace_bytes, void *stream) {
+  return qkv_attn_common(w_q, w_k, w_v, x, attn_norm_w, attn_eps, q_out, k_out, v_out, n_embd,
+                         k_cache, v_cache, out, n_head, n_head_kv, head_dim, n_kv_max, scale,
+                         q_norm_w, k_norm_w, eps, pos, sin_tab, cos_tab, n_ctx, status, workspace,
+                         workspace_bytes, stream, true);
+}
+
+extern "C" int ikv_attn_decode_rope_replay_f32(
+    const float *q_raw, const float *k_raw, const float *v_new, float *k_cache, float *v_cache,
+    float *out, int n_head, int n_head_kv, int head_dim, int64_t n_kv_max, float scale,
+    const float *q_norm_w, const float *k_norm_w, float eps, const int32_t *pos,
+    const float *sin_tab, const float *cos_tab, int64_t n_ctx, int *status, void *workspace,
+    size_t workspace_bytes, void *stream) {
+  return decode_rope_common(q_raw, k_raw, v_new, k_cache, v_cache, nullptr, out, n_head,
+                            n_head_kv, head_dim, n_kv_max, scale, q_norm_w, k_norm_w, eps, pos,
+                            sin_tab, cos_tab, n_ctx, status, workspace, workspace_bytes, stream,
+                            true);
+}
+
+extern "C" int64_t ikv_attn_decode_replay_limit(int n_head, int n_head_kv, int head_dim,
+                                                int64_t n_kv, int64_t width) {
+  if (width < 1 || shape_status(n_head, n_head_kv, head_dim, n_kv)) return 0;
+  int64_t m = n_kv;
+  while (m - n_kv + 1 < width && m + 1 <= INT_MAX - 2 * TILE &&
+         replay_compatible(n_head, n_head_kv, n_kv, m + 1))
+    ++m;
+  return m;
 }
 
 // ---------------------------------------------------------------------------

@@ -155,9 +155,16 @@ extern "C" int ikv_qwen3_generate_interleaved(ikv_qwen3 *m, const int32_t *promp
 extern "C" int ikv_qwen3_last_stats(const ikv_qwen3 *m, ikv_qwen3_stats *out) {
   if (!m || !out) return -EINVAL;
   const auto &s = static_cast<const HIPBackend *>(m->backend.get())->last_stats();
+  const Qwen3Runner::ReplayStats rs = m->runner->replay_stats();
   *out = {s.launches,       s.fused_norm_rope, s.fused_append_decode, s.fused_swiglu,
           s.fused_residual, s.fused_qkv,       s.fused_norm_mm,       s.fused_rope_decode,
-          s.fused_qkv_decode, s.fused_append};
+          s.fused_qkv_decode, s.fused_append,  rs.captures,           rs.replays};
+  return 0;
+}
+
+extern "C" int ikv_qwen3_set_step_replay(ikv_qwen3 *m, int on) {
+  if (!m) return -EINVAL;
+  m->runner->set_step_replay(on != 0);
   return 0;
 }
 

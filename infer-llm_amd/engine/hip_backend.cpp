@@ -651,15 +651,17 @@ infer::expected<void, std::error_code> HIPBackend::dispatch_qkv_decode(const Ten
   }
   auto args = decode_rope_args(attn);
   if (!args) return infer::unexpected(args.error());
-  const size_t need = ikv_attn_decode_workspace_bytes(int(Hq), int(Hkv), int(D), nkv);
+  if (_replay_max > 0 && (is_paged(k) || nkv > _replay_max)) return infer::fail(std::errc::not_supported);
+  const int64_t plan_kv = _replay_max > 0 ? _replay_max : nkv;
+  const size_t need = ikv_attn_decode_workspace_bytes(int(Hq), int(Hkv), int(D), plan_kv);
   if (auto r = ensure_workspace(need); !r) return r;
-  const int rc = ikv_qkv_attn_decode_f32(
+  const int rc = (_replay_max > 0 ? ikv_qkv_attn_decode_replay_f32 : ikv_qkv_attn_decode_f32)(
       static_cast<const float *>(a->src[0]->data), static_cast<const float *>(b->src[0]->data),
       static_cast<const float *>(c->src[0]->data), static_cast<const float *>(xin->data),
       nw ? static_cast<const float *>(nw->data) : nullptr, attn_eps, static_cast<float *>(a->data),
       static_cast<float *>(b->data), static_cast<float *>(c->data), first->src[0]->dims[0],
       static_cast<float *>(k->data), static_cast<float *>(v->data),
-      static_cast<float *>(attn->data), int(Hq), int(Hkv), int(D), nkv, p.scale,
+      static_cast<float *>(attn->data), int(Hq), int(Hkv), int(D), plan_kv, p.scale,
       args->q_norm_w, args->k_norm_w, args->eps, args->pos, args->tab->sin, args->tab->cos,
       args->tab->n_ctx, _status, _workspace, _workspace_bytes, _stream);
   if (rc == -ENOTSUP) return infer::fail(std::errc::not_supported);
@@ -778,15 +780,26 @@ infer::expected<void, std::error_code> HIPBackend::dispatch(Tensor *node) {
           vn = fused->second.second->data;
           ++_stats.fused_append_decode;
         }
-        const size_t need = ikv_attn_decode_workspace_bytes(int(Hq), int(Hkv), int(D), nkv);
-        if (auto r = ensure_workspace(need); !r) return r;
         const bool paged = is_paged(k) && is_paged(v);
+        if (_replay_max > 0 && (paged || !_rope_into_attn.count(node) || nkv > _replay_max))
+          return infer::fail(std::errc::not_supported);
+        const int64_t plan_kv = _replay_max > 0 ? _replay_max : nkv;
+        const size_t need = ikv_attn_decode_workspace_bytes(int(Hq), int(Hkv), int(D), plan_kv);
+        if (auto r = ensure_workspace(need); !r) return r;
         const ikv_kv_pages pg = paged ? pages_of(k, _status) : ikv_kv_pages{};
         if (_rope_into_attn.count(node)) {
           auto a = decode_rope_args(node);
           if (!a) return infer::unexpected(a.error());
           const RopeTables *tab = a->tab;
           ++_stats.fused_rope_decode;
+          if (_replay_max > 0)
+            return check_ikv(ikv_attn_decode_rope_replay_f32(
+                                 a->q_raw, a->k_raw, a->v_new, static_cast<float *>(k->data),
+                                 static_cast<float *>(v->data), static_cast<float *>(node->data),
+                                 int(Hq), int(Hkv), int(D), plan_kv, p.scale, a->q_norm_w,
+                                 a->k_norm_w, a->eps, a->pos, tab->sin, tab->cos, tab->n_ctx,
+                                 _status, _workspace, _workspace_bytes, s),
+                             "attn_decode_rope_replay");
           if (paged)
             return check_ikv(ikv_attn_decode_rope_paged_f32(
                                  a->q_raw, a->k_raw, a->v_new, static_cast<float *>(k->data),

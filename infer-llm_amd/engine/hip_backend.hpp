@@ -64,6 +64,13 @@ class HIPBackend : public Backend {
   static size_t decode_workspace_reservation(int n_head, int n_head_kv, int head_dim,
                                              int64_t max_kv);
   void set_fusion(bool on) { _fusion = on; }
+  bool fusion() const { return _fusion; }
+  // n_kv_max > 0: one-token decodes launch in their replay form (the context
+  // read from the position on the device, planned for n_kv_max keys), so
+  // that the step can be captured once and replayed at later positions; 0
+  // restores the per-context launches. Contiguous caches with the qk-norm /
+  // RoPE fusion only (other decodes then fail with not_supported).
+  void set_decode_replay(int64_t n_kv_max) { _replay_max = n_kv_max; }
   struct Stats {
     int launches = 0;
     int fused_norm_rope = 0;
@@ -110,6 +117,7 @@ class HIPBackend : public Backend {
   std::unordered_map<const void *, size_t> _rope;             // angle-table address -> table
   std::unordered_map<std::string, size_t> _rope_by_content;   // dims + row 1 -> table
   bool _fusion = true;
+  int64_t _replay_max = 0;
   Stats _stats;
   // per-compute() fusion plan
   std::unordered_map<const Tensor *, const Tensor *> _norm_into_rope;  // rope -> its rms_norm

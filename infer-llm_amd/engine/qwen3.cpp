@@ -1,7 +1,9 @@
 #include "qwen3.hpp"
 
+#include <algorithm>
 #include <cstring>
 
+#include "../../include/ikv.h"
 #include "../../include/ikv_model.h"
 #include "kvcache/kvstorage.hpp"
 #include "kvcache/kvstrategy.hpp"
@@ -177,6 +179,8 @@ Qwen3Runner::Qwen3Runner(Qwen3Model &model, HIPBackend &backend, size_t capacity
 
 Qwen3Runner::~Qwen3Runner() {
   (void)_backend.synchronize();
+  drop_step_graph();
+  if (_pos_state) (void)hipFree(_pos_state);
   if (_ctx) (void)_ctx->release_kv_access();
   if (_kv && _seq != kInvalidSequenceId) (void)_kv->release_sequence(_seq);
   for (hipEvent_t &e : _ready)
@@ -228,7 +232,8 @@ infer::expected<void, std::error_code> Qwen3Runner::init() {
     (void)hipGetLastError();
     return infer::fail(std::errc::not_enough_memory);
   };
-  if (hipMalloc(&_token_dev, kSlots * sizeof(int32_t)) != hipSuccess) return fail_alloc();
+  if (hipMalloc(&_token_dev, (kSlots + 1) * sizeof(int32_t)) != hipSuccess) return fail_alloc();
+  if (hipMalloc(&_pos_state, sizeof(int32_t)) != hipSuccess) return fail_alloc();
   if (hipMalloc(&_positions_dev, _capacity * sizeof(int32_t)) != hipSuccess) return fail_alloc();
   if (hipMalloc(&_argmax_ws, ikv_argmax_workspace_bytes()) != hipSuccess ||
       hipMemset(_argmax_ws, 0, ikv_argmax_workspace_bytes()) != hipSuccess)
@@ -252,8 +257,10 @@ infer::expected<void, std::error_code> Qwen3Runner::init() {
 infer::expected<void, std::error_code> Qwen3Runner::enqueue_step(const int32_t *host_tokens,
                                                                  int64_t n, int in_slot,
                                                                  int out_slot,
-                                                                 GenerationTiming &timing) {
+                                                                 GenerationTiming &timing,
+                                                                 int host_slot) {
   using Clock = std::chrono::steady_clock;
+  if (host_slot < 0) host_slot = out_slot;
   const auto t0 = Clock::now();
   auto n_past = _kv->length(_seq);
   if (!n_past) return infer::unexpected(n_past.error());
@@ -292,14 +299,132 @@ infer::expected<void, std::error_code> Qwen3Runner::enqueue_step(const int32_t *
   hipStream_t s = _backend.stream();
   // The sampler writes the token to the device slot the next step embeds
   // and to the pinned host slot the host reads once the event has fired.
-  if (ikv_argmax_ws_f32(row, vocab, _token_dev + out_slot, _token_host_dev + out_slot, _argmax_ws,
+  if (ikv_argmax_ws_f32(row, vocab, _token_dev + out_slot, _token_host_dev + host_slot, _argmax_ws,
                         ikv_argmax_workspace_bytes(), s) != 0 ||
-      hipEventRecord(_ready[out_slot], s) != hipSuccess)
+      hipEventRecord(_ready[host_slot], s) != hipSuccess)
     return abort(std::make_error_code(std::errc::io_error));
   // The kernels of this step hold no host-side state: hand the layer
   // accesses back and commit the appended range now.
   if (auto r = _ctx->release_kv_access(); !r) return r;
   if (auto r = _kv->commit_append(_seq); !r) return r;
+  const auto t2 = Clock::now();
+  timing.build_s += std::chrono::duration<double>(t1 - t0).count();
+  timing.execute_s += std::chrono::duration<double>(t2 - t1).count();
+  return {};
+}
+
+// ---------------------------------------------------------------------------
+// replayed decode steps
+
+namespace {
+
+// The position slot of the captured step: set before a capture's first
+// launch, advanced by the step itself (kernels, so that nothing but launches
+// sits in the captured stream).
+__global__ void set_position_kernel(int32_t *p, int32_t v) { *p = v; }
+__global__ void advance_position_kernel(int32_t *p) { *p += 1; }
+
+// Contexts one capture may serve; the decode's replay limit may cut it short
+// where its split plan changes.
+constexpr int64_t kReplayWidth = 256;
+
+}  // namespace
+
+void Qwen3Runner::drop_step_graph() {
+  if (_step_exec) (void)hipGraphExecDestroy(_step_exec);
+  _step_exec = nullptr;
+  _step_lo = _step_hi = 0;
+  _step_logits = nullptr;
+}
+
+// Captures one decode step of _seq at n_past (its host bookkeeping included):
+// the token comes from device slot kReplaySlot, the position from
+// _pos_state, the decode reads its context from that position and is planned
+// for the largest context the capture serves; the step ends by advancing
+// _pos_state. The sampler stays outside: its host slot alternates.
+infer::expected<void, std::error_code> Qwen3Runner::capture_step(int64_t n_past) {
+  const Qwen3Hparams &hp = _model.hparams();
+  const int64_t n_kv = n_past + 1;
+  int64_t hi = ikv_attn_decode_replay_limit(int(hp.n_head), int(hp.n_head_kv), int(hp.head_dim),
+                                            n_kv, kReplayWidth);
+  hi = std::min<int64_t>(hi, int64_t(_capacity));
+  if (hi < n_kv) return infer::fail(std::errc::not_supported);
+  drop_step_graph();
+  hipStream_t s = _backend.stream();
+  set_position_kernel<<<1, 1, 0, s>>>(_pos_state, int32_t(n_past));
+  if (hipGetLastError() != hipSuccess) return infer::fail(std::errc::io_error);
+  if (auto r = _kv->reserve_append(_seq, 1); !r) return r;
+  for (Tensor *t : {_tokens, _pos}) {
+    t->dims = {1, 1, 1, 1};
+    t->set_contiguous_strides();
+  }
+  _tokens->data = _token_dev + kReplaySlot;
+  _tokens->device = DeviceType::HIP;
+  _tokens->backend = &_backend;
+  _pos->data = _pos_state;
+  _pos->device = DeviceType::HIP;
+  _pos->backend = &_backend;
+  if (hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+    (void)hipGetLastError();
+    (void)_kv->abort_append(_seq);
+    return infer::fail(std::errc::not_supported);
+  }
+  _backend.set_decode_replay(hi);
+  auto graph = _model.build_graph(*_ctx);
+  infer::expected<void, std::error_code> r =
+      graph ? _sched->execute(*graph) : infer::expected<void, std::error_code>(infer::unexpected(graph.error()));
+  if (r) {
+    advance_position_kernel<<<1, 1, 0, s>>>(_pos_state);
+    if (hipGetLastError() != hipSuccess) r = infer::fail(std::errc::io_error);
+  }
+  _backend.set_decode_replay(0);
+  hipGraph_t g = nullptr;
+  const bool ended = hipStreamEndCapture(s, &g) == hipSuccess && g;
+  if (r && !ended) r = infer::fail(std::errc::not_supported);
+  if (r && hipGraphInstantiate(&_step_exec, g, nullptr, nullptr, 0) != hipSuccess) {
+    _step_exec = nullptr;
+    r = infer::fail(std::errc::not_supported);
+  }
+  if (g) (void)hipGraphDestroy(g);
+  (void)hipGetLastError();
+  if (!r) {
+    (void)_ctx->release_kv_access();
+    (void)_kv->abort_append(_seq);
+    return r;
+  }
+  const Tensor *logits = graph->outputs().front();
+  _step_vocab = logits->dims[0];
+  _step_logits = static_cast<const float *>(logits->data) + (logits->dims[1] - 1) * _step_vocab;
+  _step_lo = n_kv;
+  _step_hi = hi;
+  if (auto rr = _ctx->release_kv_access(); !rr) return rr;
+  if (auto rr = _kv->commit_append(_seq); !rr) return rr;
+  ++_replay_stats.captures;
+  return {};
+}
+
+infer::expected<void, std::error_code> Qwen3Runner::replay_step(int host_slot,
+                                                                GenerationTiming &timing) {
+  using Clock = std::chrono::steady_clock;
+  const auto t0 = Clock::now();
+  auto n_past = _kv->length(_seq);
+  if (!n_past) return infer::unexpected(n_past.error());
+  const int64_t n_kv = int64_t(*n_past) + 1;
+  if (!_step_exec || n_kv < _step_lo || n_kv > _step_hi) {
+    if (auto r = capture_step(int64_t(*n_past)); !r) return r;
+  } else {
+    if (auto r = _kv->reserve_append(_seq, 1); !r) return r;
+    if (auto r = _kv->commit_append(_seq); !r) return r;
+  }
+  const auto t1 = Clock::now();
+  hipStream_t s = _backend.stream();
+  if (hipGraphLaunch(_step_exec, s) != hipSuccess ||
+      ikv_argmax_ws_f32(_step_logits, _step_vocab, _token_dev + kReplaySlot,
+                        _token_host_dev + host_slot, _argmax_ws, ikv_argmax_workspace_bytes(),
+                        s) != 0 ||
+      hipEventRecord(_ready[host_slot], s) != hipSuccess)
+    return infer::fail(std::errc::io_error);
+  ++_replay_stats.replays;
   const auto t2 = Clock::now();
   timing.build_s += std::chrono::duration<double>(t1 - t0).count();
   timing.execute_s += std::chrono::duration<double>(t2 - t1).count();
@@ -329,6 +454,7 @@ infer::expected<void, std::error_code> Qwen3Runner::generate(const std::vector<i
   tokens_out.clear();
   auto finish = [&](infer::expected<void, std::error_code> r) {
     const auto sync = _backend.synchronize();
+    drop_step_graph();  // its addresses are this sequence's cache rows
     (void)_ctx->release_kv_access();
     (void)_ctx->set_kv_cache(nullptr, kInvalidSequenceId);
     (void)_kv->release_sequence(_seq);
@@ -349,13 +475,34 @@ infer::expected<void, std::error_code> Qwen3Runner::generate(const std::vector<i
     tokens_out.push_back(*tok);
     return {};
   };
-  // step i writes token slot i % 2 and reads slot (i - 1) % 2
-  if (auto r = enqueue_step(prompt.data(), int64_t(prompt.size()), 1, 0, timing); !r)
+  // Step i hands its token to the host in slot i % 2. Eager steps read
+  // device slot (i - 1) % 2 and write slot i % 2; replayed steps, whose
+  // graph holds one address, read and write device slot kReplaySlot.
+  _replay_stats = {};
+  drop_step_graph();
+  bool replay = _replay && _kv_opt.block_tokens == 0 && _kv_opt.offload_bytes == 0 &&
+                _backend.fusion();
+  const bool one_slot = replay;  // the device token stays in kReplaySlot throughout
+  if (auto r = enqueue_step(prompt.data(), int64_t(prompt.size()), 1, one_slot ? kReplaySlot : 0,
+                            timing, 0);
+      !r)
     return finish(r);
   for (size_t i = 1; i < n_gen; ++i) {
-    if (auto r = enqueue_step(nullptr, 1, int((i - 1) & 1), int(i & 1), timing); !r)
-      return finish(r);
-    if (auto r = take(int((i - 1) & 1), i - 1); !r) return finish(r);
+    const int host_slot = int(i & 1);
+    infer::expected<void, std::error_code> r;
+    if (replay) {
+      r = replay_step(host_slot, timing);
+      if (!r && r.error() == std::make_error_code(std::errc::not_supported)) {
+        replay = false;  // this step and the rest launch eagerly
+        drop_step_graph();
+      }
+    }
+    if (!replay) {
+      r = one_slot ? enqueue_step(nullptr, 1, kReplaySlot, kReplaySlot, timing, host_slot)
+                   : enqueue_step(nullptr, 1, int((i - 1) & 1), host_slot, timing);
+    }
+    if (!r) return finish(r);
+    if (auto rr = take(int((i - 1) & 1), i - 1); !rr) return finish(rr);
   }
   if (auto r = take(int((n_gen - 1) & 1), n_gen - 1); !r) return finish(r);
   timing.wall_s = std::chrono::duration<double>(Clock::now() - start).count();

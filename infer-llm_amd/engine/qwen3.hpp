@@ -143,15 +143,33 @@ class Qwen3Runner {
       std::vector<std::vector<int32_t>> &tokens_out, GenerationTiming &timing);
   // Page-in / write-back counts of an offloaded cache (zeros otherwise).
   OffloadStats offload_stats() const;
+  // Decode steps of generate() replayed from a captured HIP graph (default
+  // on). Taken with a contiguous cache and the backend's fusions on; other
+  // configurations, and any step whose capture fails, launch eagerly.
+  void set_step_replay(bool on) { _replay = on; }
+  struct ReplayStats {
+    int captures = 0;  // decode steps captured (each then replayed)
+    int replays = 0;   // decode steps launched as a graph (captured ones included)
+  };
+  // Over the last generate() call.
+  ReplayStats replay_stats() const { return _replay_stats; }
 
  private:
   // Enqueues one step of sequence _seq: its input is the host prompt, or
   // (host_tokens NULL) the token in device slot in_slot; its greedy token
-  // lands in device slot out_slot and, once event out_slot has fired, in
-  // _token_host[out_slot].
+  // lands in device slot out_slot and, once event host_slot (default:
+  // out_slot) has fired, in _token_host[host_slot].
   infer::expected<void, std::error_code> enqueue_step(const int32_t *host_tokens, int64_t n,
                                                       int in_slot, int out_slot,
-                                                      GenerationTiming &timing);
+                                                      GenerationTiming &timing, int host_slot = -1);
+  // One decode step of _seq from the captured graph, captured first when
+  // the context is outside the contexts it serves: the input token is in
+  // device slot kReplaySlot and the sampled token goes there and to host
+  // slot host_slot. not_supported: no graph could be made for this step
+  // (nothing was enqueued; launch it eagerly).
+  infer::expected<void, std::error_code> replay_step(int host_slot, GenerationTiming &timing);
+  infer::expected<void, std::error_code> capture_step(int64_t n_past);
+  void drop_step_graph();
   infer::expected<int32_t, std::error_code> collect(int slot);
 
   Qwen3Model &_model;
@@ -166,10 +184,19 @@ class Qwen3Runner {
   Tensor *_tokens = nullptr, *_pos = nullptr;
   std::vector<int32_t> _input;
   static constexpr int kSlots = 2 * kMaxInterleaved;
-  int32_t *_token_dev = nullptr;    // [kSlots] sampled-token slots, two per sequence
+  static constexpr int kReplaySlot = kSlots;  // the device token slot of replayed steps
+  int32_t *_token_dev = nullptr;    // [kSlots + 1] sampled-token slots, two per sequence
   int32_t *_token_host = nullptr;   // [kSlots] pinned read-back slots
   int32_t *_token_host_dev = nullptr;  // the same slots as the device addresses them
   int32_t *_positions_dev = nullptr;  // [capacity]: 0, 1, 2, ...
   void *_argmax_ws = nullptr;         // the multi-workgroup sampler's workspace (zeroed once)
   hipEvent_t _ready[kSlots] = {};
+  // the captured decode step
+  bool _replay = true;
+  hipGraphExec_t _step_exec = nullptr;
+  int64_t _step_lo = 0, _step_hi = 0;   // the contexts (n_past + 1) it serves
+  const float *_step_logits = nullptr;  // its logits row (in the scheduler's arena)
+  int64_t _step_vocab = 0;
+  int32_t *_pos_state = nullptr;        // device: the position the captured step reads
+  ReplayStats _replay_stats;
 };

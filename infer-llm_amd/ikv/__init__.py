@@ -65,6 +65,20 @@ SIGNATURES = {
          _c_float, _c_void_p, _c_void_p, _c_float, _c_void_p, _c_void_p, _c_void_p, _c_int64,
          _c_void_p, _c_void_p, _c_size_t, _c_void_p],
     ),
+    "ikv_qkv_attn_decode_replay_f32": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_float, _c_void_p, _c_void_p,
+         _c_void_p, _c_int64, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int64,
+         _c_float, _c_void_p, _c_void_p, _c_float, _c_void_p, _c_void_p, _c_void_p, _c_int64,
+         _c_void_p, _c_void_p, _c_size_t, _c_void_p],
+    ),
+    "ikv_attn_decode_rope_replay_f32": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int,
+         _c_int64, _c_float, _c_void_p, _c_void_p, _c_float, _c_void_p, _c_void_p, _c_void_p,
+         _c_int64, _c_void_p, _c_void_p, _c_size_t, _c_void_p],
+    ),
+    "ikv_attn_decode_replay_limit": (_c_int64, [_c_int, _c_int, _c_int, _c_int64, _c_int64]),
     "ikv_attn_prefill_f32": (
         _c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_int,
@@ -231,6 +245,10 @@ def append(dst_rows, src_rows, stream=None) -> None:
            load().ikv_append_f32(_ptr(dst_rows), _ptr(src_rows), n_rows, row_bytes, _stream(stream)))
 
 
+def decode_replay_limit(n_head: int, n_head_kv: int, head_dim: int, n_kv: int, width: int) -> int:
+    return int(load().ikv_attn_decode_replay_limit(n_head, n_head_kv, head_dim, n_kv, width))
+
+
 def decode_workspace_bytes(n_head: int, n_head_kv: int, head_dim: int, n_kv: int) -> int:
     return int(load().ikv_attn_decode_workspace_bytes(n_head, n_head_kv, head_dim, n_kv))
 
@@ -312,10 +330,12 @@ def attn_decode_noalloc(q, k_cache, v_cache, n_kv: int, *, out, k_new=None, v_ne
 def qkv_attn_decode(w_q, w_k, w_v, x, k_cache, v_cache, n_kv: int, q_norm_w, k_norm_w,
                     eps: float, pos, sin_tab, cos_tab, *, attn_norm_w=None, attn_eps: float = 0.0,
                     q_out=None, k_out=None, v_out=None, out=None, scale: float = 0.0, status=None,
-                    workspace=None, stream=None):
+                    workspace=None, replay=False, stream=None):
     """One token's q/k/v projections (attn_norm folded in when attn_norm_w is
     given) and its decode (qk-norm + RoPE + append + attention) in one launch,
-    for contexts of one decode split. Returns (out, q_out, k_out, v_out)."""
+    for contexts of one decode split. Returns (out, q_out, k_out, v_out).
+    replay=True: the replay form, n_kv is then the planned maximum and the
+    context is pos[0] + 1, read on the device."""
     torch = _torch()
     n_embd = x.numel()
     D = k_cache.shape[-1]
@@ -332,21 +352,24 @@ def qkv_attn_decode(w_q, w_k, w_v, x, k_cache, v_cache, n_kv: int, q_norm_w, k_n
         out = torch.empty((n_head, D), dtype=torch.float32, device=dev)
     if workspace is None:
         workspace = decode_workspace(n_head, n_head_kv, D, n_kv, device=dev)
-    rc = load().ikv_qkv_attn_decode_f32(
+    fn = "ikv_qkv_attn_decode_replay_f32" if replay else "ikv_qkv_attn_decode_f32"
+    rc = getattr(load(), fn)(
         _ptr(w_q), _ptr(w_k), _ptr(w_v), _ptr(x), _ptr(attn_norm_w), attn_eps, _ptr(q_out),
         _ptr(k_out), _ptr(v_out), n_embd, _ptr(k_cache), _ptr(v_cache), _ptr(out), n_head,
         n_head_kv, D, n_kv, scale, _ptr(q_norm_w), _ptr(k_norm_w), eps, _ptr(pos), _ptr(sin_tab),
         _ptr(cos_tab), sin_tab.shape[0], _ptr(status), _ptr(workspace), workspace.numel() * 4,
         _stream(stream))
-    _check("ikv_qkv_attn_decode_f32", rc)
+    _check(fn, rc)
     return out, q_out, k_out, v_out
 
 
 def attn_decode_rope(q_raw, k_raw, v_new, k_cache, v_cache, n_kv: int, q_norm_w, k_norm_w,
                      eps: float, pos, sin_tab, cos_tab, *, out=None, scale: float = 0.0,
-                     status=None, workspace=None, stream=None):
+                     status=None, workspace=None, replay=False, stream=None):
     """Decode with qk-RMSNorm + RoPE folded in: q/k rotated at position pos[0],
-    k (rotated) and v_new appended at row n_kv-1, attention over [0, n_kv)."""
+    k (rotated) and v_new appended at row n_kv-1, attention over [0, n_kv).
+    replay=True: the replay form, n_kv is then the planned maximum and the
+    context is pos[0] + 1, read on the device."""
     torch = _torch()
     n_head, D = q_raw.shape[-2], q_raw.shape[-1]
     n_head_kv = k_cache.shape[-2]
@@ -354,12 +377,13 @@ def attn_decode_rope(q_raw, k_raw, v_new, k_cache, v_cache, n_kv: int, q_norm_w,
         out = torch.empty((n_head, D), dtype=torch.float32, device=q_raw.device)
     if workspace is None:
         workspace = decode_workspace(n_head, n_head_kv, D, n_kv, device=q_raw.device)
-    rc = load().ikv_attn_decode_rope_f32(
+    fn = "ikv_attn_decode_rope_replay_f32" if replay else "ikv_attn_decode_rope_f32"
+    rc = getattr(load(), fn)(
         _ptr(q_raw), _ptr(k_raw), _ptr(v_new), _ptr(k_cache), _ptr(v_cache), _ptr(out), n_head,
         n_head_kv, D, n_kv, scale, _ptr(q_norm_w), _ptr(k_norm_w), eps, _ptr(pos), _ptr(sin_tab),
         _ptr(cos_tab), sin_tab.shape[0], _ptr(status), _ptr(workspace), workspace.numel() * 4,
         _stream(stream))
-    _check("ikv_attn_decode_rope_f32", rc)
+    _check(fn, rc)
     return out
 
 

@@ -50,7 +50,8 @@ class Stats(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in ("launches", "fused_norm_rope", "fused_append_decode",
                                             "fused_swiglu", "fused_residual", "fused_qkv",
                                             "fused_norm_mm", "fused_rope_decode",
-                                            "fused_qkv_decode", "fused_append")]
+                                            "fused_qkv_decode", "fused_append",
+                                            "step_captures", "step_replays")]
 
 
 _P = ctypes.c_void_p
@@ -78,6 +79,7 @@ ENGINE_SIGNATURES = {
                                                       ctypes.c_int64, _P, ctypes.POINTER(Timing)]),
     "ikv_qwen3_last_stats": (ctypes.c_int, [_P, ctypes.POINTER(Stats)]),
     "ikv_qwen3_set_fusion": (ctypes.c_int, [_P, ctypes.c_int]),
+    "ikv_qwen3_set_step_replay": (ctypes.c_int, [_P, ctypes.c_int]),
     "ikv_qwen3_destroy": (None, [_P]),
 }
 
@@ -186,6 +188,11 @@ class Qwen3Engine:
 
     def set_fusion(self, on: bool):
         _check("ikv_qwen3_set_fusion", _lib().ikv_qwen3_set_fusion(self._h, 1 if on else 0))
+
+    def set_step_replay(self, on: bool):
+        """Decode steps replayed from a captured HIP graph (default on)."""
+        _check("ikv_qwen3_set_step_replay",
+               _lib().ikv_qwen3_set_step_replay(self._h, 1 if on else 0))
 
     def generate(self, prompt, n_gen: int):
         """Greedy tokens (list) and Timing for prompt then n_gen tokens."""

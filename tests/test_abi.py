@@ -125,6 +125,35 @@ def test_gemm_rejects_bad_arguments_without_launching():
     assert call(m=2**40) == -errno.EOVERFLOW
 
 
+def test_decode_replay_limit_tracks_the_split_plan():
+    # (host arithmetic) Qwen3-0.6B shape: one split up to 128 keys, then
+    # 64-key splits up to 33 per KV head (2112 keys), then 128-key splits
+    lim = lambda n, w: ikv.decode_replay_limit(16, 8, 128, n, w)
+    assert lim(1, 256) == 128 and lim(33, 256) == 128 and lim(128, 256) == 128
+    assert lim(129, 256) == 384 and lim(129, 1) == 129
+    assert lim(2000, 256) == 2112 and lim(2112, 256) == 2112
+    assert lim(2113, 256) == 2368
+    # the plan the limit promises to keep: per-context workspace sizes grow
+    # with the context and never pass the limit's
+    for n in (129, 1000, 2113, 4000):
+        m = lim(n, 256)
+        need = ikv.decode_workspace_bytes(16, 8, 128, m)
+        assert all(ikv.decode_workspace_bytes(16, 8, 128, x) <= need for x in range(n, m + 1, 37))
+    assert lim(0, 256) == 0 and lim(100, 0) == 0
+    assert ikv.decode_replay_limit(16, 8, 64, 100, 256) == 0  # head_dim the decode rejects
+
+
+def test_replay_entries_reject_bad_arguments():
+    P = 64
+    assert _rc("ikv_attn_decode_rope_replay_f32", P, P, P, P, P, P, 16, 8, 128, 0, 0.0, P, P,
+               1e-6, P, P, P, 10, None, P, 1 << 20, None) == -errno.EINVAL       # n_kv_max 0
+    assert _rc("ikv_attn_decode_rope_replay_f32", P, P, P, P, P, P, 16, 8, 128, 100, 0.0, P, P,
+               1e-6, None, P, P, 10, None, P, 1 << 20, None) == -errno.EINVAL    # no pos
+    assert _rc("ikv_qkv_attn_decode_replay_f32", P, P, P, P, None, 0.0, P, P, P, 1024, P, P, P,
+               16, 8, 128, 129, 0.0, P, P, 1e-6, P, P, P, 10, None, P, 1 << 20,
+               None) == -errno.ENOTSUP                                         # two splits
+
+
 def test_prefill_and_rows_reject_bad_arguments():
     P = 64
     assert _rc("ikv_attn_prefill_f32", P, P, P, P, 16, 8, 128, 0, 10, 0, 0.0, None) == 0  # n_q=0

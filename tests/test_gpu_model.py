@@ -273,6 +273,32 @@ def test_small_model_greedy_tokens_match_oracle(dev, oracle_pool):
     eng.close()
 
 
+def test_decode_steps_replay_a_captured_graph(dev):
+    """Decode steps replayed from a captured HIP graph give the tokens of the
+    eager steps, across the captures the decode's split plan forces: a
+    100-token prompt and 300 tokens are contexts 101..399, captured at 101
+    (one split, the decode folded into the q/k/v launch, to 128), 129
+    (64-key splits, to 384) and 385."""
+    cfg = qwen3.Qwen3Config(n_layer=2, n_vocab=4096, n_ctx_train=4096)
+    w = qwen3.synthetic_weights(cfg, synth.config_seed(0, 70), std=0.05)
+    prompt = synth.uniform_ints(synth.config_seed(0, 71), 100, cfg.n_vocab)
+    eng = engine_with(cfg, w, 400)
+    toks, t = eng.generate(prompt, 300)
+    st = eng.last_stats()
+    assert st["step_replays"] == 299 and st["step_captures"] == 3
+    assert t.tpot_s > 0
+    eng.set_step_replay(False)
+    eager, _ = eng.generate(prompt, 300)
+    assert eng.last_stats()["step_replays"] == 0
+    assert toks == eager
+    # a second sequence on the same engine captures afresh (the graph holds
+    # the first sequence's cache rows)
+    eng.set_step_replay(True)
+    assert eng.generate(prompt, 40)[0] == eager[:40]
+    assert eng.last_stats()["step_captures"] == 2
+    eng.close()
+
+
 def test_prefill_appends_are_written_by_their_producers(dev, oracle_pool):
     """A prefill step writes its K rows from the qk-norm + RoPE launch and its
     V rows from the v projection straight into the cache: no copy launches,
@@ -500,6 +526,76 @@ def test_qkv_attn_folded_equals_separate_launches(dev, oracle_pool, Hq, Hkv, K, 
             assert np.array_equal(host(a).reshape(-1).view(np.uint32),
                                   host(b).reshape(-1).view(np.uint32)), f"rep {rep}: {what}"
     assert not host(ws)[:Hkv * 64].any()  # every arrival counter back at zero
+
+
+@pytest.mark.parametrize("Hq,n_kv_lo,width", [(16, 33, 256), (16, 129, 256), (16, 2050, 256),
+                                               (16, 2113, 128), (32, 300, 200)])
+def test_decode_replay_equals_per_context_launches(dev, Hq, n_kv_lo, width):
+    """The replay forms (context read from pos on the device, launch planned
+    for the replay limit) against the per-context launches at contexts
+    across the limit's range: outputs and appended cache rows bit for bit.
+    One replay launch object is reused, as a captured graph would be."""
+    import torch
+    Hkv, D, K = 8, 128, 1024
+    m = ikv.decode_replay_limit(Hq, Hkv, D, n_kv_lo, width)
+    assert n_kv_lo <= m < n_kv_lo + width
+    th = oracle.rope_theta_table(1e6, D, m + 8)
+    s, c = ikv.rope_sincos_table(th)
+    sd, cd = dev_t(s, dev), dev_t(c, dev)
+    seed = 900 + n_kv_lo + Hq
+    qn_w = dev_t(1 + 0.3 * synth.normal(seed, (D,)), dev)
+    kn_w = dev_t(1 + 0.3 * synth.normal(seed + 1, (D,)), dev)
+    hist_k = synth.normal(seed + 2, (m, Hkv, D))
+    hist_v = synth.normal(seed + 3, (m, Hkv, D))
+    ws_r = ikv.decode_workspace(Hq, Hkv, D, m, device=dev)
+    pos = torch.zeros(1, dtype=torch.int32, device=dev)
+    fold = m <= 128  # the q/k/v launch takes the decode in
+    if fold:
+        wq = dev_t(synth.normal(seed + 4, (Hq * D, K), 0.02), dev)
+        wk = dev_t(synth.normal(seed + 5, (Hkv * D, K), 0.02), dev)
+        wv = dev_t(synth.normal(seed + 6, (Hkv * D, K), 0.02), dev)
+        an = dev_t(1 + 0.2 * synth.normal(seed + 7, (K,)), dev)
+    for n_kv in sorted({n_kv_lo, (n_kv_lo + m) // 2, m}):
+        pos.fill_(n_kv - 1)
+        g = seed + 10 * n_kv
+        kc1, vc1 = dev_t(hist_k, dev), dev_t(hist_v, dev)
+        kc2, vc2 = dev_t(hist_k, dev), dev_t(hist_v, dev)
+        ws1 = ikv.decode_workspace(Hq, Hkv, D, n_kv, device=dev)
+        if fold:
+            x = dev_t(synth.normal(g, (K,)), dev)
+            out1, *_ = ikv.qkv_attn_decode(wq, wk, wv, x, kc1, vc1, n_kv, qn_w, kn_w, 1e-6, pos, sd,
+                                           cd, attn_norm_w=an, attn_eps=1e-6, workspace=ws1)
+            out2, *_ = ikv.qkv_attn_decode(wq, wk, wv, x, kc2, vc2, m, qn_w, kn_w, 1e-6, pos, sd,
+                                           cd, attn_norm_w=an, attn_eps=1e-6, workspace=ws_r,
+                                           replay=True)
+        else:
+            q_raw = dev_t(synth.normal(g, (Hq, D)), dev)
+            k_raw = dev_t(synth.normal(g + 1, (Hkv, D)), dev)
+            v_new = dev_t(synth.normal(g + 2, (Hkv, D)), dev)
+            out1 = ikv.attn_decode_rope(q_raw, k_raw, v_new, kc1, vc1, n_kv, qn_w, kn_w, 1e-6, pos,
+                                        sd, cd, workspace=ws1)
+            out2 = ikv.attn_decode_rope(q_raw, k_raw, v_new, kc2, vc2, m, qn_w, kn_w, 1e-6, pos,
+                                        sd, cd, workspace=ws_r, replay=True)
+        for a, b, what in ((out1, out2, "out"), (kc1, kc2, "K cache"), (vc1, vc2, "V cache")):
+            assert np.array_equal(host(a).reshape(-1).view(np.uint32),
+                                  host(b).reshape(-1).view(np.uint32)), f"n_kv {n_kv}: {what}"
+
+
+def test_decode_replay_position_past_plan_is_flagged(dev):
+    import torch
+    Hq, Hkv, D = 16, 8, 128
+    th = oracle.rope_theta_table(1e6, D, 1024)
+    s, c = ikv.rope_sincos_table(th)
+    sd, cd = dev_t(s, dev), dev_t(c, dev)
+    kc = torch.zeros((400, Hkv, D), device=dev)
+    vc = torch.zeros_like(kc)
+    t = torch.ones((Hq, D), device=dev)
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
+    pos = torch.tensor([384], dtype=torch.int32, device=dev)  # context 385 > planned 384
+    ikv.attn_decode_rope(t, t[:Hkv], t[:Hkv], kc, vc, 384, t[0], t[0], 1e-6, pos, sd, cd,
+                         status=status, replay=True)
+    assert int(status.item()) & ikv.STATUS_POSITION
+    assert not torch.any(kc[384:])  # nothing written past the planned rows
 
 
 def test_qkv_attn_rejects_long_contexts(dev):
