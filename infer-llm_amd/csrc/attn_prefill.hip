@@ -17,6 +17,11 @@
 //     n_blocks-1-i) of its KV head one after the other, so every workgroup
 //     walks the same number of key tiles (the heaviest block alone is twice
 //     the average).
+//   * Key split: where a block per CU leaves SIMDs idle, a block's waves form
+//     NG groups holding the same rows that take interleaved key tiles and
+//     merge their softmax states through LDS at the end: two 4-wave groups
+//     (long prompts), or for short prompts two or four one-wave groups, so
+//     that the longest causal rows take 1/NG of the serial MFMA steps.
 //   * Each wavefront owns 16 rows and computes, per 32-key tile,
 //       S^T = K Q^T    (2 x [16 keys x 16 rows], contraction over 128 dims)
 //       O^T += V^T P^T (8 x [16 dims x 16 rows], contraction over 32 keys)
@@ -39,6 +44,7 @@
 #include "ikv_common.hpp"
 #include "../../include/ikv.h"
 
+#include <algorithm>
 #include <climits>
 
 namespace {
@@ -88,29 +94,49 @@ __global__ __launch_bounds__(NW * 64) void prefill_kernel(const float *__restric
                                                           int n_q, int n_kv, int n_past,
                                                           int n_blocks, int paired,
                                                           float scale_log2, ikv::Pages pages) {
-  // NG = 2: two groups of NW / 2 waves hold the same query rows and take
-  // alternate key tiles (group r: tiles r, r + 2, ...), merging their softmax
-  // states at the end: with 8 waves so that each SIMD runs two, with 2 so
-  // that a short prompt's longest causal rows take half the serial MFMA
-  // steps.
-  static_assert(NG == 1 || NG == 2, "one or two wave groups");
+  // NG > 1: NG groups of NW / NG waves hold the same query rows and take
+  // interleaved key tiles (group r: tiles r, r + NG, ...), merging their
+  // softmax states at the end: two groups of 4 waves so that each SIMD runs
+  // two; four one-wave groups (one per SIMD) so that a short prompt's
+  // longest causal rows take a quarter of the serial MFMA steps.
+  // One-wave groups (ONE) keep a single K and V buffer each, 4 x 32 KB of
+  // LDS: the next tile's K is issued once this tile's Q K^T has read K, its
+  // V once P V has read V, with this wave's own waits and no barriers.
+  static_assert(NG == 1 || NG == 2 || NG == 4, "one, two or four wave groups");
   static_assert(NW % NG == 0, "whole groups");
   constexpr int WPG = NW / NG;         // waves per group
+  constexpr bool ONE = NG == 4;
+  static_assert(!ONE || WPG == 1, "four groups are one wave each");
   constexpr int BQ = WPG * 16 / G;
-  // [group][buffer][K | V]; K rows hold 16-byte chunk c at slot c ^ (key & 15)
-  __shared__ __attribute__((aligned(16))) float s_buf[NG][2][2 * TILE];
 
   const int g = blockIdx.x % n_head_kv;
   const int item = blockIdx.x / n_head_kv;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   int grp = 0, w = wave;  // group, wave within the group
-  if constexpr (NG == 2) {
+  if constexpr (NG > 1) {
     grp = wave / WPG;
     w = wave - grp * WPG;
   }
-  float *const buf0 = s_buf[grp][0];
-  float *const buf1 = s_buf[grp][1];
+  // K and V tile buffers of this group: two of each, or with ONE one of each
+  // in separate arrays (so that the compiler's LDS-DMA waits can tell the
+  // next tile's K from this tile's V). K rows hold 16-byte chunk c at slot
+  // c ^ (key & 15). xch: where the groups' states meet at the end.
+  float *k0, *v0, *k1, *v1, *xch0;
+  if constexpr (ONE) {
+    __shared__ __attribute__((aligned(16))) float s_k[NG][TILE];
+    __shared__ __attribute__((aligned(16))) float s_v[NG][TILE];
+    k0 = k1 = s_k[grp];
+    v0 = v1 = s_v[grp];
+    xch0 = s_k[0];
+  } else {
+    __shared__ __attribute__((aligned(16))) float s_buf[NG][2][2 * TILE];
+    k0 = s_buf[grp][0];
+    v0 = k0 + TILE;
+    k1 = s_buf[grp][1];
+    v1 = k1 + TILE;
+    xch0 = s_buf[0][0];
+  }
   const int kk = lane >> 4;
   const int j = lane & 15;
   const int row = w * 16 + j;
@@ -119,7 +145,8 @@ __global__ __launch_bounds__(NW * 64) void prefill_kernel(const float *__restric
   // this wave's share of one tile: chunks c = w + WPG*i, 1 KB (2 keys) each.
   // A paged cache's block (a multiple of 64 keys) holds every tile whole, so
   // one block offset serves the tile.
-  auto issue = [&](float *buf, int tile) {
+  // parts: 1 = K, 2 = V, 3 = both (interleaved)
+  auto issue = [&](float *kbuf, float *vbuf, int tile, int parts = 3) {
     int64_t shift = 0;
     if constexpr (PAGED) shift = ikv::page_shift(pages, tile * BN);
 #pragma unroll
@@ -129,12 +156,17 @@ __global__ __launch_bounds__(NW * 64) void prefill_kernel(const float *__restric
       const int slot = lane & 31;
       const int kg = min(tile * BN + key, n_kv - 1);
       const size_t rowoff = (static_cast<size_t>(kg + shift) * n_head_kv + g) * D;
-      __builtin_amdgcn_global_load_lds(k + rowoff + 4 * (slot ^ (key & 15)),
-                                       (lds_ptr)(buf + c * 256), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(v + rowoff + 4 * slot, (lds_ptr)(buf + TILE + c * 256),
-                                       16, 0, 0);
+      if (parts & 1)
+        __builtin_amdgcn_global_load_lds(k + rowoff + 4 * (slot ^ (key & 15)),
+                                         (lds_ptr)(kbuf + c * 256), 16, 0, 0);
+      if (parts & 2)
+        __builtin_amdgcn_global_load_lds(v + rowoff + 4 * slot, (lds_ptr)(vbuf + c * 256), 16, 0,
+                                         0);
     }
   };
+  // s_waitcnt vmcnt(n) (lgkmcnt and expcnt not waited for); with ONE, a
+  // tile's 16 K loads are issued before its 16 V loads
+  constexpr int kWaitVm0 = 0x0F70, kWaitVm16 = 0x4F70;
 
   int koff[8];
 #pragma unroll
@@ -154,7 +186,14 @@ __global__ __launch_bounds__(NW * 64) void prefill_kernel(const float *__restric
     const int n_tiles = (k_end + BN - 1) / BN;
 
     __syncthreads();  // the previous item's readers are done with the buffers
-    if (grp < n_tiles) issue(buf0, grp);
+    if (grp < n_tiles) {
+      if constexpr (ONE) {
+        issue(k0, v0, grp, 1);
+        issue(k0, v0, grp, 2);
+      } else {
+        issue(k0, v0, grp);
+      }
+    }
 
     float4 qr[8];
     {
@@ -169,17 +208,18 @@ __global__ __launch_bounds__(NW * 64) void prefill_kernel(const float *__restric
     for (int t = 0; t < 8; ++t) o[t] = floatx4{0.f, 0.f, 0.f, 0.f};
     float m_row = -INFINITY, l_part = 0.f;
 
-    auto step = [&](const float *buf, int tile, float *nbuf, bool more, int next) {
+    auto step = [&](const float *kbuf, const float *vbuf, int tile, float *nk, float *nv, bool more,
+                    int next) {
       floatx4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
       // K fragments are read one step ahead so LDS latency hides under MFMAs
-      float4 ka0 = *reinterpret_cast<const float4 *>(buf + koff[0]);
-      float4 ka1 = *reinterpret_cast<const float4 *>(buf + 16 * D + koff[0]);
+      float4 ka0 = *reinterpret_cast<const float4 *>(kbuf + koff[0]);
+      float4 ka1 = *reinterpret_cast<const float4 *>(kbuf + 16 * D + koff[0]);
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         const float4 a0 = ka0, a1 = ka1;
         if (u < 7) {
-          ka0 = *reinterpret_cast<const float4 *>(buf + koff[u + 1]);
-          ka1 = *reinterpret_cast<const float4 *>(buf + 16 * D + koff[u + 1]);
+          ka0 = *reinterpret_cast<const float4 *>(kbuf + koff[u + 1]);
+          ka1 = *reinterpret_cast<const float4 *>(kbuf + 16 * D + koff[u + 1]);
         }
         s0 = mfma16(a0.x, qr[u].x, s0);
         s1 = mfma16(a1.x, qr[u].x, s1);
@@ -190,9 +230,12 @@ __global__ __launch_bounds__(NW * 64) void prefill_kernel(const float *__restric
         s0 = mfma16(a0.w, qr[u].w, s0);
         s1 = mfma16(a1.w, qr[u].w, s1);
       }
-      const float *vb = buf + TILE + voff;
-      float4 va_n = *reinterpret_cast<const float4 *>(vb);
-      float4 vc_n = *reinterpret_cast<const float4 *>(vb + 64);
+      const float *vb = vbuf + voff;
+      float4 va_n, vc_n;
+      if constexpr (!ONE) {  // (with ONE, V may land only after Q K^T: read below)
+        va_n = *reinterpret_cast<const float4 *>(vb);
+        vc_n = *reinterpret_cast<const float4 *>(vb + 64);
+      }
       // schedule: K(0) K(1) | MMA(0) K(2) | MMA(1) K(3) | ... | MMA(6) V(0) | MMA(7)
       __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
@@ -201,7 +244,22 @@ __global__ __launch_bounds__(NW * 64) void prefill_kernel(const float *__restric
         __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
       }
       __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-      if (more) issue(nbuf, next);
+      if constexpr (ONE) {
+        // this buffer's K reads are done (their MFMAs ran): the next
+        // tile's K may land in it; this tile's V must have landed
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        if (more) issue(nk, nv, next, 1);
+        if (more)
+          __builtin_amdgcn_s_waitcnt(kWaitVm16);
+        else
+          __builtin_amdgcn_s_waitcnt(kWaitVm0);
+        __builtin_amdgcn_sched_barrier(0);
+        va_n = *reinterpret_cast<const float4 *>(vb);
+        vc_n = *reinterpret_cast<const float4 *>(vb + 64);
+      } else {
+        if (more) issue(nk, nv, next);
+      }
       const int kbase = tile * BN;
       float p[8];
 #pragma unroll
@@ -223,16 +281,16 @@ __global__ __launch_bounds__(NW * 64) void prefill_kernel(const float *__restric
       if (__builtin_amdgcn_ballot_w64(mt > m_row + kRescale) != 0) {
         const float m_new = fmaxf(m_row, row_max4(mt));
         float alpha = ikv::fast_exp2(m_row - m_new);
-        // a second group's row can see only masked keys in its first tiles
-        // (its tile 1 lies past an early query): keep -inf - -inf out
-        if constexpr (NG == 2) alpha = (m_new == -INFINITY) ? 1.f : alpha;
+        // a later group's row can see only masked keys in its first tiles
+        // (its tile lies past an early query): keep -inf - -inf out
+        if constexpr (NG > 1) alpha = (m_new == -INFINITY) ? 1.f : alpha;
         m_row = m_new;
         l_part *= alpha;
 #pragma unroll
         for (int t = 0; t < 8; ++t) o[t] *= alpha;
       }
       float ref = m_row;
-      if constexpr (NG == 2) ref = (m_row == -INFINITY) ? 0.f : m_row;
+      if constexpr (NG > 1) ref = (m_row == -INFINITY) ? 0.f : m_row;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         p[i] = ikv::fast_exp2(p[i] - ref);
@@ -267,27 +325,44 @@ __global__ __launch_bounds__(NW * 64) void prefill_kernel(const float *__restric
         __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);
       }
       __builtin_amdgcn_sched_group_barrier(0x008, 16, 1);
+      if constexpr (ONE) {
+        // this buffer's V reads are done: the next tile's V may land in it
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        if (more) issue(nk, nv, next, 2);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     };
 
+    if constexpr (ONE) {
+      // this group's tiles, one buffer, no barriers (the group is this wave)
+      for (int t = grp; t < n_tiles; t += NG) {
+        __builtin_amdgcn_s_waitcnt(kWaitVm16);  // this tile's K landed (its V may not have)
+        step(k0, v0, t, k0, v0, t + NG < n_tiles, t + NG);
+      }
+    } else
     // Rounds of NG tiles, one per group, alternating the buffers.
     for (int t0 = 0; t0 < n_tiles; t0 += 2 * NG) {
       const int ta = t0 + grp;
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's loads of its tile landed
       __syncthreads();                      // everyone's landed; the other buffers are free
-      if (ta < n_tiles) step(buf0, ta, buf1, ta + NG < n_tiles, ta + NG);
+      if (ta < n_tiles) step(k0, v0, ta, k1, v1, ta + NG < n_tiles, ta + NG);
       if (t0 + NG >= n_tiles) break;
       const int tb = t0 + NG + grp;
       __builtin_amdgcn_s_waitcnt(0x0F70);
       __syncthreads();
-      if (tb < n_tiles) step(buf1, tb, buf0, tb + NG < n_tiles, tb + NG);
+      if (tb < n_tiles) step(k1, v1, tb, k0, v0, tb + NG < n_tiles, tb + NG);
     }
 
-    if constexpr (NG == 2) {
-      // Group 1 hands its (O, max, per-lane sum) to group 0 through LDS
-      // (the tile buffers are free now); group 0 merges and writes.
+    if constexpr (NG > 1) {
+      // Groups 1 .. NG-1 hand their (O, max, per-lane sum) to group 0
+      // through LDS (the tile buffers are free now); group 0 merges them in
+      // group order and writes.
       __syncthreads();
-      float *xch = s_buf[0][0] + (w * 64 + lane) * 34;
-      if (grp == 1) {
+      float *const xbase = xch0 + (w * 64 + lane) * 34;
+      constexpr int kXchStride = WPG * 64 * 34;  // floats per group
+      if (grp > 0) {
+        float *xch = xbase + (grp - 1) * kXchStride;
 #pragma unroll
         for (int t = 0; t < 8; ++t)
 #pragma unroll
@@ -297,16 +372,20 @@ __global__ __launch_bounds__(NW * 64) void prefill_kernel(const float *__restric
       }
       __syncthreads();
       if (grp == 0) {
-        const float mb = xch[32];
-        const float M = fmaxf(m_row, mb);
-        const float a = (m_row == -INFINITY) ? 0.f : ikv::fast_exp2(m_row - M);
-        const float b = (mb == -INFINITY) ? 0.f : ikv::fast_exp2(mb - M);
-        l_part = l_part * a + xch[33] * b;
 #pragma unroll
-        for (int t = 0; t < 8; ++t)
+        for (int src = 1; src < NG; ++src) {
+          const float *xch = xbase + (src - 1) * kXchStride;
+          const float mb = xch[32];
+          const float M = fmaxf(m_row, mb);
+          const float a = (m_row == -INFINITY) ? 0.f : ikv::fast_exp2(m_row - M);
+          const float b = (mb == -INFINITY) ? 0.f : ikv::fast_exp2(mb - M);
+          l_part = l_part * a + xch[33] * b;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) o[t][r] = o[t][r] * a + xch[4 * t + r] * b;
-        m_row = M;
+          for (int t = 0; t < 8; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[t][r] = o[t][r] * a + xch[4 * t + r] * b;
+          m_row = M;
+        }
       }
     }
 
@@ -352,11 +431,19 @@ void launch(const float *q, const float *k, const float *v, float *out, int n_he
             int n_kv, int n_past, float scale_log2, const ikv::Pages *pg, hipStream_t s) {
   int nw = IKV_PREFILL_NW;
   auto blocks = [&](int w) { return (n_q + w * 16 / G - 1) / (w * 16 / G); };
-  // Short prompts: one 16-row block per workgroup, its key tiles split
-  // between two one-wave groups, when that still fits one workgroup per CU
-  // (its two double buffers take 128 KB of LDS).
+  // Short prompts: one 16-row block per workgroup, when that still fits one
+  // workgroup per CU, its key tiles split among four one-wave groups (one
+  // per SIMD; four single buffers, 128 KB of LDS) when the longest causal
+  // row spans 3 tiles or more, else between two (two double buffers). At
+  // the Qwen3-0.6B shape: P = 256 11.4 us with four groups against 15.0
+  // with two, P = 128 8.0 against 9.1; P = 32 and 64 (one or two tiles)
+  // 6.2 / 6.4 with two against 7.2 / 7.5 with four.
   if (nw == 0 && IKV_PREFILL_SPLIT && blocks(1) * n_head_kv <= kCUs) {
-    launch_nw<G, 2, 2>(q, k, v, out, n_head_kv, n_q, n_kv, n_past, scale_log2, 0, pg, s);
+    const int64_t longest = std::min<int64_t>(n_kv, static_cast<int64_t>(n_past) + n_q);
+    if (longest > 2 * BN)
+      launch_nw<G, 4, 4>(q, k, v, out, n_head_kv, n_q, n_kv, n_past, scale_log2, 0, pg, s);
+    else
+      launch_nw<G, 2, 2>(q, k, v, out, n_head_kv, n_q, n_kv, n_past, scale_log2, 0, pg, s);
     return;
   }
   if (nw == 0) nw = blocks(4) * n_head_kv >= IKV_PREFILL_PAIR_MIN_WGS ? 4 : 2;
