@@ -619,7 +619,12 @@ __device__ __forceinline__ void decode_body(
     if constexpr (PRO) {
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const bool fresh = base + r * (NWAVE * 2) + wave * 2 + half == new_row;
+        // The row this lane loaded: rows past the split were clamped onto
+        // its last, which may be the new token's. Its cache row is not yet
+        // written (its bytes are whatever the memory held): a masked row
+        // still multiplies its V by a zero weight, so it must get the new
+        // row's finite values too.
+        const bool fresh = min(base + r * (NWAVE * 2) + wave * 2 + half, t_end - 1) == new_row;
         kr[r].x = fresh ? knew_rot.x : kr[r].x;
         kr[r].y = fresh ? knew_rot.y : kr[r].y;
         kr[r].z = fresh ? knew_rot.z : kr[r].z;

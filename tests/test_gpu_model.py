@@ -528,6 +528,67 @@ def test_qkv_attn_folded_equals_separate_launches(dev, oracle_pool, Hq, Hkv, K, 
     assert not host(ws)[:Hkv * 64].any()  # every arrival counter back at zero
 
 
+@pytest.mark.parametrize("Hq,n_kv", [(16, 1), (16, 41), (16, 64), (16, 100), (16, 128), (32, 77),
+                                     (16, 129), (16, 4097), (32, 4097)])
+def test_decode_ignores_the_unwritten_rows(dev, Hq, n_kv):
+    """Every one-token decode form reads only cache rows [0, n_kv-1) and the
+    new row it is given: the new row's cache slot and the rows past it are not
+    written yet, and an allocation may hand them over holding NaN or inf. A
+    lane whose row lies past the context still multiplies a V row by a zero
+    weight, so such rows must come from the new token, not from that slot.
+    Outputs with the slot and the rows past it set to NaN / inf equal, bit for
+    bit, those with finite values there."""
+    import torch
+    Hkv, D, K, cap = 8, 128, 1024, n_kv + 70
+    th = oracle.rope_theta_table(1e6, D, cap + 8)
+    s, c = ikv.rope_sincos_table(th)
+    sd, cd = dev_t(s, dev), dev_t(c, dev)
+    seed = 1300 + n_kv + Hq
+    qn_w = dev_t(1 + 0.3 * synth.normal(seed, (D,)), dev)
+    kn_w = dev_t(1 + 0.3 * synth.normal(seed + 1, (D,)), dev)
+    hist_k = synth.normal(seed + 2, (cap, Hkv, D))
+    hist_v = synth.normal(seed + 3, (cap, Hkv, D))
+    q = dev_t(synth.normal(seed + 4, (Hq, D)), dev)
+    k_new = dev_t(synth.normal(seed + 5, (Hkv, D)), dev)
+    v_new = dev_t(synth.normal(seed + 6, (Hkv, D)), dev)
+    pos = torch.tensor([n_kv - 1], dtype=torch.int32, device=dev)
+    ws = ikv.decode_workspace(Hq, Hkv, D, n_kv, device=dev)
+    fold = n_kv <= 128
+    if fold:
+        wq = dev_t(synth.normal(seed + 7, (Hq * D, K), 0.02), dev)
+        wk = dev_t(synth.normal(seed + 8, (Hkv * D, K), 0.02), dev)
+        wv = dev_t(synth.normal(seed + 9, (Hkv * D, K), 0.02), dev)
+        x = dev_t(synth.normal(seed + 10, (K,)), dev)
+
+    def run(fill):
+        kk, vv = hist_k.copy(), hist_v.copy()
+        if fill is not None:
+            kk[n_kv - 1:] = fill
+            vv[n_kv - 1:] = fill
+        outs = []
+        for form in ("plain", "rope", "fold"):
+            if form == "fold" and not fold:
+                continue
+            kc, vc = dev_t(kk, dev), dev_t(vv, dev)
+            if form == "plain":
+                o = ikv.attn_decode(q, kc, vc, n_kv, k_new=k_new, v_new=v_new, workspace=ws)
+            elif form == "rope":
+                o = ikv.attn_decode_rope(q, k_new, v_new, kc, vc, n_kv, qn_w, kn_w, 1e-6, pos, sd, cd,
+                                         workspace=ws)
+            else:
+                o, *_ = ikv.qkv_attn_decode(wq, wk, wv, x, kc, vc, n_kv, qn_w, kn_w, 1e-6, pos, sd, cd,
+                                            workspace=ws)
+            outs.append((form, host(o).copy(), host(kc)[:n_kv].copy(), host(vc)[:n_kv].copy()))
+        return outs
+
+    base = run(None)
+    for fill in (np.nan, np.inf, -np.inf):
+        for (form, o0, k0, v0), (_, o1, k1, v1) in zip(base, run(fill)):
+            assert np.isfinite(o1).all(), f"{form}, slot {fill}: non-finite output"
+            for a, b, what in ((o0, o1, "out"), (k0, k1, "K rows"), (v0, v1, "V rows")):
+                assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"{form}, slot {fill}: {what}"
+
+
 @pytest.mark.parametrize("Hq,n_kv_lo,width", [(16, 33, 256), (16, 129, 256), (16, 2050, 256),
                                                (16, 2113, 128), (32, 300, 200)])
 def test_decode_replay_equals_per_context_launches(dev, Hq, n_kv_lo, width):
