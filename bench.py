@@ -894,6 +894,10 @@ def main():
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
             "launch_us": round(per_launch * 1e6, 3),
+            # the fastest streaming read of one launch's bytes measured in this run
+            # (extra.hbm_probes): the floor a kernel of this size reaches on this box
+            "read_floor_us": (extra["hbm_probes"] or {}).get("read_33MB_floor_us")
+            if args.ctx == 4096 else None,
         },
         "cpu_baseline": cpu,
         "extra": extra,

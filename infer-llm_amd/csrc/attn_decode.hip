@@ -112,17 +112,23 @@ struct Prologue {
   // context is pos[0] + 1, read on the device, and the launch was planned
   // for dyn_max keys (splits past pos[0] + 1 are empty).
   int dyn_max = 0;
+  // 0, as a kernel argument: an offset the compiler cannot fold, so that a
+  // load through it is a per-lane value that need not be waited for at once
+  int zero = 0;
 };
 
 // The context of a launch: n_kv, or with pro.dyn_max, pos[0] + 1. A
 // position outside [0, dyn_max) raises IKV_STATUS_POSITION and runs as
 // dyn_max keys, inside the planned splits.
-__device__ __forceinline__ int launch_n_kv(const Prologue &pro, int n_kv) {
+// p: pos[0] when the launch is a replay form (loaded early by the caller).
+__device__ __forceinline__ int launch_n_kv(const Prologue &pro, int n_kv, int p) {
   if (pro.dyn_max <= 0) return n_kv;
-  const int p = pro.pos[0];
   if (p >= 0 && p < pro.dyn_max) return p + 1;
   if (threadIdx.x == 0) ikv::raise_status(pro.status, IKV_STATUS_POSITION);
   return pro.dyn_max;
+}
+__device__ __forceinline__ int launch_n_kv(const Prologue &pro, int n_kv) {
+  return launch_n_kv(pro, n_kv, pro.dyn_max > 0 ? pro.pos[0] : 0);
 }
 
 #ifndef IKV_DECODE_MIN_SPLIT_TOKENS
@@ -811,6 +817,11 @@ __global__ __launch_bounds__(WG, 2) void qkv_attn_kernel(
     const float *__restrict__ x, const float *attn_norm_w, float attn_eps, float *q_out,
     float *k_out, float *v_out, int K, float *kc, float *vc, float *out, int *counters,
     int n_head_kv, int n_kv, int tokens_per_split, float scale_log2, Prologue pro) {
+  // A replay form's position, loaded before the projection's weights: the
+  // decode that needs it then does not wait for it. Through a per-lane
+  // address (an offset of pro.zero): a uniform load would be waited for at
+  // once, to move it to a scalar register.
+  const int pos_lane = pro.pos[threadIdx.x & pro.zero];
   const int n0 = n_head_kv * G * D;  // q rows
   const int n1 = n_head_kv * D;      // k rows, v rows
   const int lane = threadIdx.x & 63;
@@ -863,7 +874,9 @@ __global__ __launch_bounds__(WG, 2) void qkv_attn_kernel(
   __syncthreads();
   if (!s_last_qkv) return;
   decode_body<G, true, false, true>(q_out, kc, vc, k_out, v_out, out, counters, nullptr, nullptr,
-                                    n_head_kv, launch_n_kv(pro, n_kv), tokens_per_split, 1,
+                                    n_head_kv,
+                                    launch_n_kv(pro, n_kv, __builtin_amdgcn_readfirstlane(pos_lane)),
+                                    tokens_per_split, 1,
                                     scale_log2, pro, ikv::Pages{}, g, 0);
 }
 
