@@ -59,7 +59,10 @@ constexpr int D = 128;  // head_dim supported by this kernel
 constexpr int NWAVE = IKV_DECODE_NWAVE;  // wavefronts per workgroup
 constexpr int WG = NWAVE * 64;
 #ifndef IKV_DECODE_R
-#define IKV_DECODE_R 4
+// 2 (32-token tiles) against 4: ctx 4096 11.3 against 11.9 us per layer,
+// the Qwen3-8B shape 12.2 against 13.2 us (27.1 against 30.5 at ctx 16384),
+// faster at every context measured on MI355X (1: slower again)
+#define IKV_DECODE_R 2
 #endif
 constexpr int R = IKV_DECODE_R;      // K and V rows per lane per iteration
 constexpr int TILE = NWAVE * 2 * R;  // tokens per workgroup iteration
@@ -131,6 +134,11 @@ __device__ __forceinline__ int launch_n_kv(const Prologue &pro, int n_kv) {
   return launch_n_kv(pro, n_kv, pro.dyn_max > 0 ? pro.pos[0] : 0);
 }
 
+// Contexts this short run as one split per KV head (and can fold into the
+// q/k/v projection's launch).
+constexpr int kOneSplitTokens = 128;
+static_assert(kOneSplitTokens % TILE == 0, "whole tiles");
+
 #ifndef IKV_DECODE_MIN_SPLIT_TOKENS
 #define IKV_DECODE_MIN_SPLIT_TOKENS 64
 #endif
@@ -153,10 +161,10 @@ Plan plan_for(int n_head, int n_head_kv, int64_t n_kv) {
   int64_t target = max_splits(n_head, n_head_kv);
   const int64_t by_min = (n_kv + IKV_DECODE_MIN_SPLIT_TOKENS - 1) / IKV_DECODE_MIN_SPLIT_TOKENS;
   if (target > by_min) target = by_min;
-  // Up to two tiles one workgroup per KV head is faster than any split: the
-  // second tile costs less than the merge (measured on MI355X: 127 tokens
-  // take 5.4 us in one split, 6.7 us in two).
-  if (n_kv <= 2 * TILE) target = 1;
+  // Up to kOneSplitTokens keys one workgroup per KV head is faster than any
+  // split: the further tiles cost less than the merge (measured on MI355X:
+  // 127 tokens take 5.4 us in one split, 6.7 us in two).
+  if (n_kv <= kOneSplitTokens) target = 1;
   if (target < 1) target = 1;
   const int64_t n_tiles = (n_kv + TILE - 1) / TILE;
   const int64_t tiles_per_split = (n_tiles + target - 1) / target;
@@ -799,7 +807,7 @@ __global__ __launch_bounds__(WG, waves_per_simd(G)) void decode_kernel(
 // belong to one KV head g (D and the group's G * D q rows are multiples of
 // 16); a per-head arrival counter finds the last of the head's workgroups to
 // finish, and that workgroup runs the head's decode (qk-norm + RoPE + append
-// + attention over n_kv <= 2 * TILE keys, one split) with the decode kernel's
+// + attention over n_kv <= kOneSplitTokens keys, one split) with the decode kernel's
 // device code, reading the head's q, k and v rows back coherently. The
 // outputs are bit-identical to the separate launches; the decode's launch,
 // its ramp and its wait for the projection's last wave are gone.
