@@ -807,8 +807,8 @@ __global__ __launch_bounds__(WG, waves_per_simd(G)) void decode_kernel(
 // belong to one KV head g (D and the group's G * D q rows are multiples of
 // 16); a per-head arrival counter finds the last of the head's workgroups to
 // finish, and that workgroup runs the head's decode (qk-norm + RoPE + append
-// + attention over n_kv <= kOneSplitTokens keys, one split) with the decode kernel's
-// device code, reading the head's q, k and v rows back coherently. The
+// + attention over n_kv <= kOneSplitTokens keys, one split) with the decode
+// kernel's device code, reading the head's q, k and v rows back coherently. The
 // outputs are bit-identical to the separate launches; the decode's launch,
 // its ramp and its wait for the projection's last wave are gone.
 constexpr int kQkvRpw = 2;                        // rows per wave
