@@ -365,12 +365,12 @@ def hbm_probes(torch, ikv):
     res["read_long_gbs"] = round(big.numel() * 4 / t / 1e9, 1)
     del big
     # one decode layer's bytes per launch, 28 distinct buffers (> 2x the MALL), in
-    # grids shaped like decode's (264 workgroups of 512 threads at ctx 4096) and wider,
-    # with 1 to 16 loads in flight per lane; the fastest is the floor one launch of
-    # this size reaches on this box
+    # grids shaped like decode's (208 workgroups of 512 threads at ctx 4096: 26 splits
+    # x 8 KV heads; 256 = one per CU) and wider, with 1 to 16 loads in flight per lane;
+    # the fastest is the floor one launch of this size reaches on this box
     bufs = [torch.ones(decode_bytes(4096) // 4 // 16 * 16, device=dev) for _ in range(N_LAYER)]
     shapes = {}
-    for grid, u in ((264, 16), (264, 8), (528, 8), (1056, 4), (2048, 1)):
+    for grid, u in ((208, 16), (256, 16), (256, 8), (528, 8), (1056, 4), (2048, 1)):
         t = timed_graph(lambda: [read(b, grid, u) for b in bufs], 10) / N_LAYER
         shapes[f"{grid}x512_u{u}"] = round(t * 1e6, 2)
     best = min(shapes, key=shapes.get)

@@ -70,10 +70,13 @@ static_assert(64 % TILE == 0, "a paged block (a multiple of 64 tokens) must hold
 
 #ifndef IKV_DECODE_TARGET_WGS
 // Workgroups aimed for over all KV heads: one 8-wave workgroup per CU of
-// MI355X's 256 plus one per KV head (33 splits per head with 8 KV heads).
-// Fewer splits keep the merge short (it reads G x splits x 512 B in one
-// workgroup); more would not add bandwidth.
-#define IKV_DECODE_TARGET_WGS 264
+// MI355X's 256 (32 splits per head with 8 KV heads). One more split per
+// head (264 workgroups) puts a second full split on 8 CUs, and those set
+// the kernel's end: measured ctx 20000 40.9 against 31.1 us, ctx 4096 11.35
+// against 10.16 us (the plan then takes 26 splits of 5 tiles), equal or
+// slower at no context measured. Fewer splits keep the merge short (it
+// reads G x splits x 512 B in one workgroup).
+#define IKV_DECODE_TARGET_WGS 256
 #endif
 #ifndef IKV_DECODE_NT
 #define IKV_DECODE_NT 1  // 1: K/V history read with non-temporal (streaming) loads

@@ -254,9 +254,14 @@ def decode_workspace_bytes(n_head: int, n_head_kv: int, head_dim: int, n_kv: int
 
 
 def decode_workspace(n_head: int, n_head_kv: int, head_dim: int, n_kv: int, device="cuda"):
-    """Zero-filled workspace for attn_decode (reusable across ordered launches)."""
+    """Zero-filled workspace for attn_decode at every context up to n_kv
+    (reusable across ordered launches). The split count is not monotone in
+    the context (it peaks where a split's tile count steps down), so every
+    context is asked."""
     torch = _torch()
-    nbytes = max(decode_workspace_bytes(n_head, n_head_kv, head_dim, n_kv), 256)
+    nbytes = 256
+    for n in range(1, n_kv + 1):
+        nbytes = max(nbytes, decode_workspace_bytes(n_head, n_head_kv, head_dim, n))
     return torch.zeros((nbytes + 3) // 4, dtype=torch.float32, device=device)
 
 

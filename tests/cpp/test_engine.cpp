@@ -125,12 +125,13 @@ static void cpu_tests() {
         ok = ok && most == r;
       }
     }
-    // the Qwen3-0.6B shape peaks at 2049..2112 keys (33 splits), which a
-    // powers-of-two sampling misses
+    // the split count is not monotone in the context (Qwen3-0.6B shape: 2048
+    // keys take 32 splits, 2080 keys 22), so a reservation sized from the
+    // largest context alone would be too small
     const size_t at2048 = ikv_attn_decode_workspace_bytes(16, 8, 128, 2048);
     const size_t at2080 = ikv_attn_decode_workspace_bytes(16, 8, 128, 2080);
-    ok = ok && at2080 > at2048 &&
-         HIPBackend::decode_workspace_reservation(16, 8, 128, 2560) >= at2080;
+    ok = ok && at2080 < at2048 &&
+         HIPBackend::decode_workspace_reservation(16, 8, 128, 2080) >= at2048;
     CHECK(ok, "decode workspace reservation covers every context up to capacity");
   }
   {

@@ -127,12 +127,12 @@ def test_gemm_rejects_bad_arguments_without_launching():
 
 def test_decode_replay_limit_tracks_the_split_plan():
     # (host arithmetic) Qwen3-0.6B shape: one split up to 128 keys, then
-    # 64-key splits up to 33 per KV head (2112 keys), then 128-key splits
+    # 64-key splits up to 32 per KV head (2048 keys), then 96-key splits
     lim = lambda n, w: ikv.decode_replay_limit(16, 8, 128, n, w)
     assert lim(1, 256) == 128 and lim(33, 256) == 128 and lim(128, 256) == 128
     assert lim(129, 256) == 384 and lim(129, 1) == 129
-    assert lim(2000, 256) == 2112 and lim(2112, 256) == 2112
-    assert lim(2113, 256) == 2368
+    assert lim(2000, 256) == 2048 and lim(2048, 256) == 2048
+    assert lim(2049, 256) == 2304 and lim(2113, 256) == 2368
     # the plan the limit promises to keep: per-context workspace sizes grow
     # with the context and never pass the limit's
     for n in (129, 1000, 2113, 4000):
