@@ -125,6 +125,21 @@ def test_gemm_rejects_bad_arguments_without_launching():
     assert call(m=2**40) == -errno.EOVERFLOW
 
 
+def test_decode_plan_stays_within_one_workgroup_per_cu():
+    # (host arithmetic) a workspace holds n_head x n_splits partial rows of
+    # 128 floats past a fixed region, so its size tells the split count. The
+    # plan never goes past 256 workgroups (32 splits x 8 KV heads): a 33rd
+    # split per head put a second full split on some CUs, which then set the
+    # kernel's end. ctx 4096 (4097 keys) takes 26 splits of 5 tiles.
+    for n_head in (16, 32):
+        ws = lambda n: ikv.decode_workspace_bytes(n_head, 8, 128, n)
+        row = 4 * n_head * 128
+        peak = ws(2048)  # 32 splits of 64 keys
+        assert all(ws(n) <= peak for n in range(129, 50001, 3))
+        assert ws(20000) == peak and ws(40000) == peak
+        assert peak - ws(4097) == 6 * row
+
+
 def test_decode_replay_limit_tracks_the_split_plan():
     # (host arithmetic) Qwen3-0.6B shape: one split up to 128 keys, then
     # 64-key splits up to 32 per KV head (2048 keys), then 96-key splits
