@@ -75,12 +75,12 @@ int ikv_append_f32(void *dst_rows, const void *src_rows, size_t n_rows, size_t r
  *            It must be zero-filled before its first use (hipMemset at
  *            allocation); every launch leaves the counters at zero again,
  *            so the same workspace serves every later launch and context
- *            length of one (n_head, n_head_kv) shape (zero it again before
- *            using it for another shape; the split count is not monotone in
- *            n_kv, so size it for every context it will serve). Unused, and
- *            may be NULL, when the context fits one split. Launches that
- *            share one workspace must be ordered (same stream); concurrent
- *            ones race.
+ *            length of every shape with the same n_head_kv that it is large
+ *            enough for (zero it again before using it for another n_head_kv;
+ *            the split count is not monotone in n_kv, so size it for every
+ *            context it will serve). Unused, and may be NULL, when the
+ *            context fits one split. Launches that share one workspace must
+ *            be ordered (same stream); concurrent ones race.
  * head_dim must be 128; n_head/n_head_kv must be 1, 2, 4 or 8.
  * ------------------------------------------------------------------- */
 size_t ikv_attn_decode_workspace_bytes(int n_head, int n_head_kv, int head_dim, int64_t n_kv);

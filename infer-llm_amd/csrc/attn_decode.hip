@@ -82,11 +82,8 @@ static_assert(64 % TILE == 0, "a paged block (a multiple of 64 tokens) must hold
 #define IKV_DECODE_NT 1  // 1: K/V history read with non-temporal (streaming) loads
 #endif
 
-// The merging workgroup keeps one weight and one sum per (query head of the
-// group, split) in LDS: G * n_splits <= kMergeCap.
+// Splits per KV head are capped so that G * n_splits <= kMergeCap.
 constexpr int kMergeCap = 1024;
-// Partial-output loads in flight per lane while merging (float4 each).
-constexpr int kMergeChunk = 16;
 // Arrival counters: one int per KV head, kCounterStride ints apart.
 constexpr int kCounterStride = 64;
 
@@ -191,24 +188,21 @@ struct WsLayout {
 };
 
 // [n_head_kv counters, 256 B apart][n_head x n_splits x (max, sum)]
-// [n_head x n_splits x D]. The counters and the (max, sum) region sit at the
-// same offsets for every n_kv (the region is sized for max_splits), so one
-// workspace serves every context length: what one launch leaves zeroed there
-// is what the next one expects, and no launch's partial outputs land in it.
+// [n_head x n_splits x D]. Every launch leaves the counters at zero, so one
+// workspace serves every context length of a shape.
 WsLayout ws_layout(int n_head, int n_head_kv, int n_splits) {
   WsLayout w;
   w.counters = 0;
   w.part_ml = align256(sizeof(int) * kCounterStride * static_cast<size_t>(n_head_kv));
-  w.part_o = w.part_ml + align256(sizeof(float) * 2 * static_cast<size_t>(n_head) *
-                                  max_splits(n_head, n_head_kv));
+  w.part_o = w.part_ml + align256(sizeof(float) * 2 * static_cast<size_t>(n_head) * n_splits);
   w.total = w.part_o + sizeof(float) * static_cast<size_t>(n_head) * n_splits * D;
   return w;
 }
 
-// Stores and loads of the split partials, coherent across the XCDs of the
-// device (agent scope): the stores are performed at the device's coherence
-// point and the loads (sc1) read from it, so no L2 writeback or invalidate
-// is needed on either side.
+// Stores and loads between the workgroups of a launch, coherent across the
+// XCDs of the device (agent scope): the stores are performed at the device's
+// coherence point and the loads (sc1) read from it, so no L2 writeback or
+// invalidate is needed on either side.
 __device__ __forceinline__ void store_agent(float *p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -220,8 +214,9 @@ __device__ __forceinline__ void store2_agent(float *p, float a, float b) {
                      __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Agent-coherent 8- and 16-byte loads through a buffer resource over the
-// partials (raw buffer: loads past num_records return zeros).
+// Agent-coherent 8- and 16-byte loads and 16-byte stores through a buffer
+// resource over the partials (raw buffer: loads past num_records return
+// zeros).
 constexpr int kBufWord3 = 0x00020000;  // raw dword buffer, gfx9 family
 constexpr int kCpolSc1 = 16;           // cache policy: agent scope
 typedef float f2v __attribute__((ext_vector_type(2)));
@@ -237,6 +232,11 @@ __device__ __forceinline__ float2 load2_agent(__amdgpu_buffer_rsrc_t r, unsigned
 __device__ __forceinline__ float4 load4_agent(__amdgpu_buffer_rsrc_t r, unsigned byte_off) {
   const f4v v = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kCpolSc1);
   return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void store4_agent(__amdgpu_buffer_rsrc_t r, unsigned byte_off,
+                                             float4 v) {
+  const f4v x = {v.x, v.y, v.z, v.w};
+  __builtin_amdgcn_raw_buffer_store_b128(x, r, byte_off, 0, kCpolSc1);
 }
 // One float stored by another workgroup of this launch (on any XCD) before
 // it was counted: an agent-coherent load.
@@ -298,6 +298,26 @@ __device__ __forceinline__ void merge_waves(const float (&s_acc)[NWAVE][G][D],
     const float e = (mw == -INFINITY) ? 0.f : ikv::fast_exp2(mw - M);
     O += s_acc[w][h][d] * e;
     L += s_l[w][h] * e;
+  }
+}
+
+// merge_waves for output columns 4c .. 4c + 3 of query head h.
+template <int G>
+__device__ __forceinline__ void merge_waves4(const float (&s_acc)[NWAVE][G][D],
+                                             const float (&s_m)[NWAVE][G],
+                                             const float (&s_l)[NWAVE][G], int h, int c, float4 &O,
+                                             float &L, float &M) {
+  M = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < NWAVE; ++w) M = fmaxf(M, s_m[w][h]);
+  O = make_float4(0.f, 0.f, 0.f, 0.f);
+  L = 0.f;
+#pragma unroll
+  for (int w = 0; w < NWAVE; ++w) {
+    const float mw = s_m[w][h];
+    const float e = (mw == -INFINITY) ? 0.f : ikv::fast_exp2(mw - M);
+    O = ikv::fma4(e, *reinterpret_cast<const float4 *>(&s_acc[w][h][4 * c]), O);
+    L = fmaf(s_l[w][h], e, L);
   }
 }
 
@@ -456,109 +476,106 @@ __device__ __forceinline__ void qk_prologue(const Prologue &pro, ProStage<G> &st
   __syncthreads();
 }
 
-// LDS of the merging workgroup.
+// The merging workgroup's 16 half-waves ("units") split the work: unit u
+// serves query head u % G of the group and sums the splits s = k, k + U,
+// k + 2U, ... (k = u / G, U = 16 / G units per head), lane c of the unit
+// owning output columns 4c .. 4c + 3. A unit loads the (max, sum) record and
+// its 16-byte piece of the partial output of every split it sums, J splits
+// per round, all loads of a round issued before any is used and none behind
+// a branch (one memory round trip for up to J * U splits per head: J = 4 / 8
+// / 16 for G <= 2 / 4 / 8, so a round covers 32 splits at G >= 2), and folds
+// them into its own (max, sum, output) in registers. The units of a head
+// then combine through LDS. (Fewer units with more loads each, a wavefront
+// per query head combining its halves by lane swaps, measured slower: the
+// merge is bound by how fast one CU issues its loads.)
+constexpr int kMergeUnits = WG / 32;
+
 struct MergeLds {
-  float w[kMergeCap];    // per (h, split): max, then the weight 2^(max - M_h)
-  float l[kMergeCap];    // per (h, split): sum
-  float part[WG / 32 * D];  // per (lane group p, h, d): partial sums of the output
-  float L[8];            // per h: sum of the weighted split sums
+  float4 acc[kMergeUnits][32];  // per unit and lane: unnormalised output
+  float m[kMergeUnits];         // per unit: max
+  float l[kMergeUnits];         // per unit: sum
 };
 
 // Run by the last split of KV head g to arrive: out = sum_s w_s O_s / sum_s w_s l_s
-// over the n_splits partials of each of the G query heads. The statistics and
-// the first chunk of partial outputs are loaded together, so a context whose
-// splits fit one chunk costs one memory round trip.
+// over the n_splits partials of each of the G query heads, w_s = 2^(m_s - max).
 template <int G>
-__device__ __forceinline__ void merge_splits(const float *part_ml, const float *part_o, float *out, int g,
-                             int n_splits, MergeLds &lds) {
+__device__ __forceinline__ void merge_splits(const float *part_ml, const float *part_o, float *out,
+                                             int g, int n_splits, MergeLds &lds) {
+  constexpr int U = kMergeUnits / G;  // units per query head
+  // rounds of J splits per unit until every split is summed:
+  // ceil(n_splits / (U * J)), one for the plans of the Qwen3 shapes
+  constexpr int J = G <= 2 ? 4 : (G == 4 ? 8 : 16);
   const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int S = n_splits;
-  // Lane (p, hh, c) sums float4 column c of query head hh over splits
-  // p, p + P, ...
-  constexpr int P = WG / (32 * G);
+  const int u = tid >> 5;
   const int c = tid & 31;
-  const int hh = (tid >> 5) % G;
-  const int p = tid / (32 * G);
+  const int hh = u % G;
+  const int k = u / G;
+  const int S = n_splits;
   // This KV head's partials: G x S (max, sum) pairs and G x S x D outputs.
+  // Raw buffer loads past the end of a range return zeros; a split index past
+  // S inside the range reads another head's record, which the mask drops.
   const __amdgpu_buffer_rsrc_t rml =
       partial_rsrc(part_ml + static_cast<size_t>(g * G) * S * 2, sizeof(float) * 2 * G * S);
   const __amdgpu_buffer_rsrc_t ro =
       partial_rsrc(part_o + static_cast<size_t>(g * G) * S * D, sizeof(float) * G * S * D);
-  const unsigned o_base = static_cast<unsigned>(sizeof(float) * (hh * S * D + 4 * c));
-
-  // The partials were published with agent-coherent stores before their
-  // workgroups were counted; agent-coherent loads observe them.
-  constexpr int kStat = (kMergeCap + WG - 1) / WG;  // (max, sum) pairs per lane
-  float2 st[kStat];
-#pragma unroll
-  for (int k = 0; k < kStat; ++k) {
-    const int i = tid + k * WG;
-    st[k] = (i < G * S) ? load2_agent(rml, static_cast<unsigned>(sizeof(float) * 2 * i))
-                        : make_float2(-INFINITY, 0.f);
-  }
-  float4 v[kMergeChunk];
-#pragma unroll
-  for (int j = 0; j < kMergeChunk; ++j) {
-    const int s = p + j * P;
-    v[j] = (s < S) ? load4_agent(ro, o_base + static_cast<unsigned>(sizeof(float) * s * D))
-                   : make_float4(0.f, 0.f, 0.f, 0.f);
-  }
-#pragma unroll
-  for (int k = 0; k < kStat; ++k) {
-    const int i = tid + k * WG;
-    if (i < G * S) {
-      lds.w[i] = st[k].x;
-      lds.l[i] = st[k].y;
-    }
-  }
-  __syncthreads();
-  for (int h = wave; h < G; h += NWAVE) {
-    float mx = -INFINITY;
-    for (int s = lane; s < S; s += 64) mx = fmaxf(mx, lds.w[h * S + s]);
-    mx = ikv::wave_max(mx);
-    float lsum = 0.f;
-    for (int s = lane; s < S; s += 64) {
-      const float m = lds.w[h * S + s];
-      const float w = (m == -INFINITY) ? 0.f : ikv::fast_exp2(m - mx);
-      lds.w[h * S + s] = w;
-      lsum += lds.l[h * S + s] * w;
-    }
-    lsum = ikv::wave_sum(lsum);
-    if (lane == 0) lds.L[h] = lsum;
-  }
-  __syncthreads();
-
-  const float *wrow = lds.w + hh * S;
+  float M = -INFINITY, L = 0.f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int s0 = k; s0 < S; s0 += U * J) {
+    float mj[J], lj[J], ox[J], oy[J], oz[J], ow[J];
+    // The partials were published with agent-coherent stores before their
+    // workgroups were counted; agent-coherent loads observe them.
 #pragma unroll
-  for (int j = 0; j < kMergeChunk; ++j) {
-    const int s = p + j * P;
-    if (s < S) acc = ikv::fma4(wrow[s], v[j], acc);
-  }
-  for (int s0 = p + P * kMergeChunk; s0 < S; s0 += P * kMergeChunk) {
-#pragma unroll
-    for (int j = 0; j < kMergeChunk; ++j) {
-      const int s = s0 + j * P;
-      v[j] = (s < S) ? load4_agent(ro, o_base + static_cast<unsigned>(sizeof(float) * s * D))
-                     : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int j = 0; j < J; ++j) {
+      const unsigned r = static_cast<unsigned>(hh * S + s0 + j * U);
+      const float2 st = load2_agent(rml, r * static_cast<unsigned>(sizeof(float) * 2));
+      const float4 v = load4_agent(ro, r * static_cast<unsigned>(sizeof(float) * D) + 16u * c);
+      mj[j] = (s0 + j * U < S) ? st.x : -INFINITY;
+      lj[j] = st.y;
+      ox[j] = v.x;
+      oy[j] = v.y;
+      oz[j] = v.z;
+      ow[j] = v.w;
     }
+    float mx = M;
 #pragma unroll
-    for (int j = 0; j < kMergeChunk; ++j) {
-      const int s = s0 + j * P;
-      if (s < S) acc = ikv::fma4(wrow[s], v[j], acc);
+    for (int j = 0; j < J; ++j) mx = fmaxf(mx, mj[j]);
+    // with every record so far masked (mx = -inf) nothing is added
+    const float ref = (mx == -INFINITY) ? 0.f : mx;
+    const float alpha = ikv::fast_exp2(M - ref);
+    L *= alpha;
+    acc = ikv::scale4(alpha, acc);
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const float e = ikv::fast_exp2(mj[j] - ref);
+      L = fmaf(e, lj[j], L);
+      acc = make_float4(fmaf(e, ox[j], acc.x), fmaf(e, oy[j], acc.y), fmaf(e, oz[j], acc.z),
+                        fmaf(e, ow[j], acc.w));
     }
+    M = mx;
   }
-  *reinterpret_cast<float4 *>(&lds.part[(p * G + hh) * D + 4 * c]) = acc;
+  lds.acc[u][c] = acc;
+  if (c == 0) {
+    lds.m[u] = M;
+    lds.l[u] = L;
+  }
   __syncthreads();
-  for (int i = tid; i < G * D; i += WG) {
-    const int h = i / D;
-    const int d = i - h * D;
-    float o = 0.f;
+  if (tid < G * 32) {
+    // tid < G * 32: unit tid >> 5 = hh is this head's first unit
+    float Mx = -INFINITY;
 #pragma unroll
-    for (int q = 0; q < P; ++q) o += lds.part[(q * G + h) * D + d];
-    out[static_cast<size_t>(g * G + h) * D + d] = o / lds.L[h];
+    for (int q = 0; q < U; ++q) Mx = fmaxf(Mx, lds.m[hh + q * G]);
+    float Ls = 0.f;
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int q = 0; q < U; ++q) {
+      const int uu = hh + q * G;
+      const float mq = lds.m[uu];
+      const float w = (mq == -INFINITY) ? 0.f : ikv::fast_exp2(mq - Mx);
+      Ls = fmaf(w, lds.l[uu], Ls);
+      o = ikv::fma4(w, lds.acc[uu][c], o);
+    }
+    *reinterpret_cast<float4 *>(out + static_cast<size_t>(g * G + hh) * D + 4 * c) =
+        make_float4(o.x / Ls, o.y / Ls, o.z / Ls, o.w / Ls);
   }
 }
 
@@ -576,7 +593,6 @@ __device__ __forceinline__ void decode_body(
   __shared__ __attribute__((aligned(16))) float s_acc[NWAVE][G][D];
   __shared__ float s_m[NWAVE][G];
   __shared__ float s_l[NWAVE][G];
-  __shared__ __attribute__((aligned(16))) MergeLds s_merge;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -729,22 +745,21 @@ __device__ __forceinline__ void decode_body(
       *reinterpret_cast<float4 *>(vc + off) = *reinterpret_cast<const float4 *>(v_new + head_off);
   }
 
-  // Merge the two half-waves (they saw different tokens).
+  // Merge the two half-waves (they saw different tokens): lanes i and i ^ 32
+  // swap values (v_permlane32_swap), and every lane combines the pair in the
+  // same order, so both halves hold the same bits.
 #pragma unroll
   for (int h = 0; h < G; ++h) {
-    const float mo = __shfl_xor(m[h], 32, 64);
-    const float lo = __shfl_xor(l[h], 32, 64);
-    float4 ao;
-    ao.x = __shfl_xor(acc[h].x, 32, 64);
-    ao.y = __shfl_xor(acc[h].y, 32, 64);
-    ao.z = __shfl_xor(acc[h].z, 32, 64);
-    ao.w = __shfl_xor(acc[h].w, 32, 64);
-    const float M = fmaxf(m[h], mo);
-    const float a = (M == -INFINITY) ? 0.f : ikv::fast_exp2(m[h] - M);
-    const float b = (M == -INFINITY) ? 0.f : ikv::fast_exp2(mo - M);
-    l[h] = l[h] * a + lo * b;
-    acc[h] = make_float4(acc[h].x * a + ao.x * b, acc[h].y * a + ao.y * b,
-                         acc[h].z * a + ao.z * b, acc[h].w * a + ao.w * b);
+    const float2 mm = ikv::halves(m[h]);
+    const float2 ll = ikv::halves(l[h]);
+    const float2 ax = ikv::halves(acc[h].x), ay = ikv::halves(acc[h].y);
+    const float2 az = ikv::halves(acc[h].z), aw = ikv::halves(acc[h].w);
+    const float M = fmaxf(mm.x, mm.y);
+    const float a = (M == -INFINITY) ? 0.f : ikv::fast_exp2(mm.x - M);
+    const float b = (M == -INFINITY) ? 0.f : ikv::fast_exp2(mm.y - M);
+    l[h] = ll.x * a + ll.y * b;
+    acc[h] = make_float4(ax.x * a + ax.y * b, ay.x * a + ay.y * b, az.x * a + az.y * b,
+                         aw.x * a + aw.y * b);
     m[h] = M;
   }
   if (half == 0) {
@@ -759,7 +774,7 @@ __device__ __forceinline__ void decode_body(
   }
   __syncthreads();
 
-  // Merge the 4 waves. With one split the result is final.
+  // Merge the waves. With one split the result is final.
   if (n_splits == 1) {
     for (int idx = tid; idx < G * D; idx += WG) {
       const int h = idx / D;
@@ -770,30 +785,40 @@ __device__ __forceinline__ void decode_body(
     }
     return;
   }
-  for (int idx = tid; idx < G * D; idx += WG) {
-    const int h = idx / D;
-    const int d = idx - h * D;
-    float O, L, M;
-    merge_waves<G>(s_acc, s_m, s_l, h, d, O, L, M);
-    const size_t slot = static_cast<size_t>(g * G + h) * n_splits + split;
-    store_agent(part_o + slot * D + d, O);
-    if (d == 0) store2_agent(part_ml + 2 * slot, M, L);
-  }
-  // Publish: this lane's partial stores have completed (vmcnt counts stores
-  // on CDNA) before the workgroup's arrival is counted.
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(0);
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __syncthreads();
+  // Publish: wave 0 merges the waves and stores the workgroup's (max, sum,
+  // unnormalised output) agent-coherently, 16 bytes per lane and column;
+  // once its stores have completed (vmcnt counts stores on CDNA) it counts
+  // the workgroup in the KV head's arrival counter. The split that arrives
+  // last merges the head and resets the counter for the next launch.
   __shared__ int s_last;
-  if (tid == 0) {
-    int *ctr = counters + static_cast<size_t>(g) * kCounterStride;
-    const int before = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = (before == n_splits - 1);
-    if (s_last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (wave == 0) {
+    const __amdgpu_buffer_rsrc_t ro = partial_rsrc(
+        part_o + static_cast<size_t>(g * G) * n_splits * D, sizeof(float) * G * n_splits * D);
+#pragma unroll
+    for (int i = lane; i < G * 32; i += 64) {
+      const int h = i >> 5;
+      const int c = i & 31;
+      float4 O;
+      float L, M;
+      merge_waves4<G>(s_acc, s_m, s_l, h, c, O, L, M);
+      const int slot = h * n_splits + split;  // within this KV head's partials
+      store4_agent(ro, static_cast<unsigned>(sizeof(float) * (slot * D + 4 * c)), O);
+      if (c == 0) store2_agent(part_ml + 2 * (static_cast<size_t>(g * G) * n_splits + slot), M, L);
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    if (lane == 0) {
+      int *ctr = counters + static_cast<size_t>(g) * kCounterStride;
+      const int before =
+          __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = (before == n_splits - 1);
+      if (s_last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
   __syncthreads();
   if (!s_last) return;
+  __shared__ __attribute__((aligned(16))) MergeLds s_merge;
   merge_splits<G>(part_ml, part_o, out, g, n_splits, s_merge);
 }
 

@@ -49,6 +49,15 @@ __device__ __forceinline__ float half_wave_sum(float v) {
   return v;
 }
 
+// The values of x in lanes i % 32 (.x) and 32 + i % 32 (.y), in every lane i:
+// one v_permlane32_swap (lanes 32..63 of a copy trade places with lanes
+// 0..31 of another), no LDS.
+__device__ __forceinline__ float2 halves(float x) {
+  const auto a =
+      __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return make_float2(__uint_as_float(a[0]), __uint_as_float(a[1]));
+}
+
 __device__ __forceinline__ float wave_max(float v) {
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
   return v;

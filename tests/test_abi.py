@@ -125,19 +125,26 @@ def test_gemm_rejects_bad_arguments_without_launching():
     assert call(m=2**40) == -errno.EOVERFLOW
 
 
+def decode_ws_bytes(n_head, n_head_kv, n_splits):
+    """The decode workspace of n_splits splits: one 256-byte counter slot per
+    KV head, then one (max, sum) pair and one 128-float output per (query
+    head, split), the regions 256-byte aligned."""
+    a256 = lambda b: (b + 255) // 256 * 256  # noqa: E731
+    return a256(256 * n_head_kv) + a256(8 * n_head * n_splits) + 4 * 128 * n_head * n_splits
+
+
 def test_decode_plan_stays_within_one_workgroup_per_cu():
-    # (host arithmetic) a workspace holds n_head x n_splits partial rows of
-    # 128 floats past a fixed region, so its size tells the split count. The
-    # plan never goes past 256 workgroups (32 splits x 8 KV heads): a 33rd
-    # split per head put a second full split on some CUs, which then set the
+    # (host arithmetic) the workspace size tells the split count. The plan
+    # never goes past 256 workgroups (32 splits x 8 KV heads): a 33rd split
+    # per head put a second full split on some CUs, which then set the
     # kernel's end. ctx 4096 (4097 keys) takes 26 splits of 5 tiles.
     for n_head in (16, 32):
-        ws = lambda n: ikv.decode_workspace_bytes(n_head, 8, 128, n)
-        row = 4 * n_head * 128
+        ws = lambda n: ikv.decode_workspace_bytes(n_head, 8, 128, n)  # noqa: E731
         peak = ws(2048)  # 32 splits of 64 keys
+        assert peak == decode_ws_bytes(n_head, 8, 32)
         assert all(ws(n) <= peak for n in range(129, 50001, 3))
         assert ws(20000) == peak and ws(40000) == peak
-        assert peak - ws(4097) == 6 * row
+        assert ws(4097) == decode_ws_bytes(n_head, 8, 26)
 
 
 def test_decode_replay_limit_tracks_the_split_plan():

@@ -174,6 +174,25 @@ def test_decode_workspace_reuse_is_deterministic(dev):
         assert np.array_equal(bits(got.cpu().numpy()), bits(fresh.cpu().numpy())), n
 
 
+def test_decode_workspace_shared_across_group_sizes(dev):
+    # One workspace through query-head counts over the same 8 KV heads: the
+    # partials' layout changes from launch to launch, the counters stay put
+    # and every launch leaves them at zero, so each launch equals a fresh one.
+    g = gen(91)
+    shapes = [(32, 8, 4097), (16, 8, 8200), (64, 8, 3001), (32, 8, 3000), (16, 8, 8200),
+              (8, 8, 5000), (16, 8, 2049), (64, 8, 12000), (16, 8, 8200)]
+    cases = []
+    for hq, hkv, n in shapes:
+        cases.append((rand(g, (hq, D)), rand(g, (n, hkv, D)), rand(g, (n, hkv, D)), n))
+    nbytes = max(ikv.decode_workspace_bytes(q.shape[0], k.shape[1], D, n) for q, k, _, n in cases)
+    ws = torch.zeros((nbytes + 3) // 4, device=dev)
+    for i, (q, k, v, n) in enumerate(cases):
+        got = ikv.attn_decode(q, k, v, n, workspace=ws).clone()
+        fresh = ikv.attn_decode(q, k, v, n)
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(got.cpu().numpy()), bits(fresh.cpu().numpy())), (i, shapes[i])
+
+
 # ---------------------------------------------------------------------------
 # prefill attention (MFMA)
 # ---------------------------------------------------------------------------

@@ -1,5 +1,5 @@
-"""The publish order of the in-kernel merges, checked in the gfx950 code this
-build's compiler emits (CPU only: hipcc cross-compiles to assembly).
+"""The publish protocols of the in-kernel merges, checked in the gfx950 code
+this build's compiler emits (CPU only: hipcc cross-compiles to assembly).
 
 The split decode (attn_decode.hip: decode_kernel, qkv_attn_kernel) and the
 multi-workgroup sampler (model_ops.hip: argmax_ws_kernel) publish partial
@@ -7,13 +7,14 @@ results with agent-coherent stores and then count their workgroup in an
 arrival counter with a relaxed agent-scope atomic; the workgroup that counts
 last reads every partial back. What makes that correct on gfx950 is the code
 between the two: the stores carry the coherence bit (sc1), and a
-`s_waitcnt vmcnt(0)` (CDNA counts stores in vmcnt) and the workgroup barrier
-come after the last of them and before the atomic (the barrier where
-several threads store and one counts). A release fence would
-express the same order in the HIP memory model, but on this chip it writes
-back the L2 (measured ~6 us per launch), so the kernels rely on the emitted
-order instead, and this test pins it: a compiler that moved the atomic above
-the wait, or dropped sc1 from the stores, fails here before it can corrupt a
+`s_waitcnt vmcnt(0)` (CDNA counts stores in vmcnt) comes after the last of
+them and before the atomic, and so does the workgroup barrier where several
+wavefronts store and one counts (qkv_attn_kernel; in decode_kernel one
+wavefront stores every partial and counts). A release fence would express
+the same order in the HIP memory model, but on this chip it writes back the
+L2 (measured ~6 us per launch), so the kernels rely on the emitted order
+instead, and this test pins it: a compiler that moved the atomic above the
+wait, or dropped sc1 from the stores, fails here before it can corrupt a
 merge on the GPU.
 """
 import pathlib
@@ -81,7 +82,10 @@ def test_split_decode_publishes_before_counting(tmp_path):
     asm = device_asm(CSRC / "attn_decode.hip", tmp_path)
     checked = 0
     for name, body in functions(asm):
-        if "decode_kernel" in name or "qkv_attn_kernel" in name:
+        if "decode_kernel" in name:
+            check_publish_order(name, body, many_writers=False)  # wave 0 stores and counts
+            checked += 1
+        elif "qkv_attn_kernel" in name:
             check_publish_order(name, body)
             checked += 1
     # decode_kernel<G, PRO, PAGED> for G in 1, 2, 4, 8 and qkv_attn_kernel<G>
