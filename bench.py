@@ -328,7 +328,7 @@ def hbm_probes(torch, ikv):
     per kernel, 28 rotating buffers, HIP graph), and an empty kernel."""
     import ctypes
 
-    lib = ikv.load()
+    lib = ikv.load_bench()
     dev = torch.device("cuda:0")
     sink = torch.empty(16384, device=dev)
     res = {}
@@ -387,6 +387,85 @@ def hbm_probes(torch, ikv):
     res["empty_kernel_us"] = round(timed_graph(empties, 5) / 200 * 1e6, 2)
     torch.cuda.empty_cache()
     return res
+
+
+def decode_timeline(torch, ikv, ctx=4096, n_head=N_HEAD, n_layer=N_LAYER, reps=30):
+    """Phase timeline of one decode launch: the same workload as the headline
+    (n_layer rotating caches at ctx, HIP graph), run through the stamped build
+    of the decode kernels in libikv_bench.so. Each workgroup records the
+    100 MHz s_memrealtime count at its entry, first tile scored, last tile
+    scored (every wave), waves merged, partial published, arrival counted and
+    (the merging workgroup) merge done; the records of the step's last launch
+    are read after each of `reps` steps. Times are us from the launch's first
+    workgroup entry, medians over the steps; the stamps add a little work, so
+    the stamped launch runs slightly longer than the product one."""
+    import ctypes
+    import numpy as np
+    blib = ikv.load_bench()
+    rig = DecodeRig(torch, ikv, ctx, n_layer=n_layer, n_head=n_head)
+    rig.lib = blib
+    rig.capture()
+    stamped_us = rig.time(20, 5) / 20 / n_layer * 1e6
+    words = 1024 * 16
+    recs = []
+    for _ in range(reps):
+        if blib.ikv_bench_timeline_clear() != 0:
+            raise RuntimeError("ikv_bench_timeline_clear")
+        rig.run(1)
+        torch.cuda.synchronize()
+        h = (ctypes.c_ulonglong * words)()
+        if blib.ikv_bench_timeline_read(h, words) != 0:
+            raise RuntimeError("ikv_bench_timeline_read")
+        a = np.array(h, dtype=np.int64).reshape(1024, 16)
+        recs.append(a[a[:, 0] > 0])
+    del rig
+    torch.cuda.empty_cache()
+
+    def us(x):
+        return round(float(x) / 100.0, 2)  # 100 MHz ticks -> us
+
+    keys = ("first_entry_max", "first_tile_min", "first_tile_med", "first_tile_max",
+            "stream_end_min", "stream_end_med", "stream_end_max", "slowest_wave_max",
+            "wave_spread_med", "waves_merged_after_slowest_wave_med", "publish_med",
+            "arrival_atomic_med", "merge_med", "merge_max", "last_merge_end")
+    per = {k: [] for k in keys}
+    for a in recs:
+        t0 = a[:, 0].min()
+        t = a[:, :7] - t0
+        role = (a[:, 7] >> 8) & 0xFF
+        waves = a[:, 8:16]
+        wv = np.where(waves > 0, waves - t0, 0)
+        slowest = wv.max(axis=1)
+        fastest = np.where(waves > 0, wv, np.iinfo(np.int64).max).min(axis=1)
+        split = role != 2
+        m = role == 1
+        per["first_entry_max"].append(t[:, 0].max())
+        per["first_tile_min"].append(t[:, 1].min())
+        per["first_tile_med"].append(np.median(t[:, 1]))
+        per["first_tile_max"].append(t[:, 1].max())
+        per["stream_end_min"].append(t[:, 2].min())
+        per["stream_end_med"].append(np.median(t[:, 2]))
+        per["stream_end_max"].append(t[:, 2].max())
+        per["slowest_wave_max"].append(slowest.max())
+        per["wave_spread_med"].append(np.median(slowest - fastest))
+        per["waves_merged_after_slowest_wave_med"].append(np.median(t[:, 3] - slowest))
+        if split.any():
+            per["publish_med"].append(np.median(t[split, 4] - t[split, 3]))
+            per["arrival_atomic_med"].append(np.median(t[split, 5] - t[split, 4]))
+        if m.any():
+            per["merge_med"].append(np.median(t[m, 6] - t[m, 5]))
+            per["merge_max"].append((t[m, 6] - t[m, 5]).max())
+            per["last_merge_end"].append(t[m, 6].max())
+    out = {"ctx": ctx, "n_head": n_head, "workgroups": int(len(recs[-1])),
+           "stamped_launch_us": round(stamped_us, 2)}
+    for k, v in per.items():
+        out[k + "_us"] = us(np.median(v)) if v else None
+    # workgroup w = split * n_head_kv + kv head: do a KV head's splits share one XCD?
+    xcc = (recs[-1][:, 7] & 15)
+    n_kv_heads = N_HEAD_KV
+    same = all(len(set(xcc[g::n_kv_heads].tolist())) == 1 for g in range(n_kv_heads))
+    out["kv_head_splits_share_one_xcc"] = bool(same)
+    return out
 
 
 def pmc_per_dispatch(csv_path, kernel_substr):
@@ -716,6 +795,9 @@ def main():
     ap.add_argument("--gemm-only", action="store_true",
                     help="only the prefill projection GEMMs of configs 3 and 4 against the "
                          "vendor BLAS; prints their JSON")
+    ap.add_argument("--timeline-only", action="store_true",
+                    help="only the decode phase timeline (stamped build, libikv_bench.so); "
+                         "prints its JSON")
     ap.add_argument("--probes-only", action="store_true",
                     help="only the HBM / launch probes; prints their JSON")
     ap.add_argument("--pmc-calibrate", action="store_true",
@@ -752,6 +834,11 @@ def main():
     if args.probes_only:
         print(json.dumps(hbm_probes(torch, ikv)), flush=True)
         return
+    if args.timeline_only:
+        print(json.dumps({"decode_timeline": [decode_timeline(torch, ikv, args.ctx),
+                                              decode_timeline(torch, ikv, args.ctx, n_head=32,
+                                                              n_layer=36)]}), flush=True)
+        return
     if args.gemm_only:
         print(json.dumps({"prefill_gemm": gemm_table(torch, ikv)}), flush=True)
         return
@@ -786,6 +873,7 @@ def main():
     extra = {"repeats": None, "eager_gbs": None, "ctx_sweep_gbs": {}, "short_ctx_us": {},
              "g4_ctx4096": None, "paged_ctx4096_gbs": {},
              "mall_hot_gbs": None, "prefill": {}, "prefill_gemm": None, "hbm_probes": None,
+             "decode_timeline": None,
              "model": None,
              "cpu_sweep": None}
     if not args.no_extra:
@@ -843,6 +931,8 @@ def main():
         del hot
         extra["hbm_probes"] = hbm_probes(torch, ikv)
         log(f"[bench] hbm probes: {extra['hbm_probes']}")
+        extra["decode_timeline"] = decode_timeline(torch, ikv, args.ctx)
+        log(f"[bench] decode timeline: {extra['decode_timeline']}")
         for p in (32, 64, 128, 256, 2048):
             t = time_prefill(torch, ikv, p, 20 if p < 2048 else 10)
             tf = prefill_flops(p) / t / 1e12

@@ -1,5 +1,5 @@
 // probe.hip — bandwidth and launch-cost probes for the benchmark (see
-// include/ikv_probe.h). Not on the KV-cache path.
+// ikv_bench.h). Not on the KV-cache path: built into libikv_bench.so only.
 //
 // The streaming-read probe is shaped like the decode kernel so that its time
 // is a floor for one launch that reads the same bytes: workgroups of 512
@@ -7,8 +7,8 @@
 // owns a token range), and every lane issuing U independent 16-byte
 // non-temporal loads before it uses any, so a workgroup's whole slice is in
 // flight at once when it fits U loads per lane.
-#include "ikv_common.hpp"
-#include "../../include/ikv_probe.h"
+#include "../csrc/ikv_common.hpp"
+#include "ikv_bench.h"
 
 #include <climits>
 

@@ -52,6 +52,48 @@
 
 namespace {
 
+// Phase timeline of the split decode, for the bench-only build of this file
+// (IKV_DECODE_TIMELINE=1, libikv_bench.so; the product library has none of
+// it): per workgroup, the 100 MHz s_memrealtime count at its entry, its first
+// tile scored, its last tile scored (wave 0, and every wave), the waves
+// merged in LDS, its partial published, the arrival counted, and (the
+// merging workgroup) the merge done and its output stored.
+#ifndef IKV_DECODE_TIMELINE
+#define IKV_DECODE_TIMELINE 0
+#endif
+constexpr int kTimelineWgs = 1024;
+constexpr int kTimelineWords = 16;
+#if IKV_DECODE_TIMELINE
+__device__ unsigned long long g_timeline[kTimelineWgs * kTimelineWords];
+#endif
+struct Timeline {
+#if IKV_DECODE_TIMELINE
+  unsigned long long t[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  bool first_done = false;
+  __device__ void stamp(int i) { t[i] = __builtin_amdgcn_s_memrealtime(); }
+  __device__ void first() {
+    if (!first_done) stamp(1);
+    first_done = true;
+  }
+  __device__ void wave_done(int slot, int wave) {
+    if ((threadIdx.x & 63) == 0 && slot < kTimelineWgs)
+      g_timeline[static_cast<size_t>(slot) * kTimelineWords + 8 + wave] = t[2];
+  }
+  // thread 0 writes the record; role 0 published, 1 merged, 2 one split
+  __device__ void flush(int slot, int role) {
+    if (threadIdx.x != 0 || slot >= kTimelineWgs) return;
+    const unsigned xcc = __builtin_amdgcn_s_getreg((3 << 11) | 20) & 15;  // HW_REG_XCC_ID
+    t[7] = xcc | (static_cast<unsigned long long>(role) << 8);
+    for (int i = 0; i < 8; ++i) g_timeline[static_cast<size_t>(slot) * kTimelineWords + i] = t[i];
+  }
+#else
+  __device__ void stamp(int) {}
+  __device__ void first() {}
+  __device__ void wave_done(int, int) {}
+  __device__ void flush(int, int) {}
+#endif
+};
+
 constexpr int D = 128;  // head_dim supported by this kernel
 #ifndef IKV_DECODE_NWAVE
 #define IKV_DECODE_NWAVE 8
@@ -599,6 +641,9 @@ __device__ __forceinline__ void decode_body(
   const int wave = tid >> 6;
   const int half = lane >> 5;
   const int sub = lane & 31;
+  Timeline tl;
+  tl.stamp(0);
+  const int tl_slot = split * n_head_kv + g;
   const int t_begin = split * tokens_per_split;
   const int t_end = min(n_kv, t_begin + tokens_per_split);
   const int new_row = k_new ? n_kv - 1 : -1;
@@ -704,6 +749,7 @@ __device__ __forceinline__ void decode_body(
       }
       m[h] = mx;
     }
+    tl.first();
   };
   // Ping-pong over the split's tiles. The tail cases get their own calls so
   // that on every path the next tile's loads are issued unconditionally
@@ -726,6 +772,8 @@ __device__ __forceinline__ void decode_body(
     process(kb, vb, base + TILE);
   }
 
+  tl.stamp(2);
+  tl.wave_done(tl_slot, wave);
   // The append: the split holding the new token writes its K (rotated when
   // RoPE is folded in) and V rows into the caches, 16 bytes per lane of the
   // first half-wave.
@@ -773,6 +821,7 @@ __device__ __forceinline__ void decode_body(
     }
   }
   __syncthreads();
+  tl.stamp(3);
 
   // Merge the waves. With one split the result is final.
   if (n_splits == 1) {
@@ -783,6 +832,7 @@ __device__ __forceinline__ void decode_body(
       merge_waves<G>(s_acc, s_m, s_l, h, d, O, L, M);
       out[static_cast<size_t>(g * G + h) * D + d] = O / L;
     }
+    tl.flush(tl_slot, 2);
     return;
   }
   // Publish: wave 0 merges the waves and stores the workgroup's (max, sum,
@@ -808,6 +858,7 @@ __device__ __forceinline__ void decode_body(
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(0);
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    tl.stamp(4);
     if (lane == 0) {
       int *ctr = counters + static_cast<size_t>(g) * kCounterStride;
       const int before =
@@ -817,9 +868,19 @@ __device__ __forceinline__ void decode_body(
     }
   }
   __syncthreads();
-  if (!s_last) return;
+  tl.stamp(5);
+  if (!s_last) {
+    tl.flush(tl_slot, 0);
+    return;
+  }
   __shared__ __attribute__((aligned(16))) MergeLds s_merge;
   merge_splits<G>(part_ml, part_o, out, g, n_splits, s_merge);
+#if IKV_DECODE_TIMELINE
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  tl.stamp(6);
+  tl.flush(tl_slot, 1);
+#endif
 }
 
 template <int G, bool PRO, bool PAGED>
@@ -1268,3 +1329,16 @@ extern "C" int ikv_attn_decode_noalloc_f32(const float *q, float *k_cache, float
                        scale, ws, kNoAllocScratchBytes, nullptr, nullptr, stream,
                        /*clear_counters=*/true);
 }
+
+#if IKV_DECODE_TIMELINE
+// Copies the phase records of the last decode launch (kTimelineWgs x 16
+// words, workgroup split * n_head_kv + g) to host memory, or zeroes them.
+extern "C" int ikv_bench_timeline_read(unsigned long long *dst, size_t n_words) {
+  if (!dst || n_words > static_cast<size_t>(kTimelineWgs) * kTimelineWords) return -EINVAL;
+  return static_cast<int>(hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_timeline), n_words * 8));
+}
+extern "C" int ikv_bench_timeline_clear() {
+  static unsigned long long zeros[kTimelineWgs * kTimelineWords];
+  return static_cast<int>(hipMemcpyToSymbol(HIP_SYMBOL(g_timeline), zeros, sizeof(zeros)));
+}
+#endif

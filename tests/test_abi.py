@@ -31,6 +31,25 @@ def test_every_declared_entry_point_is_exported():
     assert set(ikv.SIGNATURES) | set(qwen3.ENGINE_SIGNATURES) == set(declared)
 
 
+def test_measurement_code_lives_in_the_bench_library():
+    # libikv.so exports the path's ABI only; the probes and the stamped decode
+    # build are in libikv_bench.so, which bench.py loads beside it
+    def exported(path):
+        out = subprocess.run(["nm", "-D", "--defined-only", str(path)], capture_output=True,
+                             text=True, check=True).stdout
+        return {line.split()[-1] for line in out.splitlines() if line.strip()}
+
+    product = exported(ikv.LIB_PATH)
+    assert not {n for n in product if n.startswith(("ikv_probe_", "ikv_bench_"))}
+    text = re.sub(r"/\*.*?\*/", "", ikv.BENCH_HEADER.read_text(), flags=re.S)
+    declared = set(re.findall(r"\b(ikv_[a-z0-9_]+)\s*\(", text))
+    assert declared == set(ikv.BENCH_SIGNATURES)
+    bench = exported(ikv.BENCH_LIB_PATH)
+    assert declared <= bench
+    assert "ikv_attn_decode_f32" in bench  # the stamped decode build
+    ikv.load_bench()
+
+
 def test_library_does_not_link_the_oracle():
     deps = subprocess.run(["ldd", str(ikv.LIB_PATH)], capture_output=True, text=True).stdout
     assert "oracle" not in deps
