@@ -261,42 +261,51 @@ GEMM_SHAPES = [
 ]
 
 
-def gemm_table(torch, ikv):
-    """ikv.mul_mat (the MFMA GEMM from 2048 tokens on) against torch.mm (the
-    vendor BLAS) at GEMM_SHAPES: each timed as a HIP graph of several
-    launches, best of three alternated rounds, after ~2 s of large products
-    to bring the clocks up (the first product timed cold ran ~10% slow)."""
+def graph_us(torch, fn, reps):
+    """us per call of fn, captured `reps` times in a HIP graph, 3 replays."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    # captured on the stream of the warm-up call (a split-K product allocates
+    # its stream's workspace on its first call, outside capture)
+    with torch.cuda.graph(g, stream=side):
+        for _ in range(reps):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(3):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (3 * reps)
+
+
+def warm_clocks(torch, seconds=2.0):
+    """~2 s of large products to bring the clocks up (the first product timed
+    cold ran ~10% slow)."""
     import time
-    dev = torch.device("cuda:0")
-    a = torch.randn(4096, 4096, device=dev)
+    a = torch.randn(4096, 4096, device="cuda:0")
     t0 = time.time()
-    while time.time() - t0 < 2.0:
+    while time.time() - t0 < seconds:
         for _ in range(20):
             torch.mm(a, a)
         torch.cuda.synchronize()
     del a
 
-    def graph_us(fn, reps):
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side):
-            fn()
-        torch.cuda.current_stream().wait_stream(side)
-        torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            for _ in range(reps):
-                fn()
-        g.replay()
-        torch.cuda.synchronize()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(3):
-            g.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) * 1e3 / (3 * reps)
+
+def gemm_table(torch, ikv):
+    """ikv.mul_mat (the MFMA GEMM from 2048 tokens on) against torch.mm (the
+    vendor BLAS) at GEMM_SHAPES: each timed as a HIP graph of several
+    launches, best of three alternated rounds, after warming the clocks."""
+    dev = torch.device("cuda:0")
+    warm_clocks(torch)
 
     rows = {}
     for name, n, k, m in GEMM_SHAPES:
@@ -307,8 +316,8 @@ def gemm_table(torch, ikv):
         reps = 10 if n * k * m < 1e10 else 3
         ours, blas = [], []
         for _ in range(3):
-            ours.append(graph_us(lambda: ikv.mul_mat(w, x, out=out), reps))
-            blas.append(graph_us(lambda: torch.mm(x, w.t(), out=ref), reps))
+            ours.append(graph_us(torch, lambda: ikv.mul_mat(w, x, out=out), reps))
+            blas.append(graph_us(torch, lambda: torch.mm(x, w.t(), out=ref), reps))
         o, b = min(ours), min(blas)
         tf = 2 * n * k * m / o / 1e6
         rows[name] = {"n_out": n, "k": k, "tokens": m, "us": round(o, 1), "tflops": round(tf, 1),
@@ -318,6 +327,81 @@ def gemm_table(torch, ikv):
         log(f"[bench] gemm {name}: {o:.1f} us ({tf:.1f} TF/s), torch.mm {b:.1f} us, "
             f"ratio {o / b:.3f}")
         del w, x, out, ref
+        torch.cuda.empty_cache()
+    return rows
+
+
+# (name, n_out, k) of the Qwen3 projections
+PROJECTIONS = [("0.6B q", 2048, 1024), ("0.6B k/v", 1024, 1024), ("0.6B o", 1024, 2048),
+               ("0.6B gate/up", 3072, 1024), ("0.6B down", 1024, 3072),
+               ("8B q/o", 4096, 4096), ("8B k/v", 1024, 4096), ("8B gate/up", 12288, 4096),
+               ("8B down", 4096, 12288)]
+GEMM_TILES = ["128x128", "64x64", "64x32", "32x64", "32x32"]
+
+
+def gemm_sweep(torch, ikv, tokens=(65, 128, 256, 512, 1024, 2047)):
+    """Every tile shape of the prefill GEMM (libikv_bench.so), each with K
+    split 1-8 ways (up to 2048 workgroups), against torch.mm
+    and ikv.mul_mat's own plan, on the Qwen3 projections at prompt lengths
+    below the headline's: us per product (HIP graph of several launches,
+    best of three rounds)."""
+    import ctypes
+    blib = ikv.load_bench()
+    dev = torch.device("cuda:0")
+    warm_clocks(torch)
+    ws = torch.zeros((16 << 10) + (8 << 20), dtype=torch.uint8, device=dev)
+    rows = []
+    for name, n, k in PROJECTIONS:
+        w = torch.randn(n, k, device=dev) * 0.02
+        for m in tokens:
+            x = torch.randn(m, k, device=dev)
+            out = torch.empty(m, n, device=dev)
+            ref = torch.empty(m, n, device=dev)
+            reps = 10 if n * k * m < 1e10 else 3
+
+            def tile_fn(t, sk):
+                def f():
+                    rc = blib.ikv_bench_gemm_nt_tile_f32(w.data_ptr(), x.data_ptr(), out.data_ptr(),
+                                                         n, k, m, None, t, sk, ws.data_ptr(),
+                                                         ws.numel(),
+                                                         torch.cuda.current_stream().cuda_stream)
+                    if rc:
+                        raise RuntimeError(f"tile {t} split {sk}: {rc}")
+                return f
+            tile, split = ctypes.c_int(), ctypes.c_int()
+            if blib.ikv_bench_gemm_plan(n, k, m, ctypes.byref(tile), ctypes.byref(split)):
+                raise RuntimeError("gemm plan")
+            row = {"proj": name, "n_out": n, "k": k, "tokens": m,
+                   "plan": f"{GEMM_TILES[tile.value]}/s{split.value}"}
+            row["torch_mm_us"] = round(min(graph_us(torch, lambda: torch.mm(x, w.t(), out=ref), reps)
+                                           for _ in range(3)), 2)
+            row["mul_mat_us"] = round(min(graph_us(torch, lambda: ikv.mul_mat(w, x, out=out), reps)
+                                          for _ in range(3)), 2)
+            row["mul_mat_vs_torch"] = round(row["mul_mat_us"] / row["torch_mm_us"], 3)
+            cands = []
+            for t, tname in enumerate(GEMM_TILES):
+                if t == 0 and n % 128:
+                    continue
+                bm, bn = (int(v) for v in tname.split("x"))
+                n_tiles = -(-m // bm) * (n // bn)
+                cands.append((t, 1, tname))
+                cands += [(t, sk, f"{tname}/s{sk}") for sk in (2, 3, 4, 5, 6, 8)
+                          if k // 64 >= 4 * sk and n_tiles * sk <= 2048
+                          and n_tiles * sk * bm * bn * 4 <= (8 << 20)]
+            for t, sk, key in cands:
+                row[key] = round(min(graph_us(torch, tile_fn(t, sk), reps) for _ in range(3)), 2)
+            # again after the candidates (the clocks drift over a row)
+            row["mul_mat_us"] = min(row["mul_mat_us"], round(min(
+                graph_us(torch, lambda: ikv.mul_mat(w, x, out=out), reps) for _ in range(3)), 2))
+            row["mul_mat_vs_torch"] = round(row["mul_mat_us"] / row["torch_mm_us"], 3)
+            best = min((key for _, _, key in cands), key=lambda c: row[c])
+            row["best"] = best
+            row["best_vs_torch"] = round(row[best] / row["torch_mm_us"], 3)
+            rows.append(row)
+            log(f"[bench] sweep {name} m={m}: torch {row['torch_mm_us']} mul_mat {row['mul_mat_us']} "
+                f"({row['plan']}) best {best} {row[best]}")
+            del x, out, ref
+        del w
         torch.cuda.empty_cache()
     return rows
 
@@ -607,8 +691,53 @@ def model_bench(configs, cpu_tokens):
         log(f"[bench] cpu config 0: TPOT {res['cpu_config0']['tpot_ms']} ms on {threads} threads, "
             f"tokens equal GPU: {res['cpu_config0']['tokens_equal_gpu_prefix']}")
         del w, orc
+    if 0 in configs:
+        res["published_profile"] = published_bench()
     if 3 in configs:
         res["config3_offload_2seq"] = offload_bench()
+    return res
+
+
+# The reference's published CUDA table (RTX 4060 Laptop, real Qwen3-0.6B
+# weights): docs/performance/cuda-contiguous-kv-20261107/README.md:34-37.
+PUBLISHED_REF = {32: (220.50, 17.94), 64: (423.20, 17.88), 128: (837.00, 24.68),
+                 256: (1737.24, 28.12)}  # prompt -> (TTFT ms, TPOT ms)
+
+
+def published_bench(prompts=(32, 64, 128, 256), n_gen=128):
+    """The reference's published benchmark profile on this engine: Qwen3-0.6B
+    F32 (config 0's synthetic weights), prompt ids (100 + i) % n_vocab
+    (benchmarks/cpu/bench.cpp:393), 128 greedy tokens with no EOS stop, one
+    warm-up and three timed runs per prompt length, mean and sample standard
+    deviation of TTFT and TPOT as the reference's table reports them."""
+    from ikv import qwen3, synth
+
+    cfg = qwen3.QWEN3_0_6B
+    res = {}
+    for P in prompts:
+        eng = qwen3.Qwen3Engine(cfg, P + n_gen)
+        eng.init_synthetic(synth.config_seed(0, 1), threads=16)
+        prompt = [(100 + i) % cfg.n_vocab for i in range(P)]
+        eng.generate(prompt, n_gen)  # warm-up, a whole run
+        runs = [eng.generate(prompt, n_gen) for _ in range(3)]
+        eng.close()
+        toks = runs[0][0]
+        if any(r[0] != toks for r in runs[1:]):
+            raise RuntimeError(f"published P={P}: repeated runs gave different tokens")
+        ttft = [r[1].ttft_s * 1e3 for r in runs]
+        tpot = [r[1].tpot_s * 1e3 for r in runs]
+        ref_ttft, ref_tpot = PUBLISHED_REF.get(P, (None, None))
+        res[f"P{P}"] = {
+            "ttft_ms": round(statistics.mean(ttft), 3), "ttft_std_ms": round(statistics.stdev(ttft), 3),
+            "tpot_ms": round(statistics.mean(tpot), 4), "tpot_std_ms": round(statistics.stdev(tpot), 4),
+            "decode_tok_s": round(1e3 / statistics.mean(tpot), 1),
+            "token_checksum": str(token_checksum(toks)),
+            "reference_rtx4060_ttft_ms": ref_ttft, "reference_rtx4060_tpot_ms": ref_tpot,
+        }
+        log(f"[bench] published profile P={P}, N={n_gen}: TTFT {res[f'P{P}']['ttft_ms']} ms, "
+            f"TPOT {res[f'P{P}']['tpot_ms']} ms (means of 3)")
+    res["note"] = ("synthetic weights, so the tokens and checksums differ from the reference's "
+                   "(real weights); its times are an RTX 4060 Laptop's")
     return res
 
 
@@ -798,6 +927,9 @@ def main():
     ap.add_argument("--timeline-only", action="store_true",
                     help="only the decode phase timeline (stamped build, libikv_bench.so); "
                          "prints its JSON")
+    ap.add_argument("--gemm-sweep", action="store_true",
+                    help="only the prefill GEMM's tile shapes against torch.mm on the Qwen3 "
+                         "projections below 2048 tokens; prints their JSON")
     ap.add_argument("--probes-only", action="store_true",
                     help="only the HBM / launch probes; prints their JSON")
     ap.add_argument("--pmc-calibrate", action="store_true",
@@ -838,6 +970,9 @@ def main():
         print(json.dumps({"decode_timeline": [decode_timeline(torch, ikv, args.ctx),
                                               decode_timeline(torch, ikv, args.ctx, n_head=32,
                                                               n_layer=36)]}), flush=True)
+        return
+    if args.gemm_sweep:
+        print(json.dumps({"gemm_sweep": gemm_sweep(torch, ikv)}), flush=True)
         return
     if args.gemm_only:
         print(json.dumps({"prefill_gemm": gemm_table(torch, ikv)}), flush=True)

@@ -100,7 +100,9 @@ int ikv_attn_decode_f32(const float *q, float *k_cache, float *v_cache, const fl
  * runs on until the process ends. Every call on one device shares that
  * array, so calls that overlap on one device race (order them on one
  * stream). Each call clears the counters it needs with a fill kernel on
- * `stream` before the attention launch. Returns -ENOSPC when
+ * `stream` before the attention launch (no memset, so the call may be
+ * captured in a HIP graph). The first call on a device looks up the array's
+ * address there (hipGetSymbolAddress), so make it outside stream capture. Returns -ENOSPC when
  * ikv_attn_decode_workspace_bytes() of the shape exceeds that size (every
  * supported shape of up to 128 KV heads fits). Other arguments, results and
  * return codes as for ikv_attn_decode_f32: the output and cache rows are

@@ -131,6 +131,18 @@ int ikv_qwen3_set_fusion(ikv_qwen3 *m, int on);
  * src/model.cpp:164-311). No counterpart in the reference. */
 int ikv_qwen3_set_step_replay(ikv_qwen3 *m, int on);
 
+/* Keep, during each later ikv_qwen3_generate, the logits the greedy sampler
+ * reads at each of the n_steps steps (step 0 samples from the prompt's last
+ * logits row, step i > 0 from decode step i), for checks at logit level; the
+ * reference's sampler reads the same row (src/sampler.cpp:5-35). The rows
+ * are copied on the device stream after their step, outside any captured
+ * graph, into a device buffer of n_steps x n_vocab floats that this call
+ * allocates (n_steps = 0 frees it and keeps none). ikv_qwen3_captured_logits
+ * copies them to host memory in the order of `steps`; count must be n_steps
+ * x n_vocab. No counterpart in the reference. */
+int ikv_qwen3_capture_logits(ikv_qwen3 *m, const int64_t *steps, int64_t n_steps);
+int ikv_qwen3_captured_logits(const ikv_qwen3 *m, float *host, size_t count);
+
 void ikv_qwen3_destroy(ikv_qwen3 *m);
 
 #ifdef __cplusplus

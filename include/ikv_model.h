@@ -29,12 +29,15 @@ extern "C" {
  * src/backends/cpu_backend.cpp:386-424; x: [m][k]; out: [m][n_out]).
  * m == 1 (decode) runs a hand-written streaming GEMV. 2 <= m <= 64 with
  * n_out % 16 == 0, k % 1024 == 0 and 16-byte aligned w and x runs a
- * hand-written F32 MFMA kernel (deterministic: fixed reduction order).
- * m >= 2048 with n_out % 64 == 0, k % 64 == 0 and 16-byte aligned w and x
- * runs ikv_gemm_nt_f32. Other m > 1 run rocBLAS SGEMM (full F32); the first
- * such call on a device creates that device's rocBLAS handle (kept until
- * exit), and calls that share a device must come from one host thread at a
- * time.
+ * hand-written F32 MFMA kernel. Other m > 1 with n_out % 64 == 0,
+ * k % 64 == 0 and 16-byte aligned w and x run the tiled F32 MFMA GEMM of
+ * ikv_gemm_nt_f32, with K split over several workgroups when its tiles
+ * would leave compute units idle: such a call needs a split-K workspace of
+ * its device and stream, which the first one allocates (8 MiB + 16 KiB,
+ * kept until exit; so make it outside HIP graph capture; -ENOMEM after 64
+ * device-stream pairs). Any other shape runs one wavefront per output
+ * (m <= 65535, else -ENOTSUP). Every path is deterministic: a fixed
+ * summation order per output for given n_out, k and m.
  * residual: NULL, or [m][n_out] added to the result (out may equal
  * residual).
  * ------------------------------------------------------------------- */
@@ -45,7 +48,8 @@ int ikv_mul_mat_f32(const float *w, const float *x, float *out, int64_t n_out, i
  * CPUBackend::compute_mul_mat, src/backends/cpu_backend.cpp:386-424), for
  * any m >= 1: n_out % 64 == 0, k % 64 == 0, 16-byte aligned w and x (else
  * -ENOTSUP / -EINVAL, nothing launched). Deterministic (a fixed summation
- * order per output); allocates nothing. residual as for mul_mat. */
+ * order per output); never splits K, so it allocates nothing. residual as
+ * for mul_mat. */
 int ikv_gemm_nt_f32(const float *w, const float *x, float *out, int64_t n_out, int64_t k,
                     int64_t m, const float *residual, void *stream);
 

@@ -7,7 +7,8 @@
  *    nominal peaks: a streaming read of any size (a long one, and one the
  *    size of a decode layer, 33.6 MB), and the cost of an empty kernel;
  *  - a build of the decode kernels (attn_decode.hip) with phase stamps, whose
- *    entry points are those of include/ikv.h, and the reader of the stamps.
+ *    entry points are those of include/ikv.h, and the reader of the stamps;
+ *  - the prefill GEMM (gemm.hip) on a chosen tile shape.
  * Conventions as in ikv.h (device pointers, stream as void*, 0 / -errno /
  * hipError_t).
  */
@@ -15,6 +16,7 @@
 #define IKV_BENCH_H
 
 #include <stddef.h>
+#include <stdint.h>
 
 #ifdef __cplusplus
 extern "C" {
@@ -42,6 +44,21 @@ int ikv_probe_empty(int grid, void *stream);
  * them. */
 int ikv_bench_timeline_read(unsigned long long *dst, size_t n_words);
 int ikv_bench_timeline_clear(void);
+
+/* ikv_gemm_nt_f32 (include/ikv_model.h) on tile shape `tile` (tokens x
+ * outputs: 0 128 x 128, 1 64 x 64, 2 64 x 32, 3 32 x 64, 4 32 x 32) with K
+ * split over n_split workgroups per tile (1 <= n_split <= k / 64), for the
+ * benchmark's sweep of the plans that ikv_mul_mat_f32 chooses among. For
+ * n_split > 1, ws holds 16 KiB of tile counters (zero before the first
+ * call; each call leaves them zero) followed by the partial tiles
+ * (ws_bytes in all); -EINVAL when they do not fit. */
+int ikv_bench_gemm_nt_tile_f32(const float *w, const float *x, float *out, int64_t n_out,
+                               int64_t k, int64_t m, const float *residual, int tile,
+                               int n_split, void *ws, size_t ws_bytes, void *stream);
+
+/* The plan ikv_mul_mat_f32 takes for an n_out x k x m product: tile code
+ * (as above) and K splits, written to *tile and *n_split. */
+int ikv_bench_gemm_plan(int64_t n_out, int64_t k, int64_t m, int *tile, int *n_split);
 
 #ifdef __cplusplus
 }

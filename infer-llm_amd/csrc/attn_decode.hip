@@ -43,6 +43,7 @@
 // cache is bit-identical to the one the separate ops produce. The prologue's
 // loads are issued first and the first tile's K/V loads right after them, so
 // the prologue's arithmetic runs while the tile is in flight.
+#include "coherent.hpp"
 #include "gemv_dev.hpp"
 #include "ikv_common.hpp"
 #include "../../include/ikv.h"
@@ -164,16 +165,16 @@ struct Prologue {
 
 // The context of a launch: n_kv, or with pro.dyn_max, pos[0] + 1. A
 // position outside [0, dyn_max) raises IKV_STATUS_POSITION and runs as
-// dyn_max keys, inside the planned splits.
+// dyn_max keys, inside the planned splits, with no append (*append false):
+// the cache keeps every committed row.
 // p: pos[0] when the launch is a replay form (loaded early by the caller).
-__device__ __forceinline__ int launch_n_kv(const Prologue &pro, int n_kv, int p) {
+__device__ __forceinline__ int launch_n_kv(const Prologue &pro, int n_kv, int p, bool &append) {
+  append = true;
   if (pro.dyn_max <= 0) return n_kv;
   if (p >= 0 && p < pro.dyn_max) return p + 1;
   if (threadIdx.x == 0) ikv::raise_status(pro.status, IKV_STATUS_POSITION);
+  append = false;
   return pro.dyn_max;
-}
-__device__ __forceinline__ int launch_n_kv(const Prologue &pro, int n_kv) {
-  return launch_n_kv(pro, n_kv, pro.dyn_max > 0 ? pro.pos[0] : 0);
 }
 
 // Contexts this short run as one split per KV head (and can fold into the
@@ -241,50 +242,15 @@ WsLayout ws_layout(int n_head, int n_head_kv, int n_splits) {
   return w;
 }
 
-// Stores and loads between the workgroups of a launch, coherent across the
-// XCDs of the device (agent scope): the stores are performed at the device's
-// coherence point and the loads (sc1) read from it, so no L2 writeback or
-// invalidate is needed on either side.
-__device__ __forceinline__ void store_agent(float *p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// A (max, sum) pair as one 8-byte store.
-__device__ __forceinline__ void store2_agent(float *p, float a, float b) {
-  const unsigned long long u = static_cast<unsigned long long>(__float_as_uint(a)) |
-                               (static_cast<unsigned long long>(__float_as_uint(b)) << 32);
-  __hip_atomic_store(reinterpret_cast<unsigned long long *>(p), u, __ATOMIC_RELAXED,
-                     __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Agent-coherent 8- and 16-byte loads and 16-byte stores through a buffer
-// resource over the partials (raw buffer: loads past num_records return
-// zeros).
-constexpr int kBufWord3 = 0x00020000;  // raw dword buffer, gfx9 family
-constexpr int kCpolSc1 = 16;           // cache policy: agent scope
-typedef float f2v __attribute__((ext_vector_type(2)));
-typedef float f4v __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t partial_rsrc(const float *base, size_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), 0,
-                                           static_cast<int>(bytes), kBufWord3);
-}
-__device__ __forceinline__ float2 load2_agent(__amdgpu_buffer_rsrc_t r, unsigned byte_off) {
-  const f2v v = __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, kCpolSc1);
-  return make_float2(v.x, v.y);
-}
-__device__ __forceinline__ float4 load4_agent(__amdgpu_buffer_rsrc_t r, unsigned byte_off) {
-  const f4v v = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kCpolSc1);
-  return make_float4(v.x, v.y, v.z, v.w);
-}
-__device__ __forceinline__ void store4_agent(__amdgpu_buffer_rsrc_t r, unsigned byte_off,
-                                             float4 v) {
-  const f4v x = {v.x, v.y, v.z, v.w};
-  __builtin_amdgcn_raw_buffer_store_b128(x, r, byte_off, 0, kCpolSc1);
-}
-// One float stored by another workgroup of this launch (on any XCD) before
-// it was counted: an agent-coherent load.
-__device__ __forceinline__ float load_agent(const float *p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
+using ikv::f2v;
+using ikv::f4v;
+using ikv::load2_agent;
+using ikv::load4_agent;
+using ikv::load_agent;
+using ikv::partial_rsrc;
+using ikv::store2_agent;
+using ikv::store4_agent;
+using ikv::store_agent;
 
 // Loads the K and V rows of tile `base` for this lane: row r of the lane is
 // token base + r*2*NWAVE + 2*wave + half. Rows past the split (t > t_last)
@@ -629,7 +595,7 @@ __device__ __forceinline__ void decode_body(
     const float *q, float *kc, float *vc, const float *k_new, const float *v_new,
     float *__restrict__ out, int *counters, float *part_ml, float *part_o, int n_head_kv, int n_kv,
     int tokens_per_split, int n_splits, float scale_log2, const Prologue &pro,
-    const ikv::Pages &pages, int g, int split) {
+    const ikv::Pages &pages, int g, int split, bool append = true) {
   static_assert(!COH || PRO, "the coherent form is the one with the prologue folded in");
   // Arrays read or written as float4 are declared 16-byte aligned.
   __shared__ __attribute__((aligned(16))) float s_acc[NWAVE][G][D];
@@ -646,7 +612,9 @@ __device__ __forceinline__ void decode_body(
   const int tl_slot = split * n_head_kv + g;
   const int t_begin = split * tokens_per_split;
   const int t_end = min(n_kv, t_begin + tokens_per_split);
-  const int new_row = k_new ? n_kv - 1 : -1;
+  // the new token's row: read from k_new / v_new and appended (none when the
+  // launch's position was rejected: then row n_kv - 1 is read from the cache)
+  const int new_row = (k_new && append) ? n_kv - 1 : -1;
   const size_t tok_stride = static_cast<size_t>(n_head_kv) * D;
   const size_t head_off = static_cast<size_t>(g) * D + 4 * sub;
 
@@ -888,11 +856,12 @@ __global__ __launch_bounds__(WG, waves_per_simd(G)) void decode_kernel(
     const float *__restrict__ q, float *kc, float *vc, const float *k_new, const float *v_new,
     float *__restrict__ out, int *counters, float *part_ml, float *part_o, int n_head_kv, int n_kv,
     int tokens_per_split, int n_splits, float scale_log2, Prologue pro, ikv::Pages pages) {
-  if constexpr (PRO) n_kv = launch_n_kv(pro, n_kv);
+  bool append = true;
+  if constexpr (PRO) n_kv = launch_n_kv(pro, n_kv, pro.dyn_max > 0 ? pro.pos[0] : 0, append);
   decode_body<G, PRO, PAGED, false>(q, kc, vc, k_new, v_new, out, counters, part_ml, part_o,
                                     n_head_kv, n_kv, tokens_per_split, n_splits, scale_log2, pro,
                                     pages, static_cast<int>(blockIdx.x) % n_head_kv,
-                                    static_cast<int>(blockIdx.x) / n_head_kv);
+                                    static_cast<int>(blockIdx.x) / n_head_kv, append);
 }
 
 // ---------------------------------------------------------------------------
@@ -978,11 +947,12 @@ __global__ __launch_bounds__(WG, 2) void qkv_attn_kernel(
   }
   __syncthreads();
   if (!s_last_qkv) return;
+  bool append = true;
+  const int n_kv_launch =
+      launch_n_kv(pro, n_kv, __builtin_amdgcn_readfirstlane(pos_lane), append);
   decode_body<G, true, false, true>(q_out, kc, vc, k_out, v_out, out, counters, nullptr, nullptr,
-                                    n_head_kv,
-                                    launch_n_kv(pro, n_kv, __builtin_amdgcn_readfirstlane(pos_lane)),
-                                    tokens_per_split, 1,
-                                    scale_log2, pro, ikv::Pages{}, g, 0);
+                                    n_head_kv, n_kv_launch, tokens_per_split, 1, scale_log2, pro,
+                                    ikv::Pages{}, g, 0, append);
 }
 
 bool supported_group(int G) { return G == 1 || G == 2 || G == 4 || G == 8; }

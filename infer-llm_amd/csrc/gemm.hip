@@ -1,6 +1,7 @@
 // gemm.hip — the prefill projections: out[m][n] = sum_k x[m][k] w[n][k]
 // (+ residual[m][n]) on F32 MFMA (v_mfma_f32_16x16x4_f32), used by
-// ikv_mul_mat_f32 for prompts of 2048 tokens and more.
+// ikv_mul_mat_f32 for every product of more than one token that its
+// few-token kernel does not take.
 //
 // Replaces CPUBackend::compute_mul_mat (src/backends/cpu_backend.cpp:386-424)
 // and CUDA_F32 mul_mat (src/kernels/cuda/kernel_f32.cu:142-205) for prompts;
@@ -35,12 +36,26 @@
 //     run of a grouped order (8 tile rows walked column by column):
 //     neighbouring tiles share x and w panels in that XCD's L2.
 //   * Tokens past m are clamped to row m-1 for the loads and not stored.
-//   * Results are deterministic (fixed order per output); on the measured
-//     shapes they were bit-identical to torch.mm (hipBLASLt) on MI355X.
+//   * Split K: when even the smallest tiles leave CUs idle (few tokens, few
+//     outputs, long k) the K loop of each tile is cut into n_split ranges of
+//     whole steps, one workgroup each. The splits of a tile run on one XCD
+//     (the same blockIdx % 8). Each stores its partial tile to a workspace
+//     at the device's coherence point, waits for the stores and counts
+//     itself on the tile's counter; the workgroup that counts last adds the
+//     partials in split order (0, 1, ..., its own from registers), writes
+//     the tile and sets the counter back to 0.
+//   * Tile shape and split (gemm_plan) come from a cost model fitted to a
+//     sweep of the Qwen3 projections on MI355X: rounds of tiles over the
+//     256 CUs times a measured time per tile of each shape.
+//   * Results are deterministic (fixed order per output for a given shape;
+//     the split depends only on n_out, k and m).
+#include "coherent.hpp"
 #include "ikv_common.hpp"
 #include "gemm.hpp"
 
+#include <algorithm>
 #include <climits>
+#include <mutex>
 #include <type_traits>
 
 namespace {
@@ -100,7 +115,9 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_kernel(const float *__re
                                                                const float *__restrict__ x,
                                                                float *out, const float *residual,
                                                                int n_out, int k, int m,
-                                                               int tiles_n, int n_tiles) {
+                                                               int tiles_n, int n_tiles,
+                                                               int n_split, float *part,
+                                                               int *counters) {
   constexpr int NT = WM * WN * 64;  // threads
   constexpr int BM = 16 * TM * WM, BN = 16 * TN * WN;
   constexpr int ROWS = BM + BN;     // staged rows per step: x rows, then w rows
@@ -109,14 +126,18 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_kernel(const float *__re
   constexpr int CPT = CHUNKS / NT;  // 16-byte chunks per thread per step
   constexpr int NQ = kChunks / 4;   // MFMA groups per step: 4 chunks (16 columns) each
   __shared__ __attribute__((aligned(16))) float s_buf[2][ROWS * BK];
+  __shared__ int s_last;
 
   // Tile order: XCD x (blockIdx % 8) takes positions [x * per, (x + 1) *
   // per) of a grouped order in which kGroupM tile rows are walked column by
   // column, so that the workgroups an XCD holds at once form a square block
-  // of tiles sharing few x and w panels in its L2.
+  // of tiles sharing few x and w panels in its L2. Its j-th workgroup (j =
+  // blockIdx / 8) takes split j / per of tile x * per + j % per.
   const int b = static_cast<int>(blockIdx.x);
   const int per = (n_tiles + kXcds - 1) / kXcds;
-  const int t = (b % kXcds) * per + b / kXcds;
+  const int j = b / kXcds;
+  const int t = (b % kXcds) * per + j % per;
+  const int sp = j / per;
   if (t >= n_tiles) return;
   const int tiles_m = n_tiles / tiles_n;
   const int grp = t / (kGroupM * tiles_n);
@@ -125,6 +146,12 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_kernel(const float *__re
   const int in_grp = t - grp * kGroupM * tiles_n;
   const int tm = first_m + in_grp % gsize, tn = in_grp / gsize;
   const int m0 = tm * BM, n0 = tn * BN;
+
+  // This split's steps of BK columns: [lo, hi) of k / BK, in equal shares.
+  const int all_steps = k / BK;
+  const int s_lo = static_cast<int>(static_cast<int64_t>(sp) * all_steps / n_split);
+  const int s_hi = static_cast<int>(static_cast<int64_t>(sp + 1) * all_steps / n_split);
+  const int k_lo = s_lo * BK;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -143,7 +170,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_kernel(const float *__re
     const int c = q % kChunks;
     const float *rowp = r < BM ? x + static_cast<size_t>(min(m0 + r, m - 1)) * k
                                : w + static_cast<size_t>(n0 + r - BM) * k;
-    src[i] = rowp + 4 * c;
+    src[i] = rowp + k_lo + 4 * c;
     dst[i] = r * BK + 4 * chunk_slot(r, c);
   }
   // The chunks of the next two steps, global -> registers -> LDS: at the
@@ -191,7 +218,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_kernel(const float *__re
   // write of the other is done), so that the last group's MFMAs cover the
   // reads of the next step's first operands instead of the step opening
   // on an LDS round trip.
-  const int n_steps = k / BK;
+  const int n_steps = s_hi - s_lo;
   auto step = [&](int s, auto next, auto par) {
     constexpr bool NEXT = decltype(next)::value;
     constexpr int P = decltype(par)::value;
@@ -265,6 +292,48 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_kernel(const float *__re
     step(s, std::false_type{}, P0{});
   }
 
+  if (n_split > 1) {
+    // partial float4 (ti, tj) of thread tid of split q of tile t at float4
+    // index ((t * n_split + q) * TM*TN + ti*TN + tj) * NT + tid
+    const auto rs = ikv::partial_rsrc(
+        part, static_cast<size_t>(n_tiles) * n_split * TM * TN * NT * sizeof(floatx4));
+    auto at = [&](int q, int ti, int tj) {
+      return static_cast<unsigned>(
+          (((static_cast<size_t>(t) * n_split + q) * TM * TN + ti * TN + tj) * NT + tid) *
+          sizeof(floatx4));
+    };
+#pragma unroll
+    for (int ti = 0; ti < TM; ++ti)
+#pragma unroll
+      for (int tj = 0; tj < TN; ++tj) {
+        const floatx4 a = acc[ti][tj];
+        ikv::store4_agent(rs, at(sp, ti, tj), make_float4(a[0], a[1], a[2], a[3]));
+      }
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's stores performed
+    __syncthreads();                // ... and every other wave's
+    if (tid == 0)
+      s_last = __hip_atomic_fetch_add(counters + t, 1, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT) == n_split - 1;
+    __syncthreads();
+    if (!s_last) return;
+#pragma unroll
+    for (int ti = 0; ti < TM; ++ti)
+#pragma unroll
+      for (int tj = 0; tj < TN; ++tj) {
+        floatx4 sum{};
+        for (int q = 0; q < n_split; ++q) {
+          floatx4 v = acc[ti][tj];
+          if (q != sp) {
+            const float4 l = ikv::load4_agent(rs, at(q, ti, tj));
+            v = floatx4{l.x, l.y, l.z, l.w};
+          }
+          sum = q == 0 ? v : sum + v;
+        }
+        acc[ti][tj] = sum;
+      }
+    if (tid == 0) __hip_atomic_store(counters + t, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+
   // acc[ti][tj] register r of lane l: token m0 + wm*16*TM + 16*ti + 4*(l/16)
   // + r, output n0 + wn*16*TN + 16*tj + l%16
 #pragma unroll
@@ -286,16 +355,96 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_kernel(const float *__re
 
 template <int TM, int TN, int WM, int WN>
 int launch(const float *w, const float *x, float *out, const float *residual, int n_out, int k,
-           int m, hipStream_t s) {
+           int m, int n_split, float *part, int *counters, hipStream_t s) {
   constexpr int BM = 16 * TM * WM, BN = 16 * TN * WN;
   const int tiles_m = (m + BM - 1) / BM;
   const int tiles_n = n_out / BN;
   const int64_t n_tiles = static_cast<int64_t>(tiles_m) * tiles_n;
   if (n_tiles > INT_MAX / 2) return -EOVERFLOW;
-  const int per = static_cast<int>((n_tiles + kXcds - 1) / kXcds);
-  gemm_nt_kernel<TM, TN, WM, WN><<<static_cast<unsigned>(per * kXcds), WM * WN * 64, 0, s>>>(
-      w, x, out, residual, n_out, k, m, tiles_n, static_cast<int>(n_tiles));
+  const int64_t per = (n_tiles + kXcds - 1) / kXcds;
+  if (per * n_split * kXcds > INT_MAX / 2) return -EOVERFLOW;
+  gemm_nt_kernel<TM, TN, WM, WN><<<static_cast<unsigned>(per * n_split * kXcds), WM * WN * 64, 0,
+                                   s>>>(w, x, out, residual, n_out, k, m, tiles_n,
+                                        static_cast<int>(n_tiles), n_split, part, counters);
   return ikv::launch_status();
+}
+
+struct TileShape {
+  int bm, bn;   // tokens x outputs
+  float cost;   // time of one tile's K step relative to 32 x 32, one tile per CU
+};
+// Index = the tile code of gemm_nt_tile. The plan's cost model: a launch of
+// T tiles, each split S ways, takes ceil(T * S / 256) rounds over the CUs of
+// cost * (steps / S + kFillSteps) each, steps = k / 64 (kFillSteps: the
+// pipeline's fill and the merge, in steps). Fitted to a sweep of the
+// Qwen3-0.6B and -8B projections at 65-2047 tokens over every tile shape and
+// 1-8 splits: each plan within 4.5% of the fastest measured.
+constexpr TileShape kTiles[] = {{128, 128, 12.5f}, {64, 64, 3.9f}, {64, 32, 2.0f},
+                                {32, 64, 2.1f},    {32, 32, 1.0f}};
+constexpr int kNumTiles = 5;
+constexpr double kFillSteps = 2.0;
+constexpr int kMinSplitSteps = 4;   // steps of BK columns per split, at least
+constexpr int kMaxSplit = 8;
+
+// Split-K workspace: tile counters (all 0 between launches), then partials.
+constexpr int kSplitCounters = 4096;
+constexpr size_t kSplitCounterBytes = kSplitCounters * sizeof(int);
+constexpr size_t kSplitPartBytes = size_t(8) << 20;
+
+int64_t tile_count(int tile, int n, int m) {
+  return int64_t((m + kTiles[tile].bm - 1) / kTiles[tile].bm) * (n / kTiles[tile].bn);
+}
+
+bool split_fits(int tile, int n, int m, int n_split, size_t part_bytes) {
+  const int64_t tiles = tile_count(tile, n, m);
+  return tiles <= kSplitCounters &&
+         static_cast<size_t>(tiles) * n_split * kTiles[tile].bm * kTiles[tile].bn * sizeof(float) <=
+             part_bytes;
+}
+
+__global__ void zero_ints_kernel(int *p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+// The split-K workspace of (current device, stream s): allocated and its
+// counters cleared (a kernel on s) on the first call for the pair, kept
+// until the process ends. Calls on one stream are ordered, so they never
+// share a workspace at the same time.
+int split_workspace(hipStream_t s, float **part, int **counters) {
+  struct Entry {
+    int dev;
+    hipStream_t stream;
+    char *mem;
+  };
+  constexpr int kMaxEntries = 64;
+  static std::mutex mu;
+  static Entry table[kMaxEntries];
+  static int n_entries = 0;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return static_cast<int>(e);
+  std::lock_guard<std::mutex> lock(mu);
+  for (int i = 0; i < n_entries; ++i)
+    if (table[i].dev == dev && table[i].stream == s) {
+      *counters = reinterpret_cast<int *>(table[i].mem);
+      *part = reinterpret_cast<float *>(table[i].mem + kSplitCounterBytes);
+      return 0;
+    }
+  if (n_entries == kMaxEntries) return -ENOMEM;
+  void *mem = nullptr;
+  e = hipMalloc(&mem, kSplitCounterBytes + kSplitPartBytes);
+  if (e != hipSuccess) return static_cast<int>(e);
+  zero_ints_kernel<<<kSplitCounters / 256, 256, 0, s>>>(static_cast<int *>(mem), kSplitCounters);
+  e = hipGetLastError();
+  if (e != hipSuccess) {
+    (void)hipFree(mem);
+    return static_cast<int>(e);
+  }
+  table[n_entries++] = {dev, s, static_cast<char *>(mem)};
+  *counters = static_cast<int *>(mem);
+  *part = reinterpret_cast<float *>(static_cast<char *>(mem) + kSplitCounterBytes);
+  return 0;
 }
 
 }  // namespace
@@ -307,20 +456,60 @@ bool gemm_nt_supported(int64_t n_out, int64_t k, int64_t m) {
          k <= INT_MAX / 2 && m <= INT_MAX / 2;
 }
 
+GemmPlan gemm_plan(int64_t n_out, int64_t k, int64_t m, bool may_split) {
+  const int n = static_cast<int>(n_out), mm = static_cast<int>(m);
+  const int steps = static_cast<int>(k / BK);
+  // the least estimated time; on a tie the larger tile, then fewer splits
+  GemmPlan p{4, 1};
+  double best = -1;
+  for (int i = 0; i < kNumTiles; ++i) {
+    if (n % kTiles[i].bn) continue;
+    const int64_t tiles = tile_count(i, n, mm);
+    for (int sk = 1; sk <= (may_split ? kMaxSplit : 1); ++sk) {
+      if (sk > 1 && (steps < sk * kMinSplitSteps || !split_fits(i, n, mm, sk, kSplitPartBytes)))
+        break;
+      const double rounds = double((tiles * sk + kCUs - 1) / kCUs);
+      const double est = rounds * kTiles[i].cost * (double(steps) / sk + kFillSteps);
+      if (best < 0 || est < best) {
+        best = est;
+        p = GemmPlan{i, sk};
+      }
+    }
+  }
+  return p;
+}
+
+// The tile shapes (tokens x outputs): 0 128 x 128, 1 64 x 64, 2 64 x 32,
+// 3 32 x 64, 4 32 x 32; each a 2 x 2 grid of wavefronts.
+int gemm_nt_tile(int tile, int n_split, const float *w, const float *x, float *out,
+                 const float *residual, int n, int kk, int mm, float *part, int *counters,
+                 hipStream_t s) {
+  if (n_split < 1 || n_split > kk / BK) return -EINVAL;
+  switch (tile) {
+    case 0:
+      if (n % 128) return -ENOTSUP;
+      return launch<4, 4, 2, 2>(w, x, out, residual, n, kk, mm, n_split, part, counters, s);
+    case 1: return launch<2, 2, 2, 2>(w, x, out, residual, n, kk, mm, n_split, part, counters, s);
+    case 2: return launch<2, 1, 2, 2>(w, x, out, residual, n, kk, mm, n_split, part, counters, s);
+    case 3: return launch<1, 2, 2, 2>(w, x, out, residual, n, kk, mm, n_split, part, counters, s);
+    case 4: return launch<1, 1, 2, 2>(w, x, out, residual, n, kk, mm, n_split, part, counters, s);
+    default: return -EINVAL;
+  }
+}
+
 int gemm_nt_f32(const float *w, const float *x, float *out, const float *residual, int64_t n_out,
-                int64_t k, int64_t m, hipStream_t s) {
+                int64_t k, int64_t m, bool may_split, hipStream_t s) {
   if (!gemm_nt_supported(n_out, k, m)) return -ENOTSUP;
   if (!aligned16(w) || !aligned16(x)) return -EINVAL;
-  const int n = static_cast<int>(n_out), kk = static_cast<int>(k), mm = static_cast<int>(m);
-  // 128 x 128 tiles (one workgroup per CU: 128 KB of LDS) when they make
-  // whole rounds over the CUs or at least four (a small last round); else
-  // 64 x 64 (two per CU, finer rounds). Measured on the Qwen3 projections
-  // at 1024-4096 tokens: each choice within 2% of the best of 128x128,
-  // 64x128, 128x64 and 64x64.
-  const int64_t big_tiles = int64_t((mm + 127) / 128) * (n / 128);
-  if (n % 128 == 0 && (big_tiles % kCUs == 0 || big_tiles >= 4 * kCUs))
-    return launch<4, 4, 2, 2>(w, x, out, residual, n, kk, mm, s);
-  return launch<2, 2, 2, 2>(w, x, out, residual, n, kk, mm, s);
+  const GemmPlan p = gemm_plan(n_out, k, m, may_split);
+  float *part = nullptr;
+  int *counters = nullptr;
+  if (p.split > 1) {
+    const int rc = split_workspace(s, &part, &counters);
+    if (rc) return rc;
+  }
+  return gemm_nt_tile(p.tile, p.split, w, x, out, residual, static_cast<int>(n_out),
+                      static_cast<int>(k), static_cast<int>(m), part, counters, s);
 }
 
 }  // namespace ikv
@@ -332,5 +521,41 @@ extern "C" int ikv_gemm_nt_f32(const float *w, const float *x, float *out, int64
   if (n_out == 0 || m == 0) return 0;
   if (n_out > INT_MAX / 2 || k > INT_MAX / 2 || m > INT_MAX / 2) return -EOVERFLOW;
   if (!ikv::gemm_nt_supported(n_out, k, m)) return -ENOTSUP;
-  return ikv::gemm_nt_f32(w, x, out, residual, n_out, k, m, static_cast<hipStream_t>(stream));
+  return ikv::gemm_nt_f32(w, x, out, residual, n_out, k, m, false,
+                          static_cast<hipStream_t>(stream));
 }
+
+#if IKV_GEMM_BENCH
+// Bench-only (libikv_bench.so): one product on a chosen tile shape (see
+// gemm_nt_tile) and split of K, the split-K workspace from the caller
+// (ws_bytes >= 16 KiB of zeroed counters plus the partials).
+extern "C" int ikv_bench_gemm_nt_tile_f32(const float *w, const float *x, float *out,
+                                          int64_t n_out, int64_t k, int64_t m,
+                                          const float *residual, int tile, int n_split, void *ws,
+                                          size_t ws_bytes, void *stream) {
+  if (!w || !x || !out || n_out <= 0 || k <= 0 || m <= 0) return -EINVAL;
+  if (!ikv::gemm_nt_supported(n_out, k, m)) return -ENOTSUP;
+  if (tile < 0 || tile >= kNumTiles || n_split < 1) return -EINVAL;
+  float *part = nullptr;
+  int *counters = nullptr;
+  if (n_split > 1) {
+    if (!ws || ws_bytes < kSplitCounterBytes ||
+        !split_fits(tile, int(n_out), int(m), n_split, ws_bytes - kSplitCounterBytes))
+      return -EINVAL;
+    counters = static_cast<int *>(ws);
+    part = reinterpret_cast<float *>(static_cast<char *>(ws) + kSplitCounterBytes);
+  }
+  return ikv::gemm_nt_tile(tile, n_split, w, x, out, residual, static_cast<int>(n_out),
+                           static_cast<int>(k), static_cast<int>(m), part, counters,
+                           static_cast<hipStream_t>(stream));
+}
+
+extern "C" int ikv_bench_gemm_plan(int64_t n_out, int64_t k, int64_t m, int *tile, int *n_split) {
+  if (!tile || !n_split || n_out <= 0 || k <= 0 || m <= 0) return -EINVAL;
+  if (!ikv::gemm_nt_supported(n_out, k, m)) return -ENOTSUP;
+  const ikv::GemmPlan p = ikv::gemm_plan(n_out, k, m, true);
+  *tile = p.tile;
+  *n_split = p.split;
+  return 0;
+}
+#endif

@@ -22,11 +22,11 @@
 // the norm weight as it reads it — the same float operations as the
 // standalone norm, so the products see the same inputs bit for bit.
 //
-// Prefill (m > 1) is a dense F32 GEMM and goes to rocBLAS SGEMM.
-#include <rocblas/rocblas.h>
-
+// Prefill (m > 1) is a dense F32 GEMM: up to 64 tokens the few-token MFMA
+// kernel below, otherwise the tiled MFMA GEMM of gemm.hip; shapes neither
+// takes (n_out or k not a multiple of 64, unaligned rows) run the per-output
+// wavefront kernel over every token (slow, exact order per output).
 #include <climits>
-#include <mutex>
 
 #include "gemm.hpp"
 #include "gemv_dev.hpp"
@@ -35,9 +35,6 @@
 
 namespace {
 
-#ifndef IKV_GEMM_OWN
-#define IKV_GEMM_OWN 1  // m >= 2048: this library's MFMA product (gemm.hip), else rocBLAS
-#endif
 #ifndef IKV_GEMV_WAVES
 #define IKV_GEMV_WAVES 4
 #endif
@@ -271,6 +268,10 @@ __global__ __launch_bounds__(kThreads) void gemv_generic_kernel(const float *__r
   if (n >= n_out) return;
   const int lane = threadIdx.x & 63;
   const float *row = w + static_cast<size_t>(n) * K;
+  // token blockIdx.y of a multi-token product (mode 0)
+  x += static_cast<size_t>(blockIdx.y) * K;
+  out += static_cast<size_t>(blockIdx.y) * n_out;
+  if (residual) residual += static_cast<size_t>(blockIdx.y) * n_out;
   float a = 0.f, b = 0.f;
   for (int k = lane; k < K; k += 64) {
     a = fmaf(row[k], x[k], a);
@@ -410,18 +411,6 @@ bool skinny_ok(int64_t n_out, int64_t k, int64_t m, std::initializer_list<const 
   return true;
 }
 
-// rocBLAS handle of the current device, created on first use.
-rocblas_handle blas_handle() {
-  static std::mutex mu;
-  static rocblas_handle handles[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-  std::lock_guard<std::mutex> lock(mu);
-  if (!handles[dev] && rocblas_create_handle(&handles[dev]) != rocblas_status_success)
-    handles[dev] = nullptr;
-  return handles[dev];
-}
-
 }  // namespace
 
 extern "C" int ikv_mul_mat_f32(const float *w, const float *x, float *out, int64_t n_out,
@@ -458,33 +447,12 @@ extern "C" int ikv_mul_mat_f32(const float *w, const float *x, float *out, int64
                                                                   int(k), int(m), n_tiles);
     return ikv::launch_status();
   }
-#if IKV_GEMM_OWN
-  if (m >= ikv::kGemmMinTokens && ikv::gemm_nt_supported(n_out, k, m) && ikv::aligned16(w) &&
-      ikv::aligned16(x))
-    return ikv::gemm_nt_f32(w, x, out, residual, n_out, k, m, s);
-#endif
-  rocblas_handle h = blas_handle();
-  if (!h) return static_cast<int>(hipErrorNotInitialized);
-  if (rocblas_set_stream(h, s) != rocblas_status_success) return static_cast<int>(hipErrorUnknown);
-  const float alpha = 1.f;
-  // Row-major out[m][n] is the column-major n x m matrix C = W^T(col) * X:
-  // A = w viewed column-major k x n, transposed; B = x viewed k x m. With a
-  // residual, D = A B + C reads C = residual and writes D = out, so the
-  // residual is never copied into out first (out may equal residual).
-  rocblas_status st;
-  if (residual) {
-    const float beta = 1.f;
-    st = rocblas_gemm_ex(h, rocblas_operation_transpose, rocblas_operation_none, int(n_out), int(m),
-                         int(k), &alpha, w, rocblas_datatype_f32_r, int(k), x, rocblas_datatype_f32_r,
-                         int(k), &beta, residual, rocblas_datatype_f32_r, int(n_out), out,
-                         rocblas_datatype_f32_r, int(n_out), rocblas_datatype_f32_r,
-                         rocblas_gemm_algo_standard, 0, 0);
-  } else {
-    const float beta = 0.f;
-    st = rocblas_sgemm(h, rocblas_operation_transpose, rocblas_operation_none, int(n_out), int(m),
-                       int(k), &alpha, w, int(k), x, int(k), &beta, out, int(n_out));
-  }
-  if (st != rocblas_status_success) return static_cast<int>(hipErrorLaunchFailure);
+  if (ikv::gemm_nt_supported(n_out, k, m) && ikv::aligned16(w) && ikv::aligned16(x))
+    return ikv::gemm_nt_f32(w, x, out, residual, n_out, k, m, true, s);
+  // any other shape: one wavefront per output, blockIdx.y the token
+  if (m > 65535) return -ENOTSUP;
+  gemv_generic_kernel<<<dim3(grid_for(n_out), static_cast<unsigned>(m)), kThreads, 0, s>>>(
+      w, x, out, residual, int(n_out), int(k), 0, nullptr);
   return ikv::launch_status();
 }
 

@@ -162,6 +162,19 @@ extern "C" int ikv_qwen3_last_stats(const ikv_qwen3 *m, ikv_qwen3_stats *out) {
   return 0;
 }
 
+extern "C" int ikv_qwen3_capture_logits(ikv_qwen3 *m, const int64_t *steps, int64_t n_steps) {
+  if (!m || n_steps < 0 || (n_steps > 0 && !steps)) return -EINVAL;
+  std::vector<int64_t> v(steps, steps + n_steps);
+  if (auto r = m->runner->set_logit_capture(v); !r) return -r.error().value();
+  return 0;
+}
+
+extern "C" int ikv_qwen3_captured_logits(const ikv_qwen3 *m, float *host, size_t count) {
+  if (!m) return -EINVAL;
+  if (auto r = m->runner->captured_logits(host, count); !r) return -r.error().value();
+  return 0;
+}
+
 extern "C" int ikv_qwen3_set_step_replay(ikv_qwen3 *m, int on) {
   if (!m) return -EINVAL;
   m->runner->set_step_replay(on != 0);

@@ -188,6 +188,7 @@ Qwen3Runner::~Qwen3Runner() {
   if (_token_dev) (void)hipFree(_token_dev);
   if (_positions_dev) (void)hipFree(_positions_dev);
   if (_argmax_ws) (void)hipFree(_argmax_ws);
+  if (_logit_dev) (void)hipFree(_logit_dev);
   if (_token_host) (void)hipHostFree(_token_host);
 }
 
@@ -301,7 +302,7 @@ infer::expected<void, std::error_code> Qwen3Runner::enqueue_step(const int32_t *
   // and to the pinned host slot the host reads once the event has fired.
   if (ikv_argmax_ws_f32(row, vocab, _token_dev + out_slot, _token_host_dev + host_slot, _argmax_ws,
                         ikv_argmax_workspace_bytes(), s) != 0 ||
-      hipEventRecord(_ready[host_slot], s) != hipSuccess)
+      !keep_logits(row, vocab, s) || hipEventRecord(_ready[host_slot], s) != hipSuccess)
     return abort(std::make_error_code(std::errc::io_error));
   // The kernels of this step hold no host-side state: hand the layer
   // accesses back and commit the appended range now.
@@ -422,13 +423,55 @@ infer::expected<void, std::error_code> Qwen3Runner::replay_step(int host_slot,
       ikv_argmax_ws_f32(_step_logits, _step_vocab, _token_dev + kReplaySlot,
                         _token_host_dev + host_slot, _argmax_ws, ikv_argmax_workspace_bytes(),
                         s) != 0 ||
-      hipEventRecord(_ready[host_slot], s) != hipSuccess)
+      !keep_logits(_step_logits, _step_vocab, s) || hipEventRecord(_ready[host_slot], s) != hipSuccess)
     return infer::fail(std::errc::io_error);
   ++_replay_stats.replays;
   const auto t2 = Clock::now();
   timing.build_s += std::chrono::duration<double>(t1 - t0).count();
   timing.execute_s += std::chrono::duration<double>(t2 - t1).count();
   return {};
+}
+
+infer::expected<void, std::error_code> Qwen3Runner::set_logit_capture(
+    const std::vector<int64_t> &steps) {
+  if (_logit_dev) {
+    (void)_backend.synchronize();
+    (void)hipFree(_logit_dev);
+    _logit_dev = nullptr;
+  }
+  _logit_steps.clear();
+  if (steps.empty()) return {};
+  for (const int64_t st : steps)
+    if (st < 0) return infer::fail(std::errc::invalid_argument);
+  const size_t vocab = _model.hparams().n_vocab;
+  if (hipMalloc(&_logit_dev, steps.size() * vocab * sizeof(float)) != hipSuccess) {
+    (void)hipGetLastError();
+    _logit_dev = nullptr;
+    return infer::fail(std::errc::not_enough_memory);
+  }
+  _logit_steps = steps;
+  return {};
+}
+
+infer::expected<void, std::error_code> Qwen3Runner::captured_logits(float *host,
+                                                                    size_t count) const {
+  const size_t vocab = _model.hparams().n_vocab;
+  if (!host || !_logit_dev || count != _logit_steps.size() * vocab)
+    return infer::fail(std::errc::invalid_argument);
+  if (hipMemcpy(host, _logit_dev, count * sizeof(float), hipMemcpyDeviceToHost) != hipSuccess)
+    return infer::fail(std::errc::io_error);
+  return {};
+}
+
+bool Qwen3Runner::keep_logits(const float *row, int64_t vocab, hipStream_t s) {
+  for (size_t k = 0; k < _logit_steps.size(); ++k) {
+    if (size_t(_logit_steps[k]) != _cur_step) continue;
+    if (size_t(vocab) != _model.hparams().n_vocab) return false;
+    if (hipMemcpyAsync(_logit_dev + k * size_t(vocab), row, size_t(vocab) * sizeof(float),
+                       hipMemcpyDeviceToDevice, s) != hipSuccess)
+      return false;
+  }
+  return true;
 }
 
 infer::expected<int32_t, std::error_code> Qwen3Runner::collect(int slot) {
@@ -483,12 +526,14 @@ infer::expected<void, std::error_code> Qwen3Runner::generate(const std::vector<i
   bool replay = _replay && _kv_opt.block_tokens == 0 && _kv_opt.offload_bytes == 0 &&
                 _backend.fusion();
   const bool one_slot = replay;  // the device token stays in kReplaySlot throughout
+  _cur_step = 0;
   if (auto r = enqueue_step(prompt.data(), int64_t(prompt.size()), 1, one_slot ? kReplaySlot : 0,
                             timing, 0);
       !r)
     return finish(r);
   for (size_t i = 1; i < n_gen; ++i) {
     const int host_slot = int(i & 1);
+    _cur_step = i;
     infer::expected<void, std::error_code> r;
     if (replay) {
       r = replay_step(host_slot, timing);
@@ -524,6 +569,10 @@ infer::expected<void, std::error_code> Qwen3Runner::generate_interleaved(
     if (p.size() + n_gen - 1 > _capacity) return infer::fail(std::errc::value_too_large);
   }
   if (!_kv) return infer::fail(std::errc::invalid_argument);
+  // interleaved steps are eager: nothing of an earlier generate() is replayed
+  // or counted here
+  _replay_stats = {};
+  drop_step_graph();
   std::vector<SequenceId> seqs;
   auto finish = [&](infer::expected<void, std::error_code> r) {
     const auto sync = _backend.synchronize();

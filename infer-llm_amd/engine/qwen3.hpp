@@ -153,6 +153,13 @@ class Qwen3Runner {
   };
   // Over the last generate() call.
   ReplayStats replay_stats() const { return _replay_stats; }
+  // Keep, during each later generate(), the logits row the sampler reads at
+  // each of `steps` (step 0 samples from the prompt's last row; step i > 0
+  // from decode step i), copied on the stream after the step (outside any
+  // captured graph); empty: keep none. captured_logits copies them, in the
+  // order of `steps`, n_vocab floats each.
+  infer::expected<void, std::error_code> set_logit_capture(const std::vector<int64_t> &steps);
+  infer::expected<void, std::error_code> captured_logits(float *host, size_t count) const;
 
  private:
   // Enqueues one step of sequence _seq: its input is the host prompt, or
@@ -171,6 +178,8 @@ class Qwen3Runner {
   infer::expected<void, std::error_code> capture_step(int64_t n_past);
   void drop_step_graph();
   infer::expected<int32_t, std::error_code> collect(int slot);
+  // Enqueues the copy of `row` if the step being enqueued is one to keep.
+  bool keep_logits(const float *row, int64_t vocab, hipStream_t s);
 
   Qwen3Model &_model;
   HIPBackend &_backend;
@@ -199,4 +208,8 @@ class Qwen3Runner {
   int64_t _step_vocab = 0;
   int32_t *_pos_state = nullptr;        // device: the position the captured step reads
   ReplayStats _replay_stats;
+  // logit capture: the steps, their rows on the device, the step enqueued
+  std::vector<int64_t> _logit_steps;
+  float *_logit_dev = nullptr;
+  size_t _cur_step = 0;
 };

@@ -153,6 +153,10 @@ BENCH_SIGNATURES = {
     "ikv_probe_empty": (_c_int, [_c_int, _c_void_p]),
     "ikv_bench_timeline_read": (_c_int, [_c_void_p, _c_size_t]),
     "ikv_bench_timeline_clear": (_c_int, []),
+    "ikv_bench_gemm_nt_tile_f32": (
+        _c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int64, _c_int64, _c_int64, _c_void_p, _c_int,
+                 _c_int, _c_void_p, _c_size_t, _c_void_p]),
+    "ikv_bench_gemm_plan": (_c_int, [_c_int64, _c_int64, _c_int64, _c_void_p, _c_void_p]),
 }
 
 

@@ -80,6 +80,8 @@ ENGINE_SIGNATURES = {
     "ikv_qwen3_last_stats": (ctypes.c_int, [_P, ctypes.POINTER(Stats)]),
     "ikv_qwen3_set_fusion": (ctypes.c_int, [_P, ctypes.c_int]),
     "ikv_qwen3_set_step_replay": (ctypes.c_int, [_P, ctypes.c_int]),
+    "ikv_qwen3_capture_logits": (ctypes.c_int, [_P, _P, ctypes.c_int64]),
+    "ikv_qwen3_captured_logits": (ctypes.c_int, [_P, _P, ctypes.c_size_t]),
     "ikv_qwen3_destroy": (None, [_P]),
 }
 
@@ -153,6 +155,7 @@ class Qwen3Engine:
             _check("ikv_qwen3_create", _lib().ikv_qwen3_create(ctypes.byref(c), device, max_ctx,
                                                                ctypes.byref(h)))
         self._h = h
+        self._logit_steps = []
 
     def close(self):
         if self._h:
@@ -193,6 +196,23 @@ class Qwen3Engine:
         """Decode steps replayed from a captured HIP graph (default on)."""
         _check("ikv_qwen3_set_step_replay",
                _lib().ikv_qwen3_set_step_replay(self._h, 1 if on else 0))
+
+    def capture_logits(self, steps):
+        """Keep the sampler's logits row at each of `steps` during later
+        generate() calls (step 0: the prompt's last row; [] keeps none)."""
+        st = np.ascontiguousarray(steps, dtype=np.int64)
+        self._logit_steps = [int(x) for x in st]
+        _check("ikv_qwen3_capture_logits",
+               _lib().ikv_qwen3_capture_logits(self._h, st.ctypes.data if st.size else None,
+                                               st.size))
+
+    def captured_logits(self):
+        """The kept rows of the last generate(): float32 [len(steps), n_vocab]."""
+        n = len(self._logit_steps)
+        out = np.empty((n, self.cfg.n_vocab), np.float32)
+        _check("ikv_qwen3_captured_logits",
+               _lib().ikv_qwen3_captured_logits(self._h, out.ctypes.data, out.size))
+        return out
 
     def generate(self, prompt, n_gen: int):
         """Greedy tokens (list) and Timing for prompt then n_gen tokens."""

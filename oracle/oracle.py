@@ -256,12 +256,17 @@ class Qwen3Oracle:
             raise RuntimeError(f"oracle_qwen3_step returned {rc}")
         return logits
 
-    def generate(self, prompt, n_gen):
+    def generate(self, prompt, n_gen, keep_logits=()):
+        """Greedy tokens (benchmarks/cpu/bench.cpp:239-281); the logits row the
+        sampler read at each step in keep_logits lands in self.kept[step]."""
         ids = list(prompt)
         n_past = 0
         out = []
-        for _ in range(n_gen):
+        self.kept = {}
+        for i in range(n_gen):
             logits = self.step(ids, n_past)
+            if i in keep_logits:
+                self.kept[i] = logits[-1].copy()
             tok = sample_greedy(logits[-1])
             if tok < 0:
                 raise RuntimeError("greedy sampling rejected the logits")

@@ -107,6 +107,7 @@ struct Rng {
 static void paged_cpu_tests();
 static void offload_cpu_tests();
 static void offload_gpu_tests(HIPBackend *hip);
+static void producer_cache_gpu_tests(HIPBackend *hip);
 
 static void cpu_tests() {
   {
@@ -682,7 +683,97 @@ static void gpu_tests() {
   CHECK(kv.release_sequence(*sid), "release sequence (frees HBM caches)");
   for (auto &t : qw_d) hip->free(BufferKind::WEIGHTS, t->data);
   for (auto &t : kw_d) hip->free(BufferKind::WEIGHTS, t->data);
+  producer_cache_gpu_tests(hip);
   offload_gpu_tests(hip);
+}
+
+// The prefill rows a layer's projections write straight into the cache (the
+// k projection through qk-norm + RoPE, the v projection as is): with the
+// fusions on, the producers write the cache rows themselves; with them off,
+// each result lands in an activation and a CPY copies it. The cache bytes
+// must be equal bit for bit, at prompt lengths that run the projections on
+// the few-token MFMA kernel (20), the mid-size path (70) and this build's
+// GEMM (2048).
+static void producer_cache_gpu_tests(HIPBackend *hip) {
+  const int Hq = 16, Hkv = 8, D = 128, E = 1024;
+  AttentionSliceParams sp;
+  Rng rng(0x1F0000 + 77);
+  auto upload = [&](const std::vector<float> &h, std::initializer_list<int64_t> shape, const char *name) {
+    auto t = std::make_unique<Tensor>(name, GGML_TYPE_F32, shape);
+    t->data = *hip->alloc(BufferKind::WEIGHTS, t->byte_size());
+    t->backend = hip;
+    t->device = DeviceType::HIP;
+    t->tensorRole = TensorRole::TENSOR_ROLE_WEIGHT;
+    hip->copy_tensor_set(t.get(), h.data(), 0, h.size() * 4);
+    return t;
+  };
+  auto wq = upload(rng.normal(size_t(Hq) * D * E, 0.02), {E, Hq * D, 1, 1}, "wq");
+  auto wk = upload(rng.normal(size_t(Hkv) * D * E, 0.02), {E, Hkv * D, 1, 1}, "wk");
+  auto wv = upload(rng.normal(size_t(Hkv) * D * E, 0.02), {E, Hkv * D, 1, 1}, "wv");
+  std::vector<float> ones(D, 1.0f);
+  auto qnw = upload(ones, {D, 1, 1, 1}, "q_norm_w");
+  auto knw = upload(ones, {D, 1, 1, 1}, "k_norm_w");
+  for (const int P : {20, 70, 2048}) {
+    std::vector<std::vector<float>> k_bytes(2), v_bytes(2);
+    auto xh = rng.normal(size_t(P) * E);
+    auto x = upload(xh, {E, P, 1, 1}, "x");
+    for (int fused = 1; fused >= 0; --fused) {
+      const std::string tag = "P=" + std::to_string(P) + (fused ? " fused" : " unfused");
+      hip->set_fusion(fused != 0);
+      std::vector<KVLayerSpec> specs(1, KVLayerSpec{size_t(Hkv), size_t(D), size_t(D)});
+      std::vector<Backend *> place(1, hip);
+      KVCacheManager kv(std::make_unique<ContiguousKVStrategy>(std::make_unique<NaiveKVStorage>()));
+      CHECK(kv.init(specs, place, KVCacheConfig{.layers = 1, .max_tokens_per_sequence = size_t(P)}),
+            ("kv init " + tag).c_str());
+      auto sid = kv.create_sequence();
+      if (!sid || !kv.reserve_append(*sid, P)) {
+        CHECK(false, ("sequence " + tag).c_str());
+        return;
+      }
+      GraphContext ctx(nullptr);
+      CHECK(ctx.set_kv_cache(&kv, *sid), ("bind " + tag).c_str());
+      std::vector<int32_t> pos(P);
+      for (int i = 0; i < P; ++i) pos[i] = i;
+      Tensor *pos_t = ctx.make_tensor("inp_pos", GGML_TYPE_I32, {P});
+      pos_t->device = DeviceType::CPU;
+      pos_t->tensorRole = TensorRole::TNESOR_ROLE_INPUT;
+      pos_t->data = pos.data();
+      ctx.set_input_pos(pos_t);
+      Graph g;
+      Tensor *q = OpFactory::mul_mat(g, wq.get(), x.get(), "q_proj");
+      Tensor *k = OpFactory::mul_mat(g, wk.get(), x.get(), "k_proj");
+      Tensor *v = OpFactory::mul_mat(g, wv.get(), x.get(), "v_proj");
+      auto out = build_attention_slice(g, ctx, q, k, v, qnw.get(), knw.get(), 0, sp);
+      CHECK(bool(out), ("build " + tag).c_str());
+      if (!out) return;
+      g.mark_output(*out);
+      Scheduler sched(hip);
+      auto ex = sched.execute(g);
+      auto sy = hip->synchronize();
+      CHECK(ex && sy, ("execute " + tag).c_str());
+      const StorageState *ss = kv.strategy()->storage()->state(StorageId(1));
+      const size_t bytes = size_t(P) * Hkv * D * 4;
+      k_bytes[fused].resize(bytes / 4);
+      v_bytes[fused].resize(bytes / 4);
+      (void)hipMemcpy(k_bytes[fused].data(), ss->object.k_base, bytes, hipMemcpyDeviceToHost);
+      (void)hipMemcpy(v_bytes[fused].data(), ss->object.v_base, bytes, hipMemcpyDeviceToHost);
+      if (fused) {
+        const auto &st = hip->last_stats();
+        CHECK(st.fused_append == 2, ("producers write the cache rows, " + tag).c_str());
+      }
+      ctx.release_kv_access();
+      (void)kv.abort_append(*sid);
+      (void)kv.release_sequence(*sid);
+    }
+    const size_t bytes = size_t(P) * Hkv * D * 4;
+    CHECK(std::memcmp(k_bytes[0].data(), k_bytes[1].data(), bytes) == 0,
+          ("K rows written by the RoPE producer equal the copied ones, P=" + std::to_string(P)).c_str());
+    CHECK(std::memcmp(v_bytes[0].data(), v_bytes[1].data(), bytes) == 0,
+          ("V rows written by the v projection equal the copied ones, P=" + std::to_string(P)).c_str());
+    hip->free(BufferKind::WEIGHTS, x->data);
+  }
+  hip->set_fusion(true);
+  for (auto *t : {wq.get(), wk.get(), wv.get(), qnw.get(), knw.get()}) hip->free(BufferKind::WEIGHTS, t->data);
 }
 
 // Two sequences on an offloaded cache whose HBM budget holds one sequence's

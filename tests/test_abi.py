@@ -50,6 +50,36 @@ def test_measurement_code_lives_in_the_bench_library():
     ikv.load_bench()
 
 
+def test_library_links_no_vendor_blas():
+    # every product runs on this library's own kernels
+    deps = subprocess.run(["ldd", str(ikv.LIB_PATH)], capture_output=True, text=True).stdout
+    assert "rocblas" not in deps and "hipblas" not in deps
+
+
+GEMM_TILE_NAMES = ["128x128", "64x64", "64x32", "32x64", "32x32"]
+
+
+@pytest.mark.parametrize("n_out,k,m,plan", [
+    # Qwen3-0.6B o_proj and Qwen3-8B k/v projections at 128 tokens: 128
+    # tiles of 32 x 32, K split in two (256 workgroups, one per CU)
+    (1024, 2048, 128, "32x32/2"), (1024, 4096, 128, "32x32/2"),
+    (1024, 3072, 65, "32x32/5"),     # 96 tiles, 48 steps: 480 workgroups in 2 rounds
+    (2048, 1024, 128, "32x32/1"),    # 256 tiles: one per CU
+    (3072, 1024, 512, "64x32/1"),    # 768 tiles: whole rounds (64 x 64 would leave a half round)
+    (4096, 4096, 512, "64x64/1"),
+    (1024, 1024, 2048, "64x64/1"),   # 128 tiles of 128 x 128 would idle half the CUs
+    (2048, 1024, 2048, "128x128/1"), (4096, 12288, 4096, "128x128/1"),
+    (64, 4096, 300, "32x32/8"),      # 20 tiles: at most 8 splits
+    (1024, 256, 65, "32x32/1"),      # 4 steps of 64 columns: too short to split
+])
+def test_gemm_plan(n_out, k, m, plan):
+    import ctypes
+    tile, split = ctypes.c_int(), ctypes.c_int()
+    assert ikv.load_bench().ikv_bench_gemm_plan(n_out, k, m, ctypes.byref(tile),
+                                                ctypes.byref(split)) == 0
+    assert f"{GEMM_TILE_NAMES[tile.value]}/{split.value}" == plan
+
+
 def test_library_does_not_link_the_oracle():
     deps = subprocess.run(["ldd", str(ikv.LIB_PATH)], capture_output=True, text=True).stdout
     assert "oracle" not in deps

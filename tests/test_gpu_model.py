@@ -50,7 +50,8 @@ def test_gemv_matches_oracle(dev, oracle_pool, n_out, k):
 @pytest.mark.parametrize("n_out,k,m", [(2048, 1024, 37), (1024, 3072, 5), (300, 200, 2), (3072, 1024, 64),
                                         (16, 256, 2), (4096, 4096, 17), (1024, 2048, 65),
                                         (2048, 1024, 300), (3072, 1024, 2048), (1024, 3072, 129),
-                                        (4096, 4096, 100), (192, 64, 70), (300, 200, 100)])
+                                        (4096, 4096, 100), (192, 64, 70), (300, 200, 100),
+                                        (96, 200, 2100), (1024, 1024, 1000), (4096, 1024, 512)])
 def test_mul_mat_multi_token_matches_oracle(dev, oracle_pool, n_out, k, m):
     w = synth.normal(300 + m, (n_out, k), 0.02)
     x = synth.normal(400 + m, (m, k))
@@ -73,9 +74,9 @@ def test_mul_mat_few_tokens_residual_in_place(dev, oracle_pool):
 
 
 def test_mul_mat_many_tokens_residual_in_place(dev, oracle_pool):
-    # out = out + W x for 200 tokens (rocBLAS with beta = 1) and 2048 (the
-    # MFMA GEMM of prefill projections)
-    for m in (200, 2048):
+    # out = out + W x through the MFMA GEMM: 65 tokens (K split in two), 200
+    # and 2048
+    for m in (65, 200, 2048):
         _many_tokens_residual_in_place(dev, m)
 
 
@@ -106,6 +107,95 @@ def test_gemm_matches_oracle(dev, oracle_pool, n_out, k, m):
     buf = dev_t(r, dev)
     ikv.gemm_nt(dev_t(w, dev), dev_t(x, dev), out=buf, residual=buf)
     assert proj_close(host(buf), w, x, ref.astype(np.float64) + r)
+
+
+def gemm_plan(n_out, k, m):
+    import ctypes
+    tile, split = ctypes.c_int(), ctypes.c_int()
+    assert ikv.load_bench().ikv_bench_gemm_plan(n_out, k, m, ctypes.byref(tile),
+                                                ctypes.byref(split)) == 0
+    return tile.value, split.value
+
+
+@pytest.mark.parametrize("n_out,k,m", [
+    (1024, 4096, 128), (1024, 3072, 128), (1024, 1024, 65),  # Qwen3 o / down / k,v shapes
+    (64, 4096, 300), (128, 2048, 77), (192, 1600, 40),       # ragged m and k ranges
+])
+def test_mul_mat_split_k_matches_oracle(dev, oracle_pool, n_out, k, m):
+    # tiles that leave CUs idle: each tile's K range split over several
+    # workgroups, partials added in split order by the last to finish
+    assert gemm_plan(n_out, k, m)[1] > 1
+    w = synth.normal(800 + m, (n_out, k), 0.02)
+    x = synth.normal(801 + m, (m, k))
+    r = synth.normal(802 + m, (m, n_out))
+    ref = oracle.mul_mat(w, x)
+    wd, xd = dev_t(w, dev), dev_t(x, dev)
+    got = host(ikv.mul_mat(wd, xd))
+    assert proj_close(got, w, x, ref)
+    for _ in range(3):  # deterministic, and every tile counter back at 0
+        assert np.array_equal(host(ikv.mul_mat(wd, xd)), got)
+    buf = dev_t(r, dev)
+    ikv.mul_mat(wd, xd, out=buf, residual=buf)
+    assert proj_close(host(buf), w, x, ref.astype(np.float64) + r)
+
+
+@pytest.mark.parametrize("tile", range(5))
+def test_gemm_every_tile_and_split_matches_oracle(dev, oracle_pool, tile):
+    # each tile shape with K in 1, 2, 3, 5 and 8 ranges (25 steps of 64
+    # columns: uneven ranges), ragged m, residual in place, through the
+    # bench library's entry (the plan picks among these)
+    import ctypes
+    import torch
+    n_out, k, m = 256, 1600, 77
+    w = synth.normal(820 + tile, (n_out, k), 0.02)
+    x = synth.normal(821 + tile, (m, k))
+    r = synth.normal(822 + tile, (m, n_out))
+    ref = oracle.mul_mat(w, x)
+    wd, xd = dev_t(w, dev), dev_t(x, dev)
+    ws = torch.zeros((16 << 10) + (4 << 20), dtype=torch.uint8, device=dev)
+    lib = ikv.load_bench()
+    stream = torch.cuda.current_stream().cuda_stream
+    for split in (1, 2, 3, 5, 8):
+        out = torch.empty(m, n_out, device=dev)
+        assert lib.ikv_bench_gemm_nt_tile_f32(wd.data_ptr(), xd.data_ptr(), out.data_ptr(), n_out, k,
+                                              m, None, tile, split, ws.data_ptr(), ws.numel(),
+                                              stream) == 0
+        assert proj_close(host(out), w, x, ref), f"tile {tile} split {split}"
+        buf = dev_t(r, dev)
+        assert lib.ikv_bench_gemm_nt_tile_f32(wd.data_ptr(), xd.data_ptr(), buf.data_ptr(), n_out, k,
+                                              m, buf.data_ptr(), tile, split, ws.data_ptr(),
+                                              ws.numel(), stream) == 0
+        assert proj_close(host(buf), w, x, ref.astype(np.float64) + r), f"tile {tile} split {split}"
+    torch.cuda.synchronize()
+    assert not ws[:16 << 10].any()  # every tile counter back at 0
+
+
+def test_mul_mat_split_k_replays_from_a_graph(dev):
+    # the split-K product captured in a HIP graph (its stream's workspace
+    # allocated by an eager call first): every replay equals the eager bits
+    import torch
+    w = dev_t(synth.normal(810, (1024, 2048), 0.02), dev)
+    x = dev_t(synth.normal(811, (128, 2048)), dev)
+    assert gemm_plan(1024, 2048, 128)[1] > 1
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    out = torch.empty(128, 1024, device=dev)
+    with torch.cuda.stream(side):
+        ikv.mul_mat(w, x, out=out)
+    torch.cuda.synchronize()
+    ref = out.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        ikv.mul_mat(w, x, out=out)
+        ikv.mul_mat(w, x, out=out)
+    for _ in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref)
+        ikv.mul_mat(w, x, out=out)  # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref)
 
 
 def test_gemm_is_deterministic_and_mul_mat_uses_it(dev):
@@ -243,6 +333,20 @@ def test_argmax_follows_the_greedy_sampler(dev, form):
 SMALL = qwen3.Qwen3Config(n_layer=4, n_vocab=8192, n_ctx_train=4096)
 
 
+# |engine - oracle| <= LOGIT_ATOL + LOGIT_RTOL * |oracle| for whole-model
+# logits: the same F32 arithmetic summed in other orders through every layer
+LOGIT_ATOL, LOGIT_RTOL = 1e-3, 1e-3
+
+
+def assert_logits_close(got, want, what):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    err = np.abs(got - want)
+    print(f"{what}: max |diff| {err.max():.3e}, max |logit| {np.abs(want).max():.3f}", flush=True)
+    assert np.all(err <= LOGIT_ATOL + LOGIT_RTOL * np.abs(want)), \
+        f"{what}: max |diff| {err.max():.3e} over the bound"
+
+
 def engine_with(cfg, weights, max_ctx):
     eng = qwen3.Qwen3Engine(cfg, max_ctx)
     eng.set_weights(weights)
@@ -376,10 +480,18 @@ def test_qwen3_06b_config0_greedy_tokens_match_oracle(dev, oracle_pool):
     w = qwen3.synthetic_weights(cfg, synth.config_seed(0, 1))
     prompt = synth.uniform_ints(synth.config_seed(0, 0), 32, cfg.n_vocab)
     eng = engine_with(cfg, w, 160)
+    steps = [0, 1, 64, 127]  # the prefill's row, the first decode, mid-run, last
+    eng.capture_logits(steps)
     toks, _ = eng.generate(prompt, 128)
+    got = eng.captured_logits()
     eng.close()
-    ref = oracle.Qwen3Oracle(cfg, w, 160).generate(prompt, 128)
+    orc = oracle.Qwen3Oracle(cfg, w, 160)
+    ref = orc.generate(prompt, 128, keep_logits=steps)
     assert toks == ref
+    # logits at those steps: every one of the 151936 within the model-level
+    # bound (F32 sums in another order through 28 layers)
+    for k, st in enumerate(steps):
+        assert_logits_close(got[k], orc.kept[st], f"config 0 step {st}")
 
 
 # ---------------------------------------------------------------------------
@@ -648,15 +760,50 @@ def test_decode_replay_position_past_plan_is_flagged(dev):
     th = oracle.rope_theta_table(1e6, D, 1024)
     s, c = ikv.rope_sincos_table(th)
     sd, cd = dev_t(s, dev), dev_t(c, dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(17)
     kc = torch.zeros((400, Hkv, D), device=dev)
     vc = torch.zeros_like(kc)
+    kc[:384] = torch.randn((384, Hkv, D), generator=g, device=dev)  # committed history
+    vc[:384] = torch.randn((384, Hkv, D), generator=g, device=dev)
+    k0, v0 = kc.clone(), vc.clone()
     t = torch.ones((Hq, D), device=dev)
     status = torch.zeros(1, dtype=torch.int32, device=dev)
     pos = torch.tensor([384], dtype=torch.int32, device=dev)  # context 385 > planned 384
     ikv.attn_decode_rope(t, t[:Hkv], t[:Hkv], kc, vc, 384, t[0], t[0], 1e-6, pos, sd, cd,
                          status=status, replay=True)
+    torch.cuda.synchronize()
     assert int(status.item()) & ikv.STATUS_POSITION
-    assert not torch.any(kc[384:])  # nothing written past the planned rows
+    # no append: the committed rows (the last planned one included) keep their
+    # bits, and nothing is written past the planned rows
+    assert torch.equal(kc.view(torch.int32), k0.view(torch.int32))
+    assert torch.equal(vc.view(torch.int32), v0.view(torch.int32))
+
+
+def test_qkv_decode_replay_position_past_plan_appends_nothing(dev):
+    # the same for the q/k/v-folded replay form (planned for 128 keys)
+    import torch
+    Hq, Hkv, D, K = 16, 8, 128, 1024
+    th = oracle.rope_theta_table(1e6, D, 1024)
+    s, c = ikv.rope_sincos_table(th)
+    sd, cd = dev_t(s, dev), dev_t(c, dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(18)
+    w = lambda n: torch.randn((n, K), generator=g, device=dev) * 0.02  # noqa: E731
+    x = torch.randn(K, generator=g, device=dev)
+    kc = torch.randn((160, Hkv, D), generator=g, device=dev)
+    vc = torch.randn((160, Hkv, D), generator=g, device=dev)
+    k0, v0 = kc.clone(), vc.clone()
+    ones = torch.ones(D, device=dev)
+    for p in (128, 150, -1):
+        status = torch.zeros(1, dtype=torch.int32, device=dev)
+        pos = torch.tensor([p], dtype=torch.int32, device=dev)
+        ikv.qkv_attn_decode(w(Hq * D), w(Hkv * D), w(Hkv * D), x, kc, vc, 128, ones, ones, 1e-6,
+                            pos, sd, cd, status=status, replay=True)
+        torch.cuda.synchronize()
+        assert int(status.item()) & ikv.STATUS_POSITION, p
+        assert torch.equal(kc.view(torch.int32), k0.view(torch.int32)), p
+        assert torch.equal(vc.view(torch.int32), v0.view(torch.int32)), p
 
 
 def test_qkv_attn_rejects_long_contexts(dev):

@@ -1,15 +1,16 @@
 """The publish protocols of the in-kernel merges, checked in the gfx950 code
 this build's compiler emits (CPU only: hipcc cross-compiles to assembly).
 
-The split decode (attn_decode.hip: decode_kernel, qkv_attn_kernel) and the
-multi-workgroup sampler (model_ops.hip: argmax_ws_kernel) publish partial
+The split decode (attn_decode.hip: decode_kernel, qkv_attn_kernel), the
+split-K GEMM (gemm.hip: gemm_nt_kernel) and the multi-workgroup sampler
+(model_ops.hip: argmax_ws_kernel) publish partial
 results with agent-coherent stores and then count their workgroup in an
 arrival counter with a relaxed agent-scope atomic; the workgroup that counts
 last reads every partial back. What makes that correct on gfx950 is the code
 between the two: the stores carry the coherence bit (sc1), and a
 `s_waitcnt vmcnt(0)` (CDNA counts stores in vmcnt) comes after the last of
 them and before the atomic, and so does the workgroup barrier where several
-wavefronts store and one counts (qkv_attn_kernel; in decode_kernel one
+wavefronts store and one counts (qkv_attn_kernel, gemm_nt_kernel; in decode_kernel one
 wavefront stores every partial and counts). A release fence would express
 the same order in the HIP memory model, but on this chip it writes back the
 L2 (measured ~6 us per launch), so the kernels rely on the emitted order
@@ -90,6 +91,14 @@ def test_split_decode_publishes_before_counting(tmp_path):
             checked += 1
     # decode_kernel<G, PRO, PAGED> for G in 1, 2, 4, 8 and qkv_attn_kernel<G>
     assert checked == 4 * 4 + 4
+
+
+def test_split_k_gemm_publishes_before_counting(tmp_path):
+    asm = device_asm(CSRC / "gemm.hip", tmp_path)
+    found = [(n, b) for n, b in functions(asm) if "gemm_nt_kernel" in n]
+    assert len(found) == 5  # the five tile shapes
+    for name, body in found:
+        check_publish_order(name, body)  # every thread stores its partial, one counts
 
 
 def test_sampler_publishes_before_counting(tmp_path):

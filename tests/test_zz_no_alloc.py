@@ -96,3 +96,34 @@ def test_noalloc_decode_rejects_what_does_not_fit(dev):
     want = ikv.attn_decode(q, kc2, vc2, 600, k_new=kn, v_new=vn)
     torch.cuda.synchronize()
     assert np.array_equal(_bits(out), _bits(want))
+
+
+@pytest.mark.gpu
+def test_noalloc_decode_replays_from_a_captured_graph(dev):
+    # For callers under HIP graph capture: after a first call on the device
+    # outside capture (which looks up the scratch array's address), one call
+    # is captured and replayed; every replay equals the workspace form bit for
+    # bit (output and the appended cache rows), with eager work in between.
+    q, kc, vc, kn, vn = _case(dev, 21, 16, 8, 3000, True)
+    kc2, vc2 = kc.clone(), vc.clone()
+    want = ikv.attn_decode(q, kc2, vc2, 3000, k_new=kn, v_new=vn)
+    out = torch.full((16, D), float("nan"), device=dev)
+    assert _noalloc(q, kc, vc, kn, vn, out, 3000) == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(out), _bits(want))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            rc = _noalloc(q, kc, vc, kn, vn, out, 3000)
+    assert rc == 0
+    torch.cuda.current_stream().wait_stream(side)
+    for i in range(3):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(_bits(out), _bits(want)), f"replay {i}: output differs"
+        assert np.array_equal(_bits(kc), _bits(kc2)), f"replay {i}: K cache differs"
+        assert np.array_equal(_bits(vc), _bits(vc2)), f"replay {i}: V cache differs"
