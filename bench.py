@@ -473,6 +473,29 @@ def hbm_probes(torch, ikv):
     return res
 
 
+def paged_vs_contiguous(torch, ikv, ctx, steps, rounds=5):
+    """Decode + append at ctx over 28 layers, contiguous and paged (64- and
+    256-token blocks, shuffled tables), graph-replayed, the three rigs timed
+    in alternation: GB/s of each round, and medians."""
+    rigs = {"contiguous": DecodeRig(torch, ikv, ctx)}
+    for bt in (64, 256):
+        rigs[f"paged{bt}"] = DecodeRig(torch, ikv, ctx, block_tokens=bt)
+    for r in rigs.values():
+        r.capture()
+        r.time(steps, 3)
+    b = decode_bytes(ctx) * steps * N_LAYER
+    res = {k: [] for k in rigs}
+    for _ in range(rounds):
+        for k, r in rigs.items():
+            res[k].append(round(b / r.time(steps, 0) / 1e9, 1))
+    out = {k: {"median_gbs": sorted(v)[len(v) // 2], "rounds_gbs": v} for k, v in res.items()}
+    for k in ("paged64", "paged256"):
+        out[k]["vs_contiguous"] = round(out[k]["median_gbs"] / out["contiguous"]["median_gbs"], 3)
+    log(f"[bench] paged vs contiguous at ctx {ctx}: " +
+        ", ".join(f"{k} {v['median_gbs']}" for k, v in out.items()))
+    return out
+
+
 def decode_timeline(torch, ikv, ctx=4096, n_head=N_HEAD, n_layer=N_LAYER, reps=30):
     """Phase timeline of one decode launch: the same workload as the headline
     (n_layer rotating caches at ctx, HIP graph), run through the stamped build
@@ -930,6 +953,9 @@ def main():
     ap.add_argument("--gemm-sweep", action="store_true",
                     help="only the prefill GEMM's tile shapes against torch.mm on the Qwen3 "
                          "projections below 2048 tokens; prints their JSON")
+    ap.add_argument("--paged-only", action="store_true",
+                    help="only decode at --ctx on contiguous and paged caches (5 alternated "
+                         "rounds each); prints their JSON")
     ap.add_argument("--probes-only", action="store_true",
                     help="only the HBM / launch probes; prints their JSON")
     ap.add_argument("--pmc-calibrate", action="store_true",
@@ -965,6 +991,10 @@ def main():
     log(f"[bench] {ikv.version()} on {torch.cuda.get_device_name(0)}")
     if args.probes_only:
         print(json.dumps(hbm_probes(torch, ikv)), flush=True)
+        return
+    if args.paged_only:
+        print(json.dumps({"paged_vs_contiguous": paged_vs_contiguous(torch, ikv, args.ctx,
+                                                                      args.steps)}), flush=True)
         return
     if args.timeline_only:
         print(json.dumps({"decode_timeline": [decode_timeline(torch, ikv, args.ctx),

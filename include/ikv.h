@@ -174,7 +174,9 @@ int ikv_qkv_attn_decode_f32(const float *w_q, const float *w_k, const float *w_v
  * (it only adds empty splits). pos[0] outside [0, n_kv_max) raises
  * IKV_STATUS_POSITION in *status and the launch runs as n_kv_max keys
  * (results invalid, accesses in bounds: the caches must hold n_kv_max
- * rows). Contiguous caches only.
+ * rows). ikv_attn_decode_rope_paged_replay_f32 (below, with the paged
+ * cache) is the paged form: it reads block-table entries only for blocks
+ * that hold keys [0, pos[0]], so the table need cover only those.
  * ------------------------------------------------------------------- */
 int ikv_attn_decode_rope_replay_f32(const float *q_raw, const float *k_raw, const float *v_new,
                                     float *k_cache, float *v_cache, float *out, int n_head,
@@ -258,6 +260,19 @@ int ikv_attn_decode_rope_paged_f32(const float *q_raw, const float *k_raw, const
                                    const float *sin_tab, const float *cos_tab, int64_t n_ctx,
                                    int *status, void *workspace, size_t workspace_bytes,
                                    void *stream);
+/* The replay form of ikv_attn_decode_rope_paged_f32 (see the replay forms
+ * above: the context is pos[0] + 1, read on the device; planned for
+ * n_kv_max keys; bit-identical to ikv_attn_decode_rope_paged_f32 at every
+ * context the replay limit allows). */
+int ikv_attn_decode_rope_paged_replay_f32(const float *q_raw, const float *k_raw,
+                                          const float *v_new, float *k_pool, float *v_pool,
+                                          const ikv_kv_pages *pages, float *out, int n_head,
+                                          int n_head_kv, int head_dim, int64_t n_kv_max,
+                                          float scale, const float *q_norm_w,
+                                          const float *k_norm_w, float eps, const int32_t *pos,
+                                          const float *sin_tab, const float *cos_tab,
+                                          int64_t n_ctx, int *status, void *workspace,
+                                          size_t workspace_bytes, void *stream);
 int ikv_attn_prefill_paged_f32(const float *q, const float *k_pool, const float *v_pool,
                                const ikv_kv_pages *pages, float *out, int n_head, int n_head_kv,
                                int head_dim, int64_t n_q, int64_t n_kv, int64_t n_past,

@@ -126,7 +126,8 @@ int ikv_qwen3_set_fusion(ikv_qwen3 *m, int on);
  * HIP graph once per range of contexts the decode's split plan allows (up to
  * 256 tokens) and replayed, the position advancing on the device, so that a
  * step costs the host one graph launch and one sampler launch; the tokens are
- * those of the eager steps. Taken with a contiguous cache and fusions on.
+ * those of the eager steps. Taken with a contiguous or paged cache (not the
+ * offload tier) and fusions on.
  * 0: every step is built and launched from the host (the reference's way,
  * src/model.cpp:164-311). No counterpart in the reference. */
 int ikv_qwen3_set_step_replay(ikv_qwen3 *m, int on);

@@ -620,12 +620,39 @@ __device__ __forceinline__ void decode_body(
 
   // Cache row offset of the tile at token `base`: tiles start at multiples
   // of TILE from a split start (itself a multiple of TILE), so a paged
-  // cache's block (a multiple of 64 tokens) holds each tile whole.
+  // cache's block (a multiple of 64 tokens) holds each tile whole. The
+  // offsets of the first kSplitBlocks blocks the split reads are loaded
+  // together at its start (their table loads overlap each other and the
+  // prologue), so no tile's loads wait on a table load; a longer split looks
+  // the later blocks up as it reaches them. Only entries of blocks that hold
+  // keys of [t_begin, t_end) are read (an empty split of a replay launch
+  // reads the block of the context's last key).
+  constexpr int kSplitBlocks = 4;
+  int64_t blk_shift[kSplitBlocks] = {};
+  int first_block = 0;
+  if constexpr (PAGED) {
+    first_block = min(t_begin, t_end - 1) / pages.bt;
+    const int last_block = (t_end - 1) / pages.bt;
+#pragma unroll
+    for (int i = 0; i < kSplitBlocks; ++i)
+      if (first_block + i <= last_block)
+        blk_shift[i] = ikv::page_shift(pages, (first_block + i) * pages.bt);
+  }
   auto shift_of = [&](int base) -> int64_t {
-    if constexpr (PAGED)
-      return ikv::page_shift(pages, base);
-    else
+    if constexpr (PAGED) {
+      const int i = base / pages.bt - first_block;
+      int64_t sh = 0;
+      bool hit = false;
+#pragma unroll
+      for (int j = 0; j < kSplitBlocks; ++j)
+        if (i == j) {
+          sh = blk_shift[j];
+          hit = true;
+        }
+      return hit ? sh : ikv::page_shift(pages, base);
+    } else {
       return 0;
+    }
   };
 
   // Two register buffers of K/V rows: tile t+1 loads into one while tile t
@@ -639,8 +666,11 @@ __device__ __forceinline__ void decode_body(
     const float *p = v_new + head_off;
     vnew = make_float4(load_agent(p), load_agent(p + 1), load_agent(p + 2), load_agent(p + 3));
   }
+  // (an empty split of a replay launch, past the context, clamps every row
+  // onto the context's last one: its block, not the unallocated one at
+  // t_begin)
   load_tile<COH>(ka, va, t_begin, t_end - 1, wave, half, new_row, kc, vc, k_new, v_new, tok_stride,
-                 head_off, shift_of(t_begin));
+                 head_off, shift_of(min(t_begin, t_end - 1)));
 
   float4 qv[G];
   float4 knew_rot = make_float4(0.f, 0.f, 0.f, 0.f);  // this lane's piece of rope(norm(k_new))
@@ -1235,6 +1265,18 @@ extern "C" int ikv_attn_decode_rope_replay_f32(
                             n_head_kv, head_dim, n_kv_max, scale, q_norm_w, k_norm_w, eps, pos,
                             sin_tab, cos_tab, n_ctx, status, workspace, workspace_bytes, stream,
                             true);
+}
+
+extern "C" int ikv_attn_decode_rope_paged_replay_f32(
+    const float *q_raw, const float *k_raw, const float *v_new, float *k_pool, float *v_pool,
+    const ikv_kv_pages *pages, float *out, int n_head, int n_head_kv, int head_dim,
+    int64_t n_kv_max, float scale, const float *q_norm_w, const float *k_norm_w, float eps,
+    const int32_t *pos, const float *sin_tab, const float *cos_tab, int64_t n_ctx, int *status,
+    void *workspace, size_t workspace_bytes, void *stream) {
+  if (!pages) return -EINVAL;
+  return decode_rope_common(q_raw, k_raw, v_new, k_pool, v_pool, pages, out, n_head, n_head_kv,
+                            head_dim, n_kv_max, scale, q_norm_w, k_norm_w, eps, pos, sin_tab,
+                            cos_tab, n_ctx, status, workspace, workspace_bytes, stream, true);
 }
 
 extern "C" int64_t ikv_attn_decode_replay_limit(int n_head, int n_head_kv, int head_dim,

@@ -781,7 +781,7 @@ infer::expected<void, std::error_code> HIPBackend::dispatch(Tensor *node) {
           ++_stats.fused_append_decode;
         }
         const bool paged = is_paged(k) && is_paged(v);
-        if (_replay_max > 0 && (paged || !_rope_into_attn.count(node) || nkv > _replay_max))
+        if (_replay_max > 0 && (!_rope_into_attn.count(node) || nkv > _replay_max))
           return infer::fail(std::errc::not_supported);
         const int64_t plan_kv = _replay_max > 0 ? _replay_max : nkv;
         const size_t need = ikv_attn_decode_workspace_bytes(int(Hq), int(Hkv), int(D), plan_kv);
@@ -792,6 +792,14 @@ infer::expected<void, std::error_code> HIPBackend::dispatch(Tensor *node) {
           if (!a) return infer::unexpected(a.error());
           const RopeTables *tab = a->tab;
           ++_stats.fused_rope_decode;
+          if (_replay_max > 0 && paged)
+            return check_ikv(ikv_attn_decode_rope_paged_replay_f32(
+                                 a->q_raw, a->k_raw, a->v_new, static_cast<float *>(k->data),
+                                 static_cast<float *>(v->data), &pg, static_cast<float *>(node->data),
+                                 int(Hq), int(Hkv), int(D), plan_kv, p.scale, a->q_norm_w,
+                                 a->k_norm_w, a->eps, a->pos, tab->sin, tab->cos, tab->n_ctx,
+                                 _status, _workspace, _workspace_bytes, s),
+                             "attn_decode_rope_paged_replay");
           if (_replay_max > 0)
             return check_ikv(ikv_attn_decode_rope_replay_f32(
                                  a->q_raw, a->k_raw, a->v_new, static_cast<float *>(k->data),

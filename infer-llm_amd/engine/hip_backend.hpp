@@ -68,8 +68,9 @@ class HIPBackend : public Backend {
   // n_kv_max > 0: one-token decodes launch in their replay form (the context
   // read from the position on the device, planned for n_kv_max keys), so
   // that the step can be captured once and replayed at later positions; 0
-  // restores the per-context launches. Contiguous caches with the qk-norm /
-  // RoPE fusion only (other decodes then fail with not_supported).
+  // restores the per-context launches. Decodes with the qk-norm / RoPE
+  // fusion only, contiguous or paged (other decodes then fail with
+  // not_supported).
   void set_decode_replay(int64_t n_kv_max) { _replay_max = n_kv_max; }
   struct Stats {
     int launches = 0;

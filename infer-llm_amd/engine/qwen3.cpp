@@ -523,8 +523,10 @@ infer::expected<void, std::error_code> Qwen3Runner::generate(const std::vector<i
   // graph holds one address, read and write device slot kReplaySlot.
   _replay_stats = {};
   drop_step_graph();
-  bool replay = _replay && _kv_opt.block_tokens == 0 && _kv_opt.offload_bytes == 0 &&
-                _backend.fusion();
+  // (a paged cache replays too: its block tables sit at fixed device
+  // addresses, and a step that opens a block writes the new entries before
+  // the graph is launched)
+  bool replay = _replay && _kv_opt.offload_bytes == 0 && _backend.fusion();
   const bool one_slot = replay;  // the device token stays in kReplaySlot throughout
   _cur_step = 0;
   if (auto r = enqueue_step(prompt.data(), int64_t(prompt.size()), 1, one_slot ? kReplaySlot : 0,

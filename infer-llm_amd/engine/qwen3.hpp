@@ -144,8 +144,8 @@ class Qwen3Runner {
   // Page-in / write-back counts of an offloaded cache (zeros otherwise).
   OffloadStats offload_stats() const;
   // Decode steps of generate() replayed from a captured HIP graph (default
-  // on). Taken with a contiguous cache and the backend's fusions on; other
-  // configurations, and any step whose capture fails, launch eagerly.
+  // on). Taken with a contiguous or paged cache and the backend's fusions
+  // on; the offload tier, and any step whose capture fails, launch eagerly.
   void set_step_replay(bool on) { _replay = on; }
   struct ReplayStats {
     int captures = 0;  // decode steps captured (each then replayed)

@@ -97,6 +97,12 @@ SIGNATURES = {
          _c_int, _c_int, _c_int64, _c_float, _c_void_p, _c_void_p, _c_float, _c_void_p,
          _c_void_p, _c_void_p, _c_int64, _c_void_p, _c_void_p, _c_size_t, _c_void_p],
     ),
+    "ikv_attn_decode_rope_paged_replay_f32": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_pages, _c_void_p, _c_int,
+         _c_int, _c_int, _c_int64, _c_float, _c_void_p, _c_void_p, _c_float, _c_void_p,
+         _c_void_p, _c_void_p, _c_int64, _c_void_p, _c_void_p, _c_size_t, _c_void_p],
+    ),
     "ikv_attn_prefill_paged_f32": (
         _c_int,
         [_c_void_p, _c_void_p, _c_void_p, _c_pages, _c_void_p, _c_int, _c_int, _c_int,
@@ -498,8 +504,9 @@ def attn_decode_paged(q, k_pool, v_pool, table, block_tokens: int, n_kv: int, *,
 def attn_decode_rope_paged(q_raw, k_raw, v_new, k_pool, v_pool, table, block_tokens: int,
                            n_kv: int, q_norm_w, k_norm_w, eps: float, pos, sin_tab, cos_tab, *,
                            out=None, scale: float = 0.0, status=None, page_status=None,
-                           workspace=None, stream=None):
-    """attn_decode_rope over a paged pool."""
+                           workspace=None, replay=False, stream=None):
+    """attn_decode_rope over a paged pool (replay=True: the replay form, n_kv
+    the planned maximum, the context pos[0] + 1 read on the device)."""
     torch = _torch()
     n_head, D = q_raw.shape[-2], q_raw.shape[-1]
     n_head_kv = k_pool.shape[-2]
@@ -508,12 +515,13 @@ def attn_decode_rope_paged(q_raw, k_raw, v_new, k_pool, v_pool, table, block_tok
     if workspace is None:
         workspace = decode_workspace(n_head, n_head_kv, D, n_kv, device=q_raw.device)
     pg = kv_pages(table, block_tokens, k_pool, page_status)
-    rc = load().ikv_attn_decode_rope_paged_f32(
+    fn = "ikv_attn_decode_rope_paged_replay_f32" if replay else "ikv_attn_decode_rope_paged_f32"
+    rc = getattr(load(), fn)(
         _ptr(q_raw), _ptr(k_raw), _ptr(v_new), _ptr(k_pool), _ptr(v_pool), ctypes.byref(pg),
         _ptr(out), n_head, n_head_kv, D, n_kv, scale, _ptr(q_norm_w), _ptr(k_norm_w), eps,
         _ptr(pos), _ptr(sin_tab), _ptr(cos_tab), sin_tab.shape[0], _ptr(status), _ptr(workspace),
         workspace.numel() * 4, _stream(stream))
-    _check("ikv_attn_decode_rope_paged_f32", rc)
+    _check(fn, rc)
     return out
 
 

@@ -754,6 +754,62 @@ def test_decode_replay_equals_per_context_launches(dev, Hq, n_kv_lo, width):
                                   host(b).reshape(-1).view(np.uint32)), f"n_kv {n_kv}: {what}"
 
 
+@pytest.mark.parametrize("Hq,n_kv_lo,width,bt", [(16, 2050, 256, 256), (16, 300, 200, 64),
+                                                  (32, 129, 256, 128), (16, 40, 256, 64)])
+def test_paged_decode_replay_equals_contiguous_launches(dev, Hq, n_kv_lo, width, bt):
+    """The paged replay form (context from pos, planned for the replay
+    limit) over a shuffled pool whose block table holds entries only for the
+    blocks of keys [0, n_kv) (later entries -1, as before a sequence grows
+    into them) against the contiguous per-context launch: outputs and the
+    appended rows bit for bit, and no block-table error raised."""
+    import torch
+    Hkv, D = 8, 128
+    m = ikv.decode_replay_limit(Hq, Hkv, D, n_kv_lo, width)
+    th = oracle.rope_theta_table(1e6, D, m + 8)
+    s, c = ikv.rope_sincos_table(th)
+    sd, cd = dev_t(s, dev), dev_t(c, dev)
+    seed = 1900 + n_kv_lo + Hq + bt
+    qn_w = dev_t(1 + 0.3 * synth.normal(seed, (D,)), dev)
+    kn_w = dev_t(1 + 0.3 * synth.normal(seed + 1, (D,)), dev)
+    hist_k = synth.normal(seed + 2, (m, Hkv, D))
+    hist_v = synth.normal(seed + 3, (m, Hkv, D))
+    n_blocks = -(-m // bt)
+    pool_blocks = n_blocks + 3
+    order = np.random.default_rng(seed).permutation(pool_blocks)[:n_blocks].astype(np.int32)
+    ws_r = ikv.decode_workspace(Hq, Hkv, D, m, device=dev)
+    pos = torch.zeros(1, dtype=torch.int32, device=dev)
+    for n_kv in sorted({n_kv_lo, (n_kv_lo + m) // 2, m}):
+        pos.fill_(n_kv - 1)
+        g = seed + 10 * n_kv
+        kc1, vc1 = dev_t(hist_k, dev), dev_t(hist_v, dev)
+        pools = []
+        for hist in (hist_k, hist_v):
+            pool = np.zeros((pool_blocks * bt, Hkv, D), np.float32)
+            for b, blk in enumerate(order):
+                rows = hist[b * bt:(b + 1) * bt]
+                pool[blk * bt:blk * bt + len(rows)] = rows
+            pools.append(dev_t(pool, dev))
+        live = -(-n_kv // bt)  # blocks holding keys [0, n_kv)
+        table = torch.tensor(np.where(np.arange(n_blocks) < live, order, -1).astype(np.int32),
+                             device=dev)
+        page_status = torch.zeros(1, dtype=torch.int32, device=dev)
+        ws1 = ikv.decode_workspace(Hq, Hkv, D, n_kv, device=dev)
+        q_raw = dev_t(synth.normal(g, (Hq, D)), dev)
+        k_raw = dev_t(synth.normal(g + 1, (Hkv, D)), dev)
+        v_new = dev_t(synth.normal(g + 2, (Hkv, D)), dev)
+        out1 = ikv.attn_decode_rope(q_raw, k_raw, v_new, kc1, vc1, n_kv, qn_w, kn_w, 1e-6, pos,
+                                    sd, cd, workspace=ws1)
+        out2 = ikv.attn_decode_rope_paged(q_raw, k_raw, v_new, pools[0], pools[1], table, bt, m,
+                                          qn_w, kn_w, 1e-6, pos, sd, cd, page_status=page_status,
+                                          workspace=ws_r, replay=True)
+        assert np.array_equal(host(out1).view(np.uint32), host(out2).view(np.uint32)), n_kv
+        assert int(host(page_status)[0]) == 0, f"n_kv {n_kv}: block-table error raised"
+        t = n_kv - 1
+        row = order[t // bt] * bt + t % bt
+        for cont, pool in ((kc1, pools[0]), (vc1, pools[1])):
+            assert np.array_equal(host(cont)[t].view(np.uint32), host(pool)[row].view(np.uint32))
+
+
 def test_decode_replay_position_past_plan_is_flagged(dev):
     import torch
     Hq, Hkv, D = 16, 8, 128

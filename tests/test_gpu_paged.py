@@ -229,6 +229,12 @@ def test_paged_engine_matches_contiguous_and_oracle(dev, oracle_pool):
     st = paged.last_stats()
     assert b1 == a1
     assert st["fused_rope_decode"] == cfg.n_layer and st["fused_append_decode"] == cfg.n_layer
+    # every decode step replayed from a captured graph, the steps that open
+    # a block (128) writing their table entries before the launch
+    assert st["step_replays"] == 59 and st["step_captures"] >= 1
+    paged.set_step_replay(False)
+    assert paged.generate(p1, 60)[0] == a1 and paged.last_stats()["step_replays"] == 0
+    paged.set_step_replay(True)
     # the next sequence gets the returned blocks in reverse order: a
     # non-identity block table, same tokens
     a2 = flat.generate(p2, 150)[0]
