@@ -226,6 +226,7 @@ def prefill_only(torch, ikv, p, reps):
     into a 28-layer contiguous cache and the causal GQA prefill of p tokens,
     each timed over `reps` launches per layer with HIP events."""
     dev = torch.device("cuda:0")
+    warm_clocks(torch, 1.0)
     t_pre = time_prefill(torch, ikv, p, reps)
     rows = torch.from_numpy(seeded(ikv, 2, 20 + p, (p, N_HEAD_KV, D))).to(dev)
     caches = [torch.empty((p, N_HEAD_KV, D), device=dev) for _ in range(N_LAYER)]
@@ -1098,6 +1099,7 @@ def main():
         log(f"[bench] hbm probes: {extra['hbm_probes']}")
         extra["decode_timeline"] = decode_timeline(torch, ikv, args.ctx)
         log(f"[bench] decode timeline: {extra['decode_timeline']}")
+        warm_clocks(torch, 1.0)
         for p in (32, 64, 128, 256, 2048):
             t = time_prefill(torch, ikv, p, 20 if p < 2048 else 10)
             tf = prefill_flops(p) / t / 1e12

@@ -62,9 +62,9 @@ namespace {
 #ifndef IKV_DECODE_TIMELINE
 #define IKV_DECODE_TIMELINE 0
 #endif
+#if IKV_DECODE_TIMELINE
 constexpr int kTimelineWgs = 1024;
 constexpr int kTimelineWords = 16;
-#if IKV_DECODE_TIMELINE
 __device__ unsigned long long g_timeline[kTimelineWgs * kTimelineWords];
 #endif
 struct Timeline {
