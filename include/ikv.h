@@ -81,7 +81,12 @@ int ikv_append_f32(void *dst_rows, const void *src_rows, size_t n_rows, size_t r
  *            context it will serve). Unused, and may be NULL, when the
  *            context fits one split. Launches that share one workspace must
  *            be ordered (same stream); concurrent ones race.
- * head_dim must be 128; n_head/n_head_kv must be 1, 2, 4 or 8.
+ * The split kernel takes head_dim 128 with n_head/n_head_kv 1, 2, 4 or 8.
+ * Any other head_dim in [1, 512] and any n_head that n_head_kv divides run
+ * a generic path instead (the append, then one workgroup per query head over
+ * the keys; with qk-norm + RoPE folded in, those run first as their own
+ * kernels into the workspace, which then holds the rotated q and k rows):
+ * same semantics, slower, no replay form. Larger head_dim: -ENOTSUP.
  * ------------------------------------------------------------------- */
 size_t ikv_attn_decode_workspace_bytes(int n_head, int n_head_kv, int head_dim, int64_t n_kv);
 
@@ -206,7 +211,9 @@ int64_t ikv_attn_decode_replay_limit(int n_head, int n_head_kv, int head_dim, in
  * src/kernels/cuda/kernel_f32.cu:346). F32 MFMA tiles; K/V tiles staged in
  * LDS and shared by the n_head/n_head_kv query heads of a KV head.
  * Replaces compute_flash_attn for n_q > 1. Needs no workspace.
- * head_dim must be 128; n_head/n_head_kv must be 1, 2, 4 or 8.
+ * The MFMA kernel takes head_dim 128 with n_head/n_head_kv 1, 2, 4 or 8;
+ * any other head_dim in [1, 512] and any n_head that n_head_kv divides run
+ * the generic path (decode above). Larger head_dim: -ENOTSUP.
  * ------------------------------------------------------------------- */
 int ikv_attn_prefill_f32(const float *q, const float *k, const float *v, float *out, int n_head,
                          int n_head_kv, int head_dim, int64_t n_q, int64_t n_kv, int64_t n_past,

@@ -43,6 +43,7 @@
 // cache is bit-identical to the one the separate ops produce. The prologue's
 // loads are issued first and the first tile's K/V loads right after them, so
 // the prologue's arithmetic runs while the tile is in flight.
+#include "attn_generic.hpp"
 #include "coherent.hpp"
 #include "gemv_dev.hpp"
 #include "ikv_common.hpp"
@@ -1034,6 +1035,60 @@ int shape_status(int n_head, int n_head_kv, int head_dim, int64_t n_kv) {
   return 0;
 }
 
+// The workspace of the generic path (attn_generic.hpp) with qk-norm + RoPE
+// folded in: the new token's rotated q and k rows.
+size_t generic_ws_bytes(int n_head, int n_head_kv, int head_dim) {
+  return align256(sizeof(float) * static_cast<size_t>(n_head) * head_dim) +
+         align256(sizeof(float) * static_cast<size_t>(n_head_kv) * head_dim);
+}
+
+// A decode step on the generic attention path, for head sizes and query
+// groupings the decode kernel does not take: the prologue (qk-RMSNorm + RoPE
+// of the new token, into the workspace) and the append run as the separate
+// kernels, then the attention of the one query over n_kv keys. No replay
+// form (-ENOTSUP).
+int decode_generic(const float *q, float *k_cache, float *v_cache, const float *k_new,
+                   const float *v_new, float *out, int n_head, int n_head_kv, int head_dim,
+                   int64_t n_kv, float scale, void *workspace, size_t workspace_bytes,
+                   const Prologue *pro, const ikv_kv_pages *pages, const ikv::Pages *pg,
+                   hipStream_t s) {
+  if (pro && pro->dyn_max > 0) return -ENOTSUP;
+  if (n_kv > INT_MAX / 2) return -EOVERFLOW;
+  const size_t row_bytes = sizeof(float) * static_cast<size_t>(n_head_kv) * head_dim;
+  if (k_new && pages && row_bytes % 16 != 0) return -ENOTSUP;
+  if (pro) {
+    if (!workspace || workspace_bytes < generic_ws_bytes(n_head, n_head_kv, head_dim))
+      return -EINVAL;
+    float *q_rot = static_cast<float *>(workspace);
+    float *k_rot = reinterpret_cast<float *>(
+        static_cast<char *>(workspace) +
+        align256(sizeof(float) * static_cast<size_t>(n_head) * head_dim));
+    int rc = ikv_qk_norm_rope_f32(q, pro->q_norm_w, q_rot, pro->pos, 1, n_head, head_dim,
+                                  pro->eps, pro->sin_tab, pro->cos_tab, pro->n_ctx, pro->status,
+                                  s);
+    if (!rc)
+      rc = ikv_qk_norm_rope_f32(k_new, pro->k_norm_w, k_rot, pro->pos, 1, n_head_kv, head_dim,
+                                pro->eps, pro->sin_tab, pro->cos_tab, pro->n_ctx, pro->status, s);
+    if (rc) return rc;
+    q = q_rot;
+    k_new = k_rot;
+  }
+  if (k_new) {
+    int rc;
+    if (pages) {
+      rc = ikv_append_paged_f32(k_cache, k_new, pages, n_kv - 1, 1, row_bytes, s);
+      if (!rc) rc = ikv_append_paged_f32(v_cache, v_new, pages, n_kv - 1, 1, row_bytes, s);
+    } else {
+      const size_t at = static_cast<size_t>(n_kv - 1) * (row_bytes / sizeof(float));
+      rc = ikv_append_f32(k_cache + at, k_new, 1, row_bytes, s);
+      if (!rc) rc = ikv_append_f32(v_cache + at, v_new, 1, row_bytes, s);
+    }
+    if (rc) return rc;
+  }
+  return ikv::attn_generic(q, k_cache, v_cache, pg, out, n_head, n_head_kv, head_dim, 1, n_kv,
+                           n_kv - 1, scale, s);
+}
+
 int decode_common(const float *q, float *k_cache, float *v_cache, const float *k_new,
                   const float *v_new, float *out, int n_head, int n_head_kv, int head_dim,
                   int64_t n_kv, float scale, void *workspace, size_t workspace_bytes,
@@ -1045,7 +1100,13 @@ int decode_common(const float *q, float *k_cache, float *v_cache, const float *k
     if (const int rc = ikv::pages_arg(pages, pg)) return rc;
   }
   if ((k_new == nullptr) != (v_new == nullptr)) return -EINVAL;
-  if (const int rc = shape_status(n_head, n_head_kv, head_dim, n_kv)) return rc;
+  if (const int rc = shape_status(n_head, n_head_kv, head_dim, n_kv)) {
+    if (rc == -ENOTSUP && ikv::generic_attn_shape(n_head, n_head_kv, head_dim))
+      return decode_generic(q, k_cache, v_cache, k_new, v_new, out, n_head, n_head_kv, head_dim,
+                            n_kv, scale, workspace, workspace_bytes, pro, pages,
+                            pages ? &pg : nullptr, static_cast<hipStream_t>(stream));
+    return rc;
+  }
   const int G = n_head / n_head_kv;
   if (!ikv::aligned16(q) || !ikv::aligned16(k_cache) || !ikv::aligned16(v_cache) ||
       !ikv::aligned16(out) || (k_new && (!ikv::aligned16(k_new) || !ikv::aligned16(v_new))))
@@ -1082,7 +1143,10 @@ int decode_common(const float *q, float *k_cache, float *v_cache, const float *k
 
 extern "C" size_t ikv_attn_decode_workspace_bytes(int n_head, int n_head_kv, int head_dim,
                                                   int64_t n_kv) {
-  if (shape_status(n_head, n_head_kv, head_dim, n_kv)) return 0;
+  if (const int rc = shape_status(n_head, n_head_kv, head_dim, n_kv))
+    return rc == -ENOTSUP && ikv::generic_attn_shape(n_head, n_head_kv, head_dim)
+               ? generic_ws_bytes(n_head, n_head_kv, head_dim)
+               : 0;
   const Plan p = plan_for(n_head, n_head_kv, n_kv);
   return ws_layout(n_head, n_head_kv, p.n_splits).total;
 }

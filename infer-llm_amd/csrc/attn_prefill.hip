@@ -46,6 +46,7 @@
 //     shared by two waves the one with MFMAs to issue goes first and the
 //     other's softmax fills the matrix pipe's gaps (P = 2048: 147.3 ->
 //     145.8 us, alternated runs on one box).
+#include "attn_generic.hpp"
 #include "ikv_common.hpp"
 #include "../../include/ikv.h"
 
@@ -489,9 +490,13 @@ int prefill_common(const float *q, const float *k, const float *v, const ikv_kv_
   }
   if (n_head <= 0 || n_head_kv <= 0 || n_head % n_head_kv != 0) return -EINVAL;
   if (n_q < 0 || n_kv <= 0 || n_past < 0) return -EINVAL;
-  if (head_dim != D) return -ENOTSUP;
   const int G = n_head / n_head_kv;
-  if (G != 1 && G != 2 && G != 4 && G != 8) return -ENOTSUP;
+  if (head_dim != D || (G != 1 && G != 2 && G != 4 && G != 8)) {
+    // other head sizes and groupings: the generic path
+    if (!ikv::generic_attn_shape(n_head, n_head_kv, head_dim)) return -ENOTSUP;
+    return ikv::attn_generic(q, k, v, pg, out, n_head, n_head_kv, head_dim, n_q, n_kv, n_past,
+                             scale, static_cast<hipStream_t>(stream));
+  }
   if (n_q > INT_MAX / 2 || n_kv > INT_MAX / 2 || n_past > INT_MAX / 2) return -EOVERFLOW;
   if (!ikv::aligned16(q) || !ikv::aligned16(k) || !ikv::aligned16(v) || !ikv::aligned16(out))
     return -EINVAL;

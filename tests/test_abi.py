@@ -104,8 +104,12 @@ def test_decode_rejects_bad_arguments_without_launching():
     assert call(kn=P) == -errno.EINVAL                 # k_new without v_new
     assert call(n_head=12) == -errno.EINVAL            # not a multiple of n_head_kv
     assert call(n_kv=0) == -errno.EINVAL
-    assert call(head_dim=64) == -errno.ENOTSUP
-    assert call(n_head=24) == -errno.ENOTSUP           # group of 3
+    assert call(head_dim=1024) == -errno.ENOTSUP       # past the generic path's 512
+    assert call(n_head=24, head_dim=640) == -errno.ENOTSUP
+    # other head sizes and groups take the generic path: its workspace holds
+    # the rotated q and k rows of the fused prologue
+    assert ikv.decode_workspace_bytes(24, 8, 64, 100) == 24 * 64 * 4 + 8 * 64 * 4
+    assert ikv.decode_workspace_bytes(12, 4, 96, 5000) == 12 * 96 * 4 + 4 * 96 * 4 + 0
     assert call(q=P + 4) == -errno.EINVAL              # misaligned
     assert call(n_kv=4097) == -errno.EINVAL            # split-K needs a workspace
     need = ikv.decode_workspace_bytes(ok["n_head"], ok["n_head_kv"], 128, 4097)
@@ -229,7 +233,7 @@ def test_prefill_and_rows_reject_bad_arguments():
     P = 64
     assert _rc("ikv_attn_prefill_f32", P, P, P, P, 16, 8, 128, 0, 10, 0, 0.0, None) == 0  # n_q=0
     assert _rc("ikv_attn_prefill_f32", None, P, P, P, 16, 8, 128, 4, 10, 0, 0.0, None) == -errno.EINVAL
-    assert _rc("ikv_attn_prefill_f32", P, P, P, P, 16, 8, 96, 4, 10, 0, 0.0, None) == -errno.ENOTSUP
+    assert _rc("ikv_attn_prefill_f32", P, P, P, P, 16, 8, 1024, 4, 10, 0, 0.0, None) == -errno.ENOTSUP
     assert _rc("ikv_rms_norm_f32", None, P, P, 4, 128, 1e-6, None) == -errno.EINVAL
     assert _rc("ikv_rms_norm_f32", P, P, P, 0, 128, 1e-6, None) == 0
     assert _rc("ikv_rope_neox_f32", P, P, P, 2, 8, 127, P, P, 10, None, None) == -errno.EINVAL
@@ -255,7 +259,8 @@ def test_workspace_bytes_grow_with_context_and_are_bounded():
     assert all(s > 0 for s in sizes)
     assert sizes == sorted(sizes)
     assert sizes[-1] <= 16 * 1024 * (128 + 2) * 4 + 4096  # at most 1024 splits per head
-    assert ikv.decode_workspace_bytes(16, 8, 64, 100) == 0
+    assert ikv.decode_workspace_bytes(16, 8, 64, 100) == (16 + 8) * 64 * 4  # generic path
+    assert ikv.decode_workspace_bytes(16, 8, 1024, 100) == 0
 
 
 def test_sincos_table_is_bitwise_glibc():
