@@ -46,6 +46,10 @@
 //     shared by two waves the one with MFMAs to issue goes first and the
 //     other's softmax fills the matrix pipe's gaps (P = 2048: 147.3 ->
 //     145.8 us, alternated runs on one box).
+//   * Two 4-wave key-split groups use their own double buffers, so a round
+//     of tiles needs only the waves of one group to agree: each group passes
+//     an LDS arrival counter instead of the workgroup barrier, and the
+//     groups drift apart (P = 2048: 144.4 -> 141.4 us, alternated runs).
 #include "attn_generic.hpp"
 #include "ikv_common.hpp"
 #include "../../include/ikv.h"
@@ -143,6 +147,29 @@ __global__ __launch_bounds__(NW * 64) void prefill_kernel(const float *__restric
     v1 = k1 + TILE;
     xch0 = s_buf[0][0];
   }
+  // Group barrier of the two-group tile loop: an LDS counter per group that
+  // each of its waves raises by one per round; a wave waits for WPG arrivals
+  // per round so far. Every wave of a group runs the same rounds (the loop
+  // bounds are per workgroup), so every wait ends.
+  __shared__ unsigned s_arrive[NG];
+  unsigned rounds = 0;
+  if constexpr (NG == 2) {
+    if (threadIdx.x < NG) s_arrive[threadIdx.x] = 0;
+  }
+  auto group_sync = [&]() {
+    if constexpr (NG == 2) {
+      ++rounds;
+      if (lane == 0)
+        __hip_atomic_fetch_add(&s_arrive[grp], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+      const unsigned target = WPG * rounds;
+      while (static_cast<int>(__hip_atomic_load(&s_arrive[grp], __ATOMIC_ACQUIRE,
+                                                __HIP_MEMORY_SCOPE_WORKGROUP) -
+                              target) < 0)
+        __builtin_amdgcn_s_sleep(1);
+    } else {
+      __syncthreads();
+    }
+  };
   const int kk = lane >> 4;
   const int j = lane & 15;
   const int row = w * 16 + j;
@@ -358,12 +385,12 @@ __global__ __launch_bounds__(NW * 64) void prefill_kernel(const float *__restric
     for (int t0 = 0; t0 < n_tiles; t0 += 2 * NG) {
       const int ta = t0 + grp;
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's loads of its tile landed
-      __syncthreads();                      // everyone's landed; the other buffers are free
+      group_sync();                         // the group's landed; its other buffers are free
       if (ta < n_tiles) step(k0, v0, ta, k1, v1, ta + NG < n_tiles, ta + NG);
       if (t0 + NG >= n_tiles) break;
       const int tb = t0 + NG + grp;
       __builtin_amdgcn_s_waitcnt(0x0F70);
-      __syncthreads();
+      group_sync();
       if (tb < n_tiles) step(k1, v1, tb, k0, v0, tb + NG < n_tiles, tb + NG);
     }
 
