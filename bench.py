@@ -646,9 +646,13 @@ def model_bench(configs, cpu_tokens):
 
     res = {}
     gpu_tokens0 = None
-    runs = [(c, 0) for c in configs]
-    if 3 in configs:
-        runs.append((3, 256))  # config 3 again on a paged cache of 256-token blocks
+    runs = []
+    for c in configs:
+        runs.append((c, 0))
+        if c == 3:
+            # config 3 again on a paged cache of 256-token blocks, right after
+            # the contiguous run so that both see the same clocks
+            runs.append((3, 256))
     for c, bt in runs:
         arch, P, N = MODEL_CONFIGS[c]
         cfg = getattr(qwen3, arch)

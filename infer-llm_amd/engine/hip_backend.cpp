@@ -26,6 +26,21 @@ infer::expected<void, std::error_code> check_hip(hipError_t e, const char *what)
   return infer::fail(std::errc::io_error);
 }
 
+// Host -> device copies this small ride in a kernel's arguments: the runtime
+// takes the bytes at launch, so the caller's buffer is free on return and the
+// write is ordered on the stream like any launch, with no stream
+// synchronisation (a paged cache's block-table entries, written when a step
+// opens a block, are the common case: 28 synchronous copies there stalled the
+// decode pipeline every time a block opened).
+constexpr size_t kArgCopyBytes = 256;
+struct ArgBytes {
+  unsigned char b[kArgCopyBytes];
+};
+__global__ void set_bytes_kernel(unsigned char *dst, ArgBytes src, int n) {
+  const int i = static_cast<int>(threadIdx.x);
+  if (i < n) dst[i] = src.b[i];
+}
+
 bool contiguous_f32(const Tensor *t) {
   return t && t->data && t->dataType == GGML_TYPE_F32 && t->is_contiguous();
 }
@@ -198,6 +213,14 @@ infer::expected<void, std::error_code> HIPBackend::copy_tensor_set(Tensor *tenso
   if (!tensor || !tensor->data || !data) return infer::fail(std::errc::invalid_argument);
   if (offset + size > tensor->byte_size()) return infer::fail(std::errc::invalid_argument);
   if (auto r = set_device(); !r) return r;
+  if (size == 0) return {};
+  if (size <= kArgCopyBytes) {
+    ArgBytes a;
+    std::memcpy(a.b, data, size);
+    set_bytes_kernel<<<1, kArgCopyBytes, 0, _stream>>>(
+        static_cast<unsigned char *>(tensor->data) + offset, a, static_cast<int>(size));
+    return check_hip(hipGetLastError(), "copy_tensor_set (kernel argument)");
+  }
   auto r = check_hip(hipMemcpyAsync(static_cast<char *>(tensor->data) + offset, data, size,
                                     hipMemcpyHostToDevice, _stream),
                      "copy_tensor_set");

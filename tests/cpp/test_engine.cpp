@@ -108,6 +108,7 @@ static void paged_cpu_tests();
 static void offload_cpu_tests();
 static void offload_gpu_tests(HIPBackend *hip);
 static void producer_cache_gpu_tests(HIPBackend *hip);
+static void host_copy_gpu_tests(HIPBackend *hip);
 
 static void cpu_tests() {
   {
@@ -683,8 +684,38 @@ static void gpu_tests() {
   CHECK(kv.release_sequence(*sid), "release sequence (frees HBM caches)");
   for (auto &t : qw_d) hip->free(BufferKind::WEIGHTS, t->data);
   for (auto &t : kw_d) hip->free(BufferKind::WEIGHTS, t->data);
+  host_copy_gpu_tests(hip);
   producer_cache_gpu_tests(hip);
   offload_gpu_tests(hip);
+}
+
+// copy_tensor_set: small copies (up to 256 bytes) travel in a kernel's
+// arguments, larger ones through hipMemcpyAsync. At sizes either side of
+// that bound and at unaligned offsets, the device bytes equal the host's,
+// the bytes around the range are untouched, and the host buffer may be
+// overwritten at once after the call (the copy took its bytes at launch).
+static void host_copy_gpu_tests(HIPBackend *hip) {
+  const size_t n = 4096;
+  Tensor t("host_copy", GGML_TYPE_I32, {int64_t(n / 4)});
+  t.data = *hip->alloc(BufferKind::ACTIVATION, n);
+  t.backend = hip;
+  t.device = DeviceType::HIP;
+  std::vector<unsigned char> fill(n, 0xA5), back(n);
+  bool ok = bool(hip->copy_tensor_set(&t, fill.data(), 0, n));
+  std::vector<unsigned char> want = fill;
+  unsigned char v = 1;
+  for (const auto &[off, len] : std::vector<std::pair<size_t, size_t>>{
+           {3, 1}, {17, 255}, {300, 256}, {700, 257}, {1101, 1000}, {2500, 4}}) {
+    std::vector<unsigned char> src(len);
+    for (auto &b : src) b = v++;
+    ok = ok && bool(hip->copy_tensor_set(&t, src.data(), off, len));
+    std::copy(src.begin(), src.end(), want.begin() + off);
+    std::fill(src.begin(), src.end(), 0);  // the call must not read it later
+  }
+  ok = ok && bool(hip->synchronize()) && bool(hip->copy_tensor_get(&t, back.data(), 0, n));
+  CHECK(ok && back == want, "copy_tensor_set: kernel-argument and memcpy sizes, unaligned offsets");
+  CHECK(!hip->copy_tensor_set(&t, fill.data(), n - 8, 16), "copy_tensor_set past the tensor is rejected");
+  hip->free(BufferKind::ACTIVATION, t.data);
 }
 
 // The prefill rows a layer's projections write straight into the cache (the
