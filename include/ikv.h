@@ -83,10 +83,16 @@ int ikv_append_f32(void *dst_rows, const void *src_rows, size_t n_rows, size_t r
  *            be ordered (same stream); concurrent ones race.
  * The split kernel takes head_dim 128 with n_head/n_head_kv 1, 2, 4 or 8.
  * Any other head_dim in [1, 512] and any n_head that n_head_kv divides run
- * a generic path instead (the append, then one workgroup per query head over
- * the keys; with qk-norm + RoPE folded in, those run first as their own
- * kernels into the workspace, which then holds the rotated q and k rows):
- * same semantics, slower, no replay form. Larger head_dim: -ENOTSUP.
+ * a generic path instead: the append, then two launches, the context split
+ * over workgroups that each serve all query heads of one KV head and a merge
+ * of the splits in order (their partials in the workspace), or, when
+ * n_head/n_head_kv * ceil(head_dim/64) exceeds 32 (dims per lane rounded to
+ * 1, 2, 4, 8) or the workspace is smaller than
+ * ikv_attn_decode_workspace_bytes() asks, one workgroup per query head over
+ * all keys. With qk-norm + RoPE folded in, those run first as their own
+ * kernels into the workspace, which then holds the rotated q and k rows
+ * ahead of the partials. Same semantics within the attention bar, slower,
+ * no replay form. Larger head_dim: -ENOTSUP.
  * ------------------------------------------------------------------- */
 size_t ikv_attn_decode_workspace_bytes(int n_head, int n_head_kv, int head_dim, int64_t n_kv);
 

@@ -1037,9 +1037,14 @@ int shape_status(int n_head, int n_head_kv, int head_dim, int64_t n_kv) {
 
 // The workspace of the generic path (attn_generic.hpp) with qk-norm + RoPE
 // folded in: the new token's rotated q and k rows.
-size_t generic_ws_bytes(int n_head, int n_head_kv, int head_dim) {
+// [rotated q rows][rotated k row][the split partials of the generic decode]
+size_t generic_pro_bytes(int n_head, int n_head_kv, int head_dim) {
   return align256(sizeof(float) * static_cast<size_t>(n_head) * head_dim) +
          align256(sizeof(float) * static_cast<size_t>(n_head_kv) * head_dim);
+}
+size_t generic_ws_bytes(int n_head, int n_head_kv, int head_dim, int64_t n_kv) {
+  return generic_pro_bytes(n_head, n_head_kv, head_dim) +
+         ikv::generic_decode_ws_bytes(n_head, n_head_kv, head_dim, n_kv);
 }
 
 // A decode step on the generic attention path, for head sizes and query
@@ -1057,7 +1062,7 @@ int decode_generic(const float *q, float *k_cache, float *v_cache, const float *
   const size_t row_bytes = sizeof(float) * static_cast<size_t>(n_head_kv) * head_dim;
   if (k_new && pages && row_bytes % 16 != 0) return -ENOTSUP;
   if (pro) {
-    if (!workspace || workspace_bytes < generic_ws_bytes(n_head, n_head_kv, head_dim))
+    if (!workspace || workspace_bytes < generic_pro_bytes(n_head, n_head_kv, head_dim))
       return -EINVAL;
     float *q_rot = static_cast<float *>(workspace);
     float *k_rot = reinterpret_cast<float *>(
@@ -1085,8 +1090,17 @@ int decode_generic(const float *q, float *k_cache, float *v_cache, const float *
     }
     if (rc) return rc;
   }
-  return ikv::attn_generic(q, k_cache, v_cache, pg, out, n_head, n_head_kv, head_dim, 1, n_kv,
-                           n_kv - 1, scale, s);
+  // the split form's partials after the prologue's rows (a smaller or no
+  // workspace runs the one-workgroup-per-head form)
+  const size_t pro_bytes = generic_pro_bytes(n_head, n_head_kv, head_dim);
+  void *split_ws = nullptr;
+  size_t split_bytes = 0;
+  if (workspace && workspace_bytes > pro_bytes) {
+    split_ws = static_cast<char *>(workspace) + pro_bytes;
+    split_bytes = workspace_bytes - pro_bytes;
+  }
+  return ikv::attn_generic_decode(q, k_cache, v_cache, pg, out, n_head, n_head_kv, head_dim, n_kv,
+                                  scale, split_ws, split_bytes, s);
 }
 
 int decode_common(const float *q, float *k_cache, float *v_cache, const float *k_new,
@@ -1145,7 +1159,7 @@ extern "C" size_t ikv_attn_decode_workspace_bytes(int n_head, int n_head_kv, int
                                                   int64_t n_kv) {
   if (const int rc = shape_status(n_head, n_head_kv, head_dim, n_kv))
     return rc == -ENOTSUP && ikv::generic_attn_shape(n_head, n_head_kv, head_dim)
-               ? generic_ws_bytes(n_head, n_head_kv, head_dim)
+               ? generic_ws_bytes(n_head, n_head_kv, head_dim, n_kv)
                : 0;
   const Plan p = plan_for(n_head, n_head_kv, n_kv);
   return ws_layout(n_head, n_head_kv, p.n_splits).total;

@@ -16,6 +16,7 @@
 #include "attn_generic.hpp"
 #include "ikv_common.hpp"
 
+#include <algorithm>
 #include <climits>
 
 namespace {
@@ -102,6 +103,202 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(const float *__restric
   }
 }
 
+// ---------------------------------------------------------------------------
+// One query token (a decode step), split over the context: workgroup
+// (KV head g, split) serves all G query heads of g over keys [t_begin,
+// t_end), so every K and V row is read once. Its 4 wavefronts take keys
+// t_begin + wave, + 4, ...; a key's row is spread over the lanes (dims lane,
+// lane + 64, ...: DL per lane, head_dim <= 64 DL), loaded 4 keys ahead, and
+// each query head's score is a wave sum. Online softmax in base 2 per head;
+// the waves meet in LDS and the split's (max, sum, unnormalised output) per
+// head goes to the workspace; a second launch merges the splits in split
+// order. Registers hold G x DL query and output values per lane: G * DL <=
+// kSplitHeadDims.
+constexpr int kSplitHeadDims = 32;
+constexpr int kSplitWaves = 4;
+// keys per wave in flight: 16 dims' worth of registers per lane for K and V
+constexpr int split_ahead(int dl) { return dl >= 8 ? 2 : 16 / dl; }
+constexpr int kSplitMinKeys = 64;
+constexpr int kSplitTargetWgs = 256;  // one per MI355X compute unit
+
+template <int DL>
+__global__ __launch_bounds__(kSplitWaves * 64) void generic_split_kernel(
+    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
+    float *__restrict__ part_ml, float *__restrict__ part_o, int n_head_kv, int G, int dim,
+    int n_kv, int keys_per_split, int n_splits, float scale_log2, bool paged, ikv::Pages pg) {
+  constexpr int GM = kSplitHeadDims / DL;  // most query heads per KV head
+  constexpr int kSplitAhead = split_ahead(DL);
+  __shared__ float s_m[kSplitWaves][GM], s_l[kSplitWaves][GM];
+  __shared__ float s_o[kSplitWaves][GM][64 * DL];
+  const int g = static_cast<int>(blockIdx.x) % n_head_kv;
+  const int split = static_cast<int>(blockIdx.x) / n_head_kv;
+  const int t_begin = split * keys_per_split;
+  const int t_end = min(n_kv, t_begin + keys_per_split);
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const size_t tok_stride = static_cast<size_t>(n_head_kv) * dim;
+  const size_t head_off = static_cast<size_t>(g) * dim;
+
+  float qv[GM][DL], o[GM][DL], m[GM], l[GM];
+#pragma unroll
+  for (int h = 0; h < GM; ++h) {
+    m[h] = -INFINITY;
+    l[h] = 0.f;
+#pragma unroll
+    for (int t = 0; t < DL; ++t) {
+      const int d = lane + 64 * t;
+      qv[h][t] = (h < G && d < dim)
+                     ? q[(static_cast<size_t>(g) * G + h) * dim + d] * scale_log2
+                     : 0.f;
+      o[h][t] = 0.f;
+    }
+  }
+  for (int j0 = t_begin + wave; j0 < t_end; j0 += kSplitWaves * kSplitAhead) {
+    float kr[kSplitAhead][DL], vr[kSplitAhead][DL];
+#pragma unroll
+    for (int u = 0; u < kSplitAhead; ++u) {
+      const int j = j0 + kSplitWaves * u;
+      const bool ok = j < t_end;
+      const int64_t row = key_row(pg, paged, ok ? j : t_begin);
+      const float *kp = k + row * tok_stride + head_off;
+      const float *vp = v + row * tok_stride + head_off;
+#pragma unroll
+      for (int t = 0; t < DL; ++t) {
+        const int d = lane + 64 * t;
+        kr[u][t] = (ok && d < dim) ? kp[d] : 0.f;
+        vr[u][t] = (ok && d < dim) ? vp[d] : 0.f;
+      }
+    }
+    // per query head: the chunk's scores (independent wave sums), then one
+    // online-softmax step over them (the chunk's first key is always valid)
+#pragma unroll
+    for (int h = 0; h < GM; ++h) {
+      if (h < G) {  // (guards, not breaks: the register arrays stay unrolled)
+        float sc[kSplitAhead];
+#pragma unroll
+        for (int u = 0; u < kSplitAhead; ++u) {
+          float part = 0.f;
+#pragma unroll
+          for (int t = 0; t < DL; ++t) part = fmaf(qv[h][t], kr[u][t], part);
+          const float w = ikv::wave_sum(part);
+          sc[u] = (j0 + kSplitWaves * u < t_end) ? w : -INFINITY;
+        }
+        float mx = m[h];
+#pragma unroll
+        for (int u = 0; u < kSplitAhead; ++u) mx = fmaxf(mx, sc[u]);
+        const float alpha = ikv::fast_exp2(m[h] - mx);  // 0 on the first chunk
+        float psum = 0.f;
+#pragma unroll
+        for (int t = 0; t < DL; ++t) o[h][t] *= alpha;
+#pragma unroll
+        for (int u = 0; u < kSplitAhead; ++u) {
+          const float pu = ikv::fast_exp2(sc[u] - mx);  // 0 for a key past the split
+          psum += pu;
+#pragma unroll
+          for (int t = 0; t < DL; ++t) o[h][t] = fmaf(pu, vr[u][t], o[h][t]);
+        }
+        l[h] = fmaf(l[h], alpha, psum);
+        m[h] = mx;
+      }
+    }
+  }
+  // the waves meet in LDS (a wave with no key holds m = -inf, l = 0, o = 0)
+#pragma unroll
+  for (int h = 0; h < GM; ++h) {
+    if (h < G) {
+      if (lane == 0) {
+        s_m[wave][h] = m[h];
+        s_l[wave][h] = l[h];
+      }
+#pragma unroll
+      for (int t = 0; t < DL; ++t) s_o[wave][h][lane + 64 * t] = o[h][t];
+    }
+  }
+  __syncthreads();
+  const size_t rec0 = static_cast<size_t>(g) * G * n_splits + split;  // record of head 0
+  for (int idx = threadIdx.x; idx < G * dim; idx += kSplitWaves * 64) {
+    const int h = idx / dim, d = idx - h * dim;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kSplitWaves; ++w) M = fmaxf(M, s_m[w][h]);
+    float L = 0.f, O = 0.f;
+#pragma unroll
+    for (int w = 0; w < kSplitWaves; ++w) {
+      const float mw = s_m[w][h];
+      const float e = (mw == -INFINITY) ? 0.f : ikv::fast_exp2(mw - M);
+      L = fmaf(e, s_l[w][h], L);
+      O = fmaf(e, s_o[w][h][d], O);
+    }
+    const size_t rec = rec0 + static_cast<size_t>(h) * n_splits;
+    part_o[rec * dim + d] = O;
+    if (d == 0) {
+      part_ml[2 * rec] = M;
+      part_ml[2 * rec + 1] = L;
+    }
+  }
+}
+
+// out[head][d] = sum_s e_s O_s[d] / sum_s e_s L_s, e_s = 2^(M_s - max_s M_s):
+// one workgroup per query head. Wave 0 forms the weights (lanes over splits)
+// and the sum; then every thread takes output dims and adds the splits'
+// parts in split order.
+constexpr int kMergeThreads = 256;
+__global__ __launch_bounds__(kMergeThreads) void generic_merge_kernel(
+    const float *__restrict__ part_ml, const float *__restrict__ part_o, float *__restrict__ out,
+    int dim, int n_splits) {
+  __shared__ float s_e[kSplitTargetWgs];
+  __shared__ float s_L;
+  const int head = blockIdx.x;
+  const size_t rec0 = static_cast<size_t>(head) * n_splits;
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    float M = -INFINITY;
+    for (int sp = lane; sp < n_splits; sp += 64) M = fmaxf(M, part_ml[2 * (rec0 + sp)]);
+    M = ikv::wave_max(M);
+    float L = 0.f;
+    for (int sp = lane; sp < n_splits; sp += 64) {
+      const float ms = part_ml[2 * (rec0 + sp)];
+      const float e = ms == -INFINITY ? 0.f : ikv::fast_exp2(ms - M);
+      s_e[sp] = e;
+      L = fmaf(e, part_ml[2 * (rec0 + sp) + 1], L);
+    }
+    L = ikv::wave_sum(L);
+    if (lane == 0) s_L = L;
+  }
+  __syncthreads();
+  const float inv = 1.0f / s_L;
+  for (int d = threadIdx.x; d < dim; d += kMergeThreads) {
+    float O = 0.f;
+#pragma unroll 8
+    for (int sp = 0; sp < n_splits; ++sp) O = fmaf(s_e[sp], part_o[(rec0 + sp) * dim + d], O);
+    out[static_cast<size_t>(head) * dim + d] = O * inv;
+  }
+}
+
+struct SplitPlan {
+  int dl = 0;  // dims per lane; 0: the shape does not fit the split kernel
+  int n_splits = 0, keys_per_split = 0;
+};
+
+SplitPlan split_plan(int n_head, int n_head_kv, int head_dim, int64_t n_kv) {
+  SplitPlan p;
+  const int G = n_head / n_head_kv;
+  const int dl = head_dim <= 64 ? 1 : head_dim <= 128 ? 2 : head_dim <= 256 ? 4 : 8;
+  if (G * dl > kSplitHeadDims || n_kv < 1 || n_kv > INT_MAX / 2) return p;
+  const int64_t target = std::max<int64_t>(1, (kSplitTargetWgs + n_head_kv - 1) / n_head_kv);
+  int64_t per = (n_kv + target - 1) / target;
+  if (per < kSplitMinKeys) per = kSplitMinKeys;
+  p.dl = dl;
+  p.keys_per_split = static_cast<int>(per);
+  p.n_splits = static_cast<int>((n_kv + per - 1) / per);
+  return p;
+}
+
+size_t split_ws_bytes(int n_head, int head_dim, int n_splits) {
+  const size_t ml = (sizeof(float) * 2 * static_cast<size_t>(n_head) * n_splits + 255) & ~size_t(255);
+  return ml + sizeof(float) * static_cast<size_t>(n_head) * n_splits * head_dim;
+}
+
 }  // namespace
 
 namespace ikv {
@@ -122,6 +319,51 @@ int attn_generic(const float *q, const float *k, const float *v, const Pages *pa
   attn_generic_kernel<<<static_cast<unsigned>(n_q * n_head), 64, 0, s>>>(
       q, k, v, out, n_head, n_head_kv, head_dim, static_cast<int>(n_kv),
       static_cast<int>(n_past), scale, pages != nullptr, pages ? *pages : Pages{});
+  return launch_status();
+}
+
+}  // namespace ikv
+
+namespace ikv {
+
+size_t generic_decode_ws_bytes(int n_head, int n_head_kv, int head_dim, int64_t n_kv) {
+  if (!generic_attn_shape(n_head, n_head_kv, head_dim)) return 0;
+  const SplitPlan p = split_plan(n_head, n_head_kv, head_dim, n_kv);
+  return p.dl ? split_ws_bytes(n_head, head_dim, p.n_splits) : 0;
+}
+
+int attn_generic_decode(const float *q, const float *k, const float *v, const Pages *pages,
+                        float *out, int n_head, int n_head_kv, int head_dim, int64_t n_kv,
+                        float scale, void *workspace, size_t workspace_bytes, hipStream_t s) {
+  if (!generic_attn_shape(n_head, n_head_kv, head_dim)) return -ENOTSUP;
+  if (n_kv <= 0) return -EINVAL;
+  const SplitPlan p = split_plan(n_head, n_head_kv, head_dim, n_kv);
+  if (!p.dl || !workspace || !aligned16(workspace) ||
+      workspace_bytes < split_ws_bytes(n_head, head_dim, p.n_splits))
+    return attn_generic(q, k, v, pages, out, n_head, n_head_kv, head_dim, 1, n_kv, n_kv - 1,
+                        scale, s);
+  if (!(scale > 0.0f)) scale = 1.0f / sqrtf(static_cast<float>(head_dim));
+  float *part_ml = static_cast<float *>(workspace);
+  float *part_o = reinterpret_cast<float *>(
+      static_cast<char *>(workspace) +
+      ((sizeof(float) * 2 * static_cast<size_t>(n_head) * p.n_splits + 255) & ~size_t(255)));
+  const unsigned grid = static_cast<unsigned>(n_head_kv) * static_cast<unsigned>(p.n_splits);
+  const int G = n_head / n_head_kv;
+  const float sl2 = scale * kLog2e;
+  const Pages pg = pages ? *pages : Pages{};
+#define IKV_GENERIC_SPLIT(DD)                                                                \
+  generic_split_kernel<DD><<<grid, kSplitWaves * 64, 0, s>>>(                                \
+      q, k, v, part_ml, part_o, n_head_kv, G, head_dim, static_cast<int>(n_kv),              \
+      p.keys_per_split, p.n_splits, sl2, pages != nullptr, pg)
+  switch (p.dl) {
+    case 1: IKV_GENERIC_SPLIT(1); break;
+    case 2: IKV_GENERIC_SPLIT(2); break;
+    case 4: IKV_GENERIC_SPLIT(4); break;
+    default: IKV_GENERIC_SPLIT(8); break;
+  }
+#undef IKV_GENERIC_SPLIT
+  generic_merge_kernel<<<static_cast<unsigned>(n_head), kMergeThreads, 0, s>>>(
+      part_ml, part_o, out, head_dim, p.n_splits);
   return launch_status();
 }
 

@@ -25,4 +25,17 @@ int attn_generic(const float *q, const float *k, const float *v, const Pages *pa
                  int n_head, int n_head_kv, int head_dim, int64_t n_q, int64_t n_kv,
                  int64_t n_past, float scale, hipStream_t s);
 
+// One query token (a decode step) over keys [0, n_kv): the same result as
+// attn_generic with n_q = 1 and n_past = n_kv - 1 (within the path's float
+// tolerance, not bitwise: the context is split over workgroups, each serving
+// every query head of its KV head, and the splits are merged in order by a
+// second launch). The split form needs workspace_bytes >=
+// generic_decode_ws_bytes(...) of 16-byte aligned device memory and
+// n_head / n_head_kv * ceil(head_dim / 64) <= 32 (rounded to 1, 2, 4, 8
+// dims per lane); otherwise (or with no workspace) attn_generic runs.
+size_t generic_decode_ws_bytes(int n_head, int n_head_kv, int head_dim, int64_t n_kv);
+int attn_generic_decode(const float *q, const float *k, const float *v, const Pages *pages,
+                        float *out, int n_head, int n_head_kv, int head_dim, int64_t n_kv,
+                        float scale, void *workspace, size_t workspace_bytes, hipStream_t s);
+
 }  // namespace ikv

@@ -107,9 +107,22 @@ def test_decode_rejects_bad_arguments_without_launching():
     assert call(head_dim=1024) == -errno.ENOTSUP       # past the generic path's 512
     assert call(n_head=24, head_dim=640) == -errno.ENOTSUP
     # other head sizes and groups take the generic path: its workspace holds
-    # the rotated q and k rows of the fused prologue
-    assert ikv.decode_workspace_bytes(24, 8, 64, 100) == 24 * 64 * 4 + 8 * 64 * 4
-    assert ikv.decode_workspace_bytes(12, 4, 96, 5000) == 12 * 96 * 4 + 4 * 96 * 4 + 0
+    # the rotated q and k rows of the fused prologue (each 256-byte aligned),
+    # then the split partials: (max, sum) records, 256-byte aligned, and
+    # head_dim floats per query head and split. Splits: at least 64 keys
+    # each, at most ceil(256 / n_head_kv).
+    def a256(b):
+        return (b + 255) // 256 * 256
+
+    def generic(n_head, n_head_kv, d, n_splits):
+        pro = a256(n_head * d * 4) + a256(n_head_kv * d * 4)
+        return pro + a256(2 * n_head * n_splits * 4) + n_head * n_splits * d * 4
+
+    assert ikv.decode_workspace_bytes(24, 8, 64, 100) == generic(24, 8, 64, 2)
+    assert ikv.decode_workspace_bytes(12, 4, 96, 5000) == generic(12, 4, 96, 64)
+    assert ikv.decode_workspace_bytes(12, 4, 96, 64) == generic(12, 4, 96, 1)
+    # G * ceil(head_dim / 64) > 32 (dims per lane 1, 2, 4, 8): no split form
+    assert ikv.decode_workspace_bytes(12, 2, 300, 5000) == a256(12 * 300 * 4) + a256(2 * 300 * 4)
     assert call(q=P + 4) == -errno.EINVAL              # misaligned
     assert call(n_kv=4097) == -errno.EINVAL            # split-K needs a workspace
     need = ikv.decode_workspace_bytes(ok["n_head"], ok["n_head_kv"], 128, 4097)
@@ -259,7 +272,11 @@ def test_workspace_bytes_grow_with_context_and_are_bounded():
     assert all(s > 0 for s in sizes)
     assert sizes == sorted(sizes)
     assert sizes[-1] <= 16 * 1024 * (128 + 2) * 4 + 4096  # at most 1024 splits per head
-    assert ikv.decode_workspace_bytes(16, 8, 64, 100) == (16 + 8) * 64 * 4  # generic path
+    # the generic path: prologue rows, then two splits' partials at 100 keys
+    assert ikv.decode_workspace_bytes(16, 8, 64, 100) == (16 + 8) * 64 * 4 + 256 + 16 * 2 * 64 * 4
+    # and its workspace too grows with the context and stops at 256 / n_head_kv splits
+    gen = [ikv.decode_workspace_bytes(16, 8, 64, n) for n in (1, 100, 4097, 10**6)]
+    assert gen == sorted(gen) and gen[-1] == gen[-2] == (16 + 8) * 64 * 4 + 2 * 16 * 32 * 4 + 16 * 32 * 64 * 4
     assert ikv.decode_workspace_bytes(16, 8, 1024, 100) == 0
 
 

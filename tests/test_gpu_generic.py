@@ -77,7 +77,14 @@ def test_generic_paged_prefill_equals_contiguous(dev, D, Hq, Hkv, bt):
 
 
 @pytest.mark.parametrize("D,Hq,Hkv,n_kv", [(64, 12, 4, 1), (64, 12, 4, 200), (96, 6, 1, 129),
-                                           (256, 8, 8, 70)])
+                                           (256, 8, 8, 70),
+                                           # longer contexts: the split-K form
+                                           # (several splits, a short last one)
+                                           (64, 12, 4, 3001), (80, 10, 5, 2500),
+                                           (256, 16, 2, 1500), (8, 3, 3, 777),
+                                           # G * ceil(D / 64) > 32: the
+                                           # one-workgroup-per-head form
+                                           (300, 12, 2, 700), (64, 64, 1, 300)])
 def test_generic_decode_append_matches_oracle(dev, oracle_pool, D, Hq, Hkv, n_kv):
     seed = 5200 + D + n_kv
     cap = n_kv + 3
@@ -95,6 +102,56 @@ def test_generic_decode_append_matches_oracle(dev, oracle_pool, D, Hq, Hkv, n_kv
     # the appended rows bitwise, nothing else written
     assert np.array_equal(host(kd).view(np.uint32), k_ref.view(np.uint32))
     assert np.array_equal(host(vd).view(np.uint32), v_ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("D,Hq,Hkv,n_kv,bt", [(64, 12, 4, 3001, 64), (96, 6, 2, 1000, 128)])
+def test_generic_paged_decode_equals_contiguous(dev, D, Hq, Hkv, n_kv, bt):
+    """The split-K generic decode over a shuffled paged pool: bitwise the
+    contiguous launch (same splits, same order), appended rows included."""
+    import torch
+    seed = 5400 + D
+    n_blocks = -(-n_kv // bt)
+    k = synth.normal(seed, (n_kv, Hkv, D))
+    v = synth.normal(seed + 1, (n_kv, Hkv, D))
+    q = dev_t(synth.normal(seed + 2, (Hq, D)), dev)
+    kn = dev_t(synth.normal(seed + 3, (Hkv, D)), dev)
+    vn = dev_t(synth.normal(seed + 4, (Hkv, D)), dev)
+    order = np.random.default_rng(seed).permutation(n_blocks + 3)[:n_blocks].astype(np.int32)
+    pools = []
+    for a in (k, v):
+        pool = np.zeros(((n_blocks + 3) * bt, Hkv, D), np.float32)
+        for b, blk in enumerate(order):
+            rows = a[b * bt:(b + 1) * bt]
+            pool[blk * bt:blk * bt + len(rows)] = rows
+        pools.append(dev_t(pool, dev))
+    table = torch.tensor(order, device=dev)
+    kd, vd = dev_t(k, dev), dev_t(v, dev)
+    flat = host(ikv.attn_decode(q, kd, vd, n_kv, k_new=kn, v_new=vn))
+    paged = host(ikv.attn_decode_paged(q, pools[0], pools[1], table, bt, n_kv, k_new=kn,
+                                       v_new=vn))
+    assert np.array_equal(flat.view(np.uint32), paged.view(np.uint32))
+    last = n_kv - 1
+    blk = order[last // bt]
+    row = blk * bt + last % bt
+    assert np.array_equal(host(pools[0])[row].view(np.uint32), host(kd)[last].view(np.uint32))
+    assert np.array_equal(host(pools[1])[row].view(np.uint32), host(vd)[last].view(np.uint32))
+
+
+def test_generic_decode_without_workspace_room_takes_the_per_head_form(dev, oracle_pool):
+    """A workspace too small for the split partials runs the one-workgroup-per-
+    head kernel: the same result within the bar."""
+    import torch
+    D, Hq, Hkv, n_kv = 64, 12, 4, 2000
+    seed = 5500
+    kc = synth.normal(seed, (n_kv, Hkv, D))
+    vc = synth.normal(seed + 1, (n_kv, Hkv, D))
+    q = synth.normal(seed + 2, (Hq, D))
+    small = torch.zeros(1024, dtype=torch.float32, device=dev)  # prologue room only
+    got = host(ikv.attn_decode(dev_t(q, dev), dev_t(kc, dev), dev_t(vc, dev), n_kv,
+                               workspace=small))
+    ref = oracle.decode_append_attn(q, kc[n_kv - 1], vc[n_kv - 1], kc.copy(), vc.copy(),
+                                    n_kv - 1).astype(np.float64)
+    assert close(got, ref)
 
 
 def test_generic_decode_rope_equals_separate_ops(dev, oracle_pool):
