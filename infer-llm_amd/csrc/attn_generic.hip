@@ -6,13 +6,21 @@
 // key j is visible to query t iff j <= n_past + t and j < n_kv; q head h
 // reads KV head h / (n_head / n_head_kv).
 //
-// One 64-lane workgroup per (query token, query head): the query row is
-// staged in LDS; keys go 64 at a time, one per lane, each lane forming its
-// key's score in a sequential loop over the row; the wave's online softmax
-// (running max and sum, natural exp) rescales the output, whose dims lane,
-// lane + 64, ... each lane owns, and every key's weight then multiplies its V
-// row. It is simple rather than fast: a correct path for models whose heads
-// the MFMA kernels were not built for.
+// Prompts (and any n_q): a workgroup of 4 wavefronts owns 16 query rows of
+// one KV head g (row r = token * G + query head in the group, so a block of
+// rows covers every query head of its tokens and each K / V tile serves all
+// of them). Key tiles of KT rows (64 keys for head_dim <= 128, fewer for
+// wider heads so a tile stays about 34 KB) are staged in LDS (16-byte loads
+// when rows are 16-byte aligned) with rows padded by 4 floats (16-byte reads
+// from 16 rows hit distinct banks). A wave
+// holds 4 rows: for the scores each lane takes a key (and, with KT < 64, a
+// part of its dims, the parts summed by lane swaps) and forms its dot with
+// the 4 query rows, broadcast from LDS; online softmax in base 2 per row
+// over the wave; the weights go through LDS and every lane then adds the
+// tile's V rows for its output dims (lane, lane + 64, ...), once per key for
+// all 4 rows.
+//
+// One query token (a decode step): the split form below.
 #include "attn_generic.hpp"
 #include "ikv_common.hpp"
 
@@ -20,9 +28,6 @@
 #include <climits>
 
 namespace {
-
-constexpr int kMaxDim = ikv::kGenericMaxDim;
-constexpr int kOut = kMaxDim / 64;  // output dims per lane
 
 // Pool row of logical key j (per lane): table[j / bt] * bt + j % bt; an entry
 // outside the pool reads block 0 and raises IKV_STATUS_BLOCK.
@@ -37,69 +42,178 @@ __device__ __forceinline__ int64_t key_row(const ikv::Pages &pg, bool paged, int
   return static_cast<int64_t>(blk) * pg.bt + (j - b * pg.bt);
 }
 
-__global__ __launch_bounds__(64) void attn_generic_kernel(const float *__restrict__ q,
-                                                          const float *__restrict__ k,
-                                                          const float *__restrict__ v,
-                                                          float *__restrict__ out, int n_head,
-                                                          int n_head_kv, int dim, int n_kv,
-                                                          int n_past, float scale, bool paged,
-                                                          ikv::Pages pg) {
-  __shared__ float s_q[kMaxDim];
-  __shared__ float s_p[64];
-  __shared__ int64_t s_row[64];
-  const int t = static_cast<int>(blockIdx.x) / n_head;
-  const int h = static_cast<int>(blockIdx.x) - t * n_head;
-  const int g = h / (n_head / n_head_kv);
-  const int lane = threadIdx.x;
-  const float *qr = q + (static_cast<size_t>(t) * n_head + h) * dim;
-  for (int d = lane; d < dim; d += 64) s_q[d] = qr[d];
-  __syncthreads();
+constexpr int kTileRowsPerWave = 4;  // 8 measured slower (fewer workgroups, more registers)
+constexpr int kTileRows = 4 * kTileRowsPerWave;  // query rows per workgroup
 
+template <int DL>  // dims per lane: head_dim <= 64 * DL
+__global__ __launch_bounds__(256) void generic_tile_kernel(
+    const float *__restrict__ q, const float *__restrict__ k, const float *__restrict__ v,
+    float *__restrict__ out, int n_head, int n_head_kv, int dim, int n_q, int n_kv, int n_past,
+    float scale_log2, bool paged, ikv::Pages pg, bool vec4) {
+  constexpr int KT = DL <= 2 ? 64 : 128 / DL;  // keys per tile: 64, 64, 32, 16
+  constexpr int LPK = 64 / KT;                 // lanes per key in the score phase
+  constexpr int DA = 64 * DL;                  // dims held (zeros past head_dim)
+  constexpr int DP = DA + 4;                   // padded LDS row
+  constexpr int DPART = DA / LPK;              // dims of a lane's score part
+  constexpr int RW = kTileRowsPerWave;
+  __shared__ __attribute__((aligned(16))) float s_k[KT * DP];
+  __shared__ __attribute__((aligned(16))) float s_v[KT * DP];
+  __shared__ __attribute__((aligned(16))) float s_q[kTileRows * DP];
+  __shared__ __attribute__((aligned(16))) float s_p[4][RW][KT];
+  const int G = n_head / n_head_kv;
+  const int g = static_cast<int>(blockIdx.x) % n_head_kv;
+  const int blk = static_cast<int>(blockIdx.x) / n_head_kv;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n_rows = n_q * G;
+  const int r0 = blk * kTileRows;
   const size_t tok_stride = static_cast<size_t>(n_head_kv) * dim;
   const size_t head_off = static_cast<size_t>(g) * dim;
-  const int kv_end = min(n_kv, n_past + t + 1);
-  float o[kOut];
-#pragma unroll
-  for (int i = 0; i < kOut; ++i) o[i] = 0.f;
-  float m = -INFINITY, l = 0.f;
-  for (int base = 0; base < kv_end; base += 64) {
-    const int j = base + lane;
-    const bool valid = j < kv_end;
-    const int64_t row = key_row(pg, paged, valid ? j : base);
-    float sc = -INFINITY;
-    if (valid) {
-      const float *kr = k + row * tok_stride + head_off;
-      float acc = 0.f;
-      for (int d = 0; d < dim; ++d) acc = fmaf(s_q[d], kr[d], acc);
-      sc = acc * scale;
+
+  // the block's query rows, pre-scaled, zero past head_dim and past the rows
+  for (int i = tid; i < kTileRows * DA; i += 256) {
+    const int rr = i / DA, d = i - rr * DA;
+    const int r = r0 + rr;
+    float x = 0.f;
+    if (r < n_rows && d < dim) {
+      const int t = r / G, hh = r - t * G;
+      x = q[(static_cast<size_t>(t) * n_head + g * G + hh) * dim + d] * scale_log2;
     }
-    const float m_new = fmaxf(m, ikv::wave_max(sc));  // finite: lane 0's key is valid
-    const float alpha = expf(m - m_new);              // 0 on the first chunk (m = -inf)
-    const float p = valid ? expf(sc - m_new) : 0.f;
-    l = l * alpha + ikv::wave_sum(p);
+    s_q[rr * DP + d] = x;
+  }
+  const int r_last = min(r0 + kTileRows, n_rows) - 1;
+  const int kv_end = min(n_kv, n_past + r_last / G + 1);  // keys any row of the block sees
+
+  int tok[RW];
+  bool rok[RW];
+  float m[RW], l[RW], o[RW][DL];
 #pragma unroll
-    for (int i = 0; i < kOut; ++i) o[i] *= alpha;
-    s_p[lane] = p;
-    s_row[lane] = row;
-    __syncthreads();
-    const int n = min(64, kv_end - base);
-    for (int jj = 0; jj < n; ++jj) {
-      const float pj = s_p[jj];
-      const float *vr = v + s_row[jj] * tok_stride + head_off;
+  for (int i = 0; i < RW; ++i) {
+    const int r = r0 + wave * RW + i;
+    rok[i] = r < n_rows;
+    tok[i] = rok[i] ? r / G : 0;
+    m[i] = -INFINITY;
+    l[i] = 0.f;
 #pragma unroll
-      for (int i = 0; i < kOut; ++i) {
-        const int d = lane + 64 * i;
-        if (d < dim) o[i] = fmaf(pj, vr[d], o[i]);
+    for (int t = 0; t < DL; ++t) o[i][t] = 0.f;
+  }
+  const int jl = lane % KT;    // this lane's key in the score phase
+  const int part = lane / KT;  // and its part of the dims
+  for (int kb = 0; kb < kv_end; kb += KT) {
+    __syncthreads();  // the previous tile's readers are done (and q is staged)
+    if (vec4) {
+      // 16-byte pieces: thread tid takes piece c = tid + 256 i of the tile
+      constexpr int P4 = DA / 4;  // pieces per padded row
+#pragma unroll
+      for (int i = 0; i < KT * P4 / 256; ++i) {
+        const int c = tid + 256 * i;
+        const int jj = c / P4, d = 4 * (c - jj * P4);
+        const int j = kb + jj;
+        float4 kx = make_float4(0.f, 0.f, 0.f, 0.f), vx = kx;
+        if (j < kv_end && d < dim) {
+          const int64_t row = key_row(pg, paged, j);
+          kx = *reinterpret_cast<const float4 *>(k + row * tok_stride + head_off + d);
+          vx = *reinterpret_cast<const float4 *>(v + row * tok_stride + head_off + d);
+        }
+        *reinterpret_cast<float4 *>(s_k + jj * DP + d) = kx;
+        *reinterpret_cast<float4 *>(s_v + jj * DP + d) = vx;
+      }
+    } else {
+      for (int i = tid; i < KT * DA; i += 256) {
+        const int jj = i / DA, d = i - jj * DA;
+        const int j = kb + jj;
+        float kx = 0.f, vx = 0.f;
+        if (j < kv_end && d < dim) {
+          const int64_t row = key_row(pg, paged, j);
+          kx = k[row * tok_stride + head_off + d];
+          vx = v[row * tok_stride + head_off + d];
+        }
+        s_k[jj * DP + d] = kx;
+        s_v[jj * DP + d] = vx;
       }
     }
     __syncthreads();
-    m = m_new;
-  }
-  float *orow = out + (static_cast<size_t>(t) * n_head + h) * dim;
+    // scores of key kb + jl with the wave's 4 rows, over this lane's part
+    float sc[RW];
 #pragma unroll
-  for (int i = 0; i < kOut; ++i) {
-    const int d = lane + 64 * i;
-    if (d < dim) orow[d] = o[i] / l;
+    for (int i = 0; i < RW; ++i) sc[i] = 0.f;
+    const float *kp = s_k + jl * DP + part * DPART;
+    const float *qp = s_q + (wave * RW) * DP + part * DPART;
+#pragma unroll 4
+    for (int d4 = 0; d4 < DPART; d4 += 4) {
+      const float4 kx = *reinterpret_cast<const float4 *>(kp + d4);
+#pragma unroll
+      for (int i = 0; i < RW; ++i) {
+        const float4 qx = *reinterpret_cast<const float4 *>(qp + i * DP + d4);
+        sc[i] = fmaf(qx.x, kx.x, sc[i]);
+        sc[i] = fmaf(qx.y, kx.y, sc[i]);
+        sc[i] = fmaf(qx.z, kx.z, sc[i]);
+        sc[i] = fmaf(qx.w, kx.w, sc[i]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < RW; ++i) {
+      if constexpr (LPK >= 2) {  // parts at lanes l, l ^ 32 (and l ^ 16)
+        auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(sc[i]), __float_as_uint(sc[i]),
+                                                  false, false);
+        sc[i] = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+      }
+      if constexpr (LPK >= 4) {
+        auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(sc[i]), __float_as_uint(sc[i]),
+                                                  false, false);
+        sc[i] = __uint_as_float(b[0]) + __uint_as_float(b[1]);
+      }
+    }
+    const int j = kb + jl;
+    float alpha[RW];
+#pragma unroll
+    for (int i = 0; i < RW; ++i) {
+      const bool vis = rok[i] && j < kv_end && j <= n_past + tok[i];
+      const float s = vis ? sc[i] : -INFINITY;
+      const float m_new = fmaxf(m[i], ikv::wave_max(s));
+      // a row that has seen no key yet keeps a zero state (reference 0)
+      const float ref = (m_new == -INFINITY) ? 0.f : m_new;
+      alpha[i] = ikv::fast_exp2(m[i] - ref);
+      const float p = ikv::fast_exp2(s - ref);
+      l[i] = fmaf(l[i], alpha[i], ikv::wave_sum(part == 0 ? p : 0.f));
+      if (part == 0) s_p[wave][i][jl] = p;
+      m[i] = m_new;
+    }
+    // the wave's weights are in LDS (its own writes, in order): add V
+#pragma unroll
+    for (int i = 0; i < RW; ++i)
+#pragma unroll
+      for (int t = 0; t < DL; ++t) o[i][t] *= alpha[i];
+    for (int j4 = 0; j4 < KT; j4 += 4) {  // 4 keys: the rows' weights as one 16-byte read
+      float vd[4][DL];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int t = 0; t < DL; ++t) vd[u][t] = s_v[(j4 + u) * DP + lane + 64 * t];
+#pragma unroll
+      for (int i = 0; i < RW; ++i) {
+        const float4 pj = *reinterpret_cast<const float4 *>(&s_p[wave][i][j4]);
+#pragma unroll
+        for (int t = 0; t < DL; ++t) {
+          o[i][t] = fmaf(pj.x, vd[0][t], o[i][t]);
+          o[i][t] = fmaf(pj.y, vd[1][t], o[i][t]);
+          o[i][t] = fmaf(pj.z, vd[2][t], o[i][t]);
+          o[i][t] = fmaf(pj.w, vd[3][t], o[i][t]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < RW; ++i) {
+    if (!rok[i]) continue;
+    const int r = r0 + wave * RW + i;
+    const int hh = r - tok[i] * G;
+    float *orow = out + (static_cast<size_t>(tok[i]) * n_head + g * G + hh) * dim;
+    const float inv = 1.0f / l[i];
+#pragma unroll
+    for (int t = 0; t < DL; ++t) {
+      const int d = lane + 64 * t;
+      if (d < dim) orow[d] = o[i][t] * inv;
+    }
   }
 }
 
@@ -316,9 +430,28 @@ int attn_generic(const float *q, const float *k, const float *v, const Pages *pa
   if (n_q < 0 || n_kv <= 0 || n_past < 0) return -EINVAL;
   if (n_q > INT_MAX / n_head || n_kv > INT_MAX / 2 || n_past > INT_MAX / 2) return -EOVERFLOW;
   if (!(scale > 0.0f)) scale = 1.0f / sqrtf(static_cast<float>(head_dim));
-  attn_generic_kernel<<<static_cast<unsigned>(n_q * n_head), 64, 0, s>>>(
-      q, k, v, out, n_head, n_head_kv, head_dim, static_cast<int>(n_kv),
-      static_cast<int>(n_past), scale, pages != nullptr, pages ? *pages : Pages{});
+  const int dl = head_dim <= 64 ? 1 : head_dim <= 128 ? 2 : head_dim <= 256 ? 4 : 8;
+  const int64_t rows = n_q * (n_head / n_head_kv);
+  const int64_t blocks = (rows + kTileRows - 1) / kTileRows;
+  if (blocks * n_head_kv > INT_MAX) return -EOVERFLOW;
+  const unsigned grid = static_cast<unsigned>(blocks * n_head_kv);
+  const float sl2 = scale * kLog2e;
+  const Pages pgv = pages ? *pages : Pages{};
+  // K and V rows staged 16 bytes at a time when every row starts 16-byte
+  // aligned
+  const bool vec4 = head_dim % 4 == 0 && aligned16(k) && aligned16(v);
+#define IKV_GENERIC_TILE(DD)                                                                  \
+  generic_tile_kernel<DD><<<grid, 256, 0, s>>>(q, k, v, out, n_head, n_head_kv, head_dim,     \
+                                               static_cast<int>(n_q), static_cast<int>(n_kv), \
+                                               static_cast<int>(n_past), sl2, pages != nullptr, pgv, \
+                                               vec4)
+  switch (dl) {
+    case 1: IKV_GENERIC_TILE(1); break;
+    case 2: IKV_GENERIC_TILE(2); break;
+    case 4: IKV_GENERIC_TILE(4); break;
+    default: IKV_GENERIC_TILE(8); break;
+  }
+#undef IKV_GENERIC_TILE
   return launch_status();
 }
 
