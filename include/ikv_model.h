@@ -30,7 +30,7 @@ extern "C" {
  * m == 1 (decode) runs a hand-written streaming GEMV. 2 <= m <= 64 with
  * n_out % 16 == 0, k % 1024 == 0 and 16-byte aligned w and x runs a
  * hand-written F32 MFMA kernel. Other m > 1 with n_out % 64 == 0,
- * k % 64 == 0 and 16-byte aligned w and x run the tiled F32 MFMA GEMM of
+ * k % 64 == 0, k < 2^22 and 16-byte aligned w and x run the tiled F32 MFMA GEMM of
  * ikv_gemm_nt_f32, with K split over several workgroups when its tiles
  * would leave compute units idle: such a call needs a split-K workspace of
  * its device and stream, which the first one allocates (8 MiB + 16 KiB,
@@ -46,7 +46,7 @@ int ikv_mul_mat_f32(const float *w, const float *x, float *out, int64_t n_out, i
 
 /* The hand-written F32 MFMA GEMM of mul_mat for prompts (the same product,
  * CPUBackend::compute_mul_mat, src/backends/cpu_backend.cpp:386-424), for
- * any m >= 1: n_out % 64 == 0, k % 64 == 0, 16-byte aligned w and x (else
+ * any m >= 1: n_out % 64 == 0, k % 64 == 0, k < 2^22, 16-byte aligned w and x (else
  * -ENOTSUP / -EINVAL, nothing launched). Deterministic (a fixed summation
  * order per output); never splits K, so it allocates nothing. residual as
  * for mul_mat. */

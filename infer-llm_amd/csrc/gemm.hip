@@ -65,6 +65,7 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 constexpr int BK = 64;      // columns per step: 16 chunks of 16 bytes per row
 constexpr int kChunks = BK / 4;
 constexpr int kXcds = 8;
+constexpr int64_t kMaxK = INT_MAX / (128 * 4);  // columns of a panel addressed in 32 bits
 constexpr int kGroupM = 8;  // tile rows per group of the tile order
 
 // Slot of 16-byte chunk c in staged row r (a row is 256 bytes, the width of
@@ -161,18 +162,34 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_kernel(const float *__re
   // This thread's chunks: chunk q = tid + NT*i is column chunk c = q %
   // kChunks of staged row r = q / kChunks (16 consecutive threads read one
   // row's 256 contiguous bytes), stored at slot chunk_slot(r, c) of row r.
-  const float *src[CPT];
+  // Rows r = tid / 16 + 16 i, so chunks i < CPT_X are x rows and the rest w
+  // rows for every thread. Loads go through a buffer resource over the
+  // tile's x panel and one over its w panel: a fixed 32-bit byte offset per
+  // chunk and the step's column offset as the scalar offset, so the loop
+  // issues no address arithmetic (with 64-bit pointers it added a VALU op
+  // per load and ran ~1.7% slower).
+  constexpr int CPT_X = BM * kChunks / NT;
+  static_assert(BM % (NT / kChunks) == 0, "x and w chunks split at a whole i");
+  const int x_rows = min(BM, m - m0);
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float *>(x + static_cast<size_t>(m0) * k), 0, x_rows * k * 4, ikv::kBufWord3);
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float *>(w + static_cast<size_t>(n0) * k), 0, BN * k * 4, ikv::kBufWord3);
+  unsigned voff[CPT];
   int dst[CPT];
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
     const int q = tid + NT * i;
     const int r = q / kChunks;
     const int c = q % kChunks;
-    const float *rowp = r < BM ? x + static_cast<size_t>(min(m0 + r, m - 1)) * k
-                               : w + static_cast<size_t>(n0 + r - BM) * k;
-    src[i] = rowp + k_lo + 4 * c;
+    const int row = r < BM ? min(r, x_rows - 1) : r - BM;  // within the panel
+    voff[i] = static_cast<unsigned>((row * k + k_lo + 4 * c) * 4);
     dst[i] = r * BK + 4 * chunk_slot(r, c);
   }
+  // chunk i of the step whose columns start at kb
+  auto gload = [&](int i, int kb) -> floatx4 {
+    return __builtin_amdgcn_raw_buffer_load_b128(i < CPT_X ? rx : rw, voff[i], kb * 4, 0);
+  };
   // The chunks of the next two steps, global -> registers -> LDS: at the
   // start of step s, stage[(s + 1) & 1] holds step s + 1 and stage[s & 1]
   // step s + 2 (loads in flight), so a load has two steps to land.
@@ -244,7 +261,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_kernel(const float *__re
 #pragma unroll
       for (int i = lo; i < hi; ++i) {
         *reinterpret_cast<floatx4 *>(nbuf + dst[i]) = stg[i];
-        stg[i] = *reinterpret_cast<const floatx4 *>(src[i] + kb3);
+        stg[i] = gload(i, kb3);
       }
 #pragma unroll
       for (int e = 0; e < 4; ++e)
@@ -269,7 +286,7 @@ __global__ __launch_bounds__(WM * WN * 64) void gemm_nt_kernel(const float *__re
   auto load = [&](floatx4 *stg, int st) {
     const int kb = min(st, n_steps - 1) * BK;
 #pragma unroll
-    for (int i = 0; i < CPT; ++i) stg[i] = *reinterpret_cast<const floatx4 *>(src[i] + kb);
+    for (int i = 0; i < CPT; ++i) stg[i] = gload(i, kb);
   };
   load(stage[0], 0);
 #pragma unroll
@@ -357,6 +374,7 @@ template <int TM, int TN, int WM, int WN>
 int launch(const float *w, const float *x, float *out, const float *residual, int n_out, int k,
            int m, int n_split, float *part, int *counters, hipStream_t s) {
   constexpr int BM = 16 * TM * WM, BN = 16 * TN * WN;
+  static_assert(BM <= 128 && BN <= 128, "kMaxK covers the panels");
   const int tiles_m = (m + BM - 1) / BM;
   const int tiles_n = n_out / BN;
   const int64_t n_tiles = static_cast<int64_t>(tiles_m) * tiles_n;
@@ -452,8 +470,9 @@ int split_workspace(hipStream_t s, float **part, int **counters) {
 namespace ikv {
 
 bool gemm_nt_supported(int64_t n_out, int64_t k, int64_t m) {
+  // k bound: a 128-row panel of k floats is one buffer resource's range
   return m >= 1 && n_out % 64 == 0 && k % BK == 0 && k > 0 && n_out <= INT_MAX / 2 &&
-         k <= INT_MAX / 2 && m <= INT_MAX / 2;
+         k <= kMaxK && m <= INT_MAX / 2;
 }
 
 GemmPlan gemm_plan(int64_t n_out, int64_t k, int64_t m, bool may_split) {
