@@ -219,7 +219,8 @@ int64_t ikv_attn_decode_replay_limit(int n_head, int n_head_kv, int head_dim, in
  * Replaces compute_flash_attn for n_q > 1. Needs no workspace.
  * The MFMA kernel takes head_dim 128 with n_head/n_head_kv 1, 2, 4 or 8;
  * any other head_dim in [1, 512] and any n_head that n_head_kv divides run
- * the generic path (decode above). Larger head_dim: -ENOTSUP.
+ * the generic path (decode above). Larger head_dim: -ENOTSUP. The MFMA
+ * kernel's shapes with n_head_kv > 65536: -EOVERFLOW.
  * ------------------------------------------------------------------- */
 int ikv_attn_prefill_f32(const float *q, const float *k, const float *v, float *out, int n_head,
                          int n_head_kv, int head_dim, int64_t n_q, int64_t n_kv, int64_t n_past,

@@ -29,12 +29,18 @@
 //     come from registers (Q, P) or 16-byte LDS reads (one ds_read_b128 of K
 //     feeds 4 MFMAs); output tile t, register r of lane l holds dim
 //     64*(t/4) + 16*(l/16) + 4r + t%4.
-//   * Tiles move global -> LDS with global_load_lds_dwordx4 (no VGPR
+//   * Tiles move global -> LDS with buffer_load_dwordx4 ... lds (no VGPR
 //     staging) into two LDS buffers: tile t+1 loads while tile t is used.
+//     Each tile's K and V rows are a buffer resource built from scalars (the
+//     tile's first row, or its paged block's) and each lane's byte offsets
+//     are the same for every tile, so issuing a tile costs no vector
+//     address arithmetic (with 64-bit per-lane addresses: P = 4096 520 ->
+//     501 us, P = 2048 ~1-4% faster, outputs bit-identical).
 //     The DMA writes each wave's 64 x 16 bytes contiguously, so K rows are
 //     stored with 16-byte chunk c at slot c ^ (key % 16): the 16 lanes that
 //     read one chunk index from 16 keys then hit 16 different bank groups.
-//     Keys past n_kv are clamped to the last row (finite data, masked out).
+//     Keys past n_kv lie outside the tile's buffer range and read as zeros
+//     (finite data, masked out).
 //   * Softmax runs in base 2 on a per-row reference max that only moves when
 //     a score exceeds it by 2^8 (checked with one wave vote), so most tiles
 //     skip the cross-lane max and the O rescale; row sums stay per lane until
@@ -51,6 +57,7 @@
 //     an LDS arrival counter instead of the workgroup barrier, and the
 //     groups drift apart (P = 2048: 144.4 -> 141.4 us, alternated runs).
 #include "attn_generic.hpp"
+#include "coherent.hpp"
 #include "ikv_common.hpp"
 #include "../../include/ikv.h"
 
@@ -65,6 +72,7 @@ typedef __attribute__((address_space(3))) void *lds_ptr;
 constexpr int D = 128;
 constexpr int BN = 32;              // keys per tile
 constexpr int TILE = BN * D;        // floats of K (or V) per tile
+constexpr int kMaxKvHeads = 1 << 16;  // tile rows addressed with 32-bit offsets
 constexpr float kRescale = 8.0f;    // log2 headroom before the running max is moved
 #ifndef IKV_PREFILL_PAIR_MIN_WGS
 #define IKV_PREFILL_PAIR_MIN_WGS 256  // one workgroup per CU
@@ -76,6 +84,12 @@ constexpr float kRescale = 8.0f;    // log2 headroom before the running max is m
 #define IKV_PREFILL_SPLIT 1  // 8-wave workgroups (two key-split groups) at one block per CU
 #endif
 constexpr int kCUs = 256;  // MI355X compute units
+
+// 16 bytes per lane from a buffer resource at byte offset voff into LDS at
+// dst (the wave's 64 x 16 bytes contiguous from dst)
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, float *dst, unsigned voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)dst, 16, voff, 0, 0, 0);
+}
 
 __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -179,22 +193,37 @@ __global__ __launch_bounds__(NW * 64) void prefill_kernel(const float *__restric
   // A paged cache's block (a multiple of 64 keys) holds every tile whole, so
   // one block offset serves the tile.
   // parts: 1 = K, 2 = V, 3 = both (interleaved)
+  // Per tile, one buffer resource over its K rows and one over its V rows
+  // (this KV head's 512 bytes of each of the tile's keys, the range ending
+  // at the last key inside the cache: keys past n_kv read zeros, which the
+  // mask drops); each lane's byte offsets within a tile are fixed.
+  constexpr int NI = 16 / WPG;
+  unsigned kvo[NI], vvo[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int c = w + WPG * i;
+    const int key = 2 * c + (lane >> 5);
+    const int slot = lane & 31;
+    kvo[i] = static_cast<unsigned>((key * n_head_kv * D + 4 * (slot ^ (key & 15))) * 4);
+    vvo[i] = static_cast<unsigned>((key * n_head_kv * D + 4 * slot) * 4);
+  }
   auto issue = [&](float *kbuf, float *vbuf, int tile, int parts = 3) {
     int64_t shift = 0;
     if constexpr (PAGED) shift = ikv::page_shift(pages, tile * BN);
+    const int rows = min(BN, n_kv - tile * BN);
+    const size_t base = (static_cast<size_t>(tile * BN + shift) * n_head_kv + g) * D;
+    const int bytes = ((rows - 1) * n_head_kv * D + D) * 4;
+    const __amdgpu_buffer_rsrc_t rk =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(k + base), 0, bytes, ikv::kBufWord3);
+    const __amdgpu_buffer_rsrc_t rv =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(v + base), 0, bytes, ikv::kBufWord3);
 #pragma unroll
-    for (int i = 0; i < 16 / WPG; ++i) {
+    for (int i = 0; i < NI; ++i) {
       const int c = w + WPG * i;
-      const int key = 2 * c + (lane >> 5);
-      const int slot = lane & 31;
-      const int kg = min(tile * BN + key, n_kv - 1);
-      const size_t rowoff = (static_cast<size_t>(kg + shift) * n_head_kv + g) * D;
       if (parts & 1)
-        __builtin_amdgcn_global_load_lds(k + rowoff + 4 * (slot ^ (key & 15)),
-                                         (lds_ptr)(kbuf + c * 256), 16, 0, 0);
+        dma16(rk, kbuf + c * 256, kvo[i]);
       if (parts & 2)
-        __builtin_amdgcn_global_load_lds(v + rowoff + 4 * slot, (lds_ptr)(vbuf + c * 256), 16, 0,
-                                         0);
+        dma16(rv, vbuf + c * 256, vvo[i]);
     }
   };
   // s_waitcnt vmcnt(n) (lgkmcnt and expcnt not waited for); with ONE, a
@@ -525,6 +554,8 @@ int prefill_common(const float *q, const float *k, const float *v, const ikv_kv_
                              scale, static_cast<hipStream_t>(stream));
   }
   if (n_q > INT_MAX / 2 || n_kv > INT_MAX / 2 || n_past > INT_MAX / 2) return -EOVERFLOW;
+  // a tile's 32 key rows (n_head_kv x 512 bytes each) are one buffer range
+  if (n_head_kv > kMaxKvHeads) return -EOVERFLOW;
   if (!ikv::aligned16(q) || !ikv::aligned16(k) || !ikv::aligned16(v) || !ikv::aligned16(out))
     return -EINVAL;
   if (!(scale > 0.0f)) scale = 1.0f / sqrtf(static_cast<float>(head_dim));
