@@ -28,6 +28,7 @@
 // wavefront kernel over every token (slow, exact order per output).
 #include <climits>
 
+#include "coherent.hpp"
 #include "gemm.hpp"
 #include "gemv_dev.hpp"
 #include "ikv_common.hpp"
@@ -333,14 +334,22 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_kernel(const float *
   const int kw = k / kSkinnyWaves;  // a multiple of 2 * kSkinnyCols
   const int kb0 = wave * kw;
   const int n_steps = kw / kSkinnyCols;
-  // staging: instruction i reads rows 4i + lane / 16, 16-byte column lane % 16
+  // staging: instruction i reads rows 4i + lane / 16, 16-byte column lane % 16,
+  // through a buffer resource over the 16 w rows and one over the tile's
+  // x rows (rows past m read zeros; their outputs are not stored): a fixed
+  // byte offset per instruction and the step's column offset as the scalar
+  // offset, so the loop issues no address arithmetic
   const int sc = lane & 15;
-  const float *wsrc[4], *xsrc[4];
+  const __amdgpu_buffer_rsrc_t rsw = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float *>(w + static_cast<size_t>(n0) * k), 0, 16 * k * 4, ikv::kBufWord3);
+  const __amdgpu_buffer_rsrc_t rsx = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float *>(x + static_cast<size_t>(m0) * k), 0, min(16, m - m0) * k * 4,
+      ikv::kBufWord3);
+  unsigned voff[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int r = 4 * i + (lane >> 4);
-    wsrc[i] = w + static_cast<size_t>(n0 + r) * k + kb0 + 4 * sc;
-    xsrc[i] = x + static_cast<size_t>(min(m0 + r, m - 1)) * k + kb0 + 4 * sc;  // clamped token
+    voff[i] = static_cast<unsigned>((r * k + kb0 + 4 * sc) * 4);
   }
   float(*tw)[kSkinnyCols] = s_tile[wave][0];
   float(*tx)[kSkinnyCols] = s_tile[wave][1];
@@ -349,20 +358,25 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_kernel(const float *
   auto load_step = [&](floatx4 (&rw)[4], floatx4 (&rx)[4], int step) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      rw[i] = *reinterpret_cast<const floatx4 *>(wsrc[i] + kSkinnyCols * step);
-      rx[i] = *reinterpret_cast<const floatx4 *>(xsrc[i] + kSkinnyCols * step);
+      rw[i] = __builtin_amdgcn_raw_buffer_load_b128(rsw, voff[i], kSkinnyCols * step * 4, 0);
+      rx[i] = __builtin_amdgcn_raw_buffer_load_b128(rsx, voff[i], kSkinnyCols * step * 4, 0);
     }
   };
   // store a register set as the current step, refill it with step `next`
   // (if any), then multiply the step out of LDS
   auto body = [&](floatx4 (&rw)[4], floatx4 (&rx)[4], int next) __attribute__((always_inline)) {
+    // each register set is refilled right after its LDS write, in the
+    // order it was loaded
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 4 * i + (lane >> 4);
       *reinterpret_cast<floatx4 *>(&tw[r][4 * (sc ^ r)]) = rw[i];
+      if (next >= 0)
+        rw[i] = __builtin_amdgcn_raw_buffer_load_b128(rsw, voff[i], kSkinnyCols * next * 4, 0);
       *reinterpret_cast<floatx4 *>(&tx[r][4 * (sc ^ r)]) = rx[i];
+      if (next >= 0)
+        rx[i] = __builtin_amdgcn_raw_buffer_load_b128(rsx, voff[i], kSkinnyCols * next * 4, 0);
     }
-    if (next >= 0) load_step(rw, rx, next);
     __builtin_amdgcn_sched_barrier(0);  // the refill stays ahead of this step's reads and MFMAs
 #pragma unroll
     for (int u = 0; u < 4; ++u) {

@@ -189,6 +189,7 @@ def test_gemm_rejects_bad_arguments_without_launching():
     assert call(m=-1) == -errno.EINVAL
     assert call(m=0) == 0 and call(n_out=0) == 0  # nothing to do
     assert call(m=2**40) == -errno.EOVERFLOW
+    assert call(k=2**22) == -errno.ENOTSUP        # a 128-row panel past 32-bit offsets
 
 
 def decode_ws_bytes(n_head, n_head_kv, n_splits):
@@ -247,6 +248,9 @@ def test_prefill_and_rows_reject_bad_arguments():
     assert _rc("ikv_attn_prefill_f32", P, P, P, P, 16, 8, 128, 0, 10, 0, 0.0, None) == 0  # n_q=0
     assert _rc("ikv_attn_prefill_f32", None, P, P, P, 16, 8, 128, 4, 10, 0, 0.0, None) == -errno.EINVAL
     assert _rc("ikv_attn_prefill_f32", P, P, P, P, 16, 8, 1024, 4, 10, 0, 0.0, None) == -errno.ENOTSUP
+    # the MFMA kernel's tile rows (n_head_kv x 512 bytes) take 32-bit offsets
+    assert _rc("ikv_attn_prefill_f32", P, P, P, P, 1 << 17, 1 << 17, 128, 4, 10, 0, 0.0,
+               None) == -errno.EOVERFLOW
     assert _rc("ikv_rms_norm_f32", None, P, P, 4, 128, 1e-6, None) == -errno.EINVAL
     assert _rc("ikv_rms_norm_f32", P, P, P, 0, 128, 1e-6, None) == 0
     assert _rc("ikv_rope_neox_f32", P, P, P, 2, 8, 127, P, P, 10, None, None) == -errno.EINVAL

@@ -109,6 +109,25 @@ def test_gemm_matches_oracle(dev, oracle_pool, n_out, k, m):
     assert proj_close(host(buf), w, x, ref.astype(np.float64) + r)
 
 
+@pytest.mark.parametrize("n_out,k,m", [(1024, 256, 200), (8192, 128, 2047)])
+def test_gemm_unaligned_output_equals_aligned(dev, n_out, k, m):
+    # an output or residual that is not 16-byte aligned takes the 4-byte
+    # stores of the output tile: the same values, bit for bit
+    import torch
+    w = dev_t(synth.normal(710 + m, (n_out, k), 0.02), dev)
+    x = dev_t(synth.normal(711 + m, (m, k)), dev)
+    r = synth.normal(712 + m, (m, n_out))
+    want = ikv.gemm_nt(w, x)
+    want_r = ikv.gemm_nt(w, x, residual=dev_t(r, dev))
+    buf = torch.empty(m * n_out + 1, device=dev)
+    got = buf[1:].view(m, n_out)
+    ikv.gemm_nt(w, x, out=got)
+    assert torch.equal(got, want)
+    got.copy_(dev_t(r, dev))
+    ikv.gemm_nt(w, x, out=got, residual=got)
+    assert torch.equal(got, want_r)
+
+
 def gemm_plan(n_out, k, m):
     import ctypes
     tile, split = ctypes.c_int(), ctypes.c_int()
