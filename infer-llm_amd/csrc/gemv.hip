@@ -420,6 +420,8 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_kernel(const float *
 bool skinny_ok(int64_t n_out, int64_t k, int64_t m, std::initializer_list<const void *> ptrs) {
   if (m < 2 || m > kSkinnyMaxM || n_out % 16 != 0 || k % (2 * kSkinnyCols * kSkinnyWaves) != 0)
     return false;
+  if (k > INT_MAX / (16 * 4)) return false;  // 16 rows of k floats: one buffer range
+
   for (const void *p : ptrs)
     if (p && !ikv::aligned16(p)) return false;
   return true;
