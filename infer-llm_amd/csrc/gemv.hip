@@ -318,32 +318,36 @@ constexpr int kSkinnyMaxM = 64;
 constexpr int kSkinnyWaves = 8;
 constexpr int kSkinnyCols = 64;  // k columns per step
 
+// MT token tiles of 16 per workgroup: the 16 weight rows of a step are staged
+// once and multiplied into MT accumulators (one weight read per 16 * MT
+// tokens; MT = 2 fits 112 KB of LDS with 8 wavefronts).
+template <int MT>
 __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_kernel(const float *__restrict__ w,
                                                                    const float *__restrict__ x,
                                                                    float *out, const float *residual,
                                                                    int n_out, int k, int m, int n_tiles) {
-  __shared__ __attribute__((aligned(16))) float s_tile[kSkinnyWaves][2][16][kSkinnyCols];
-  __shared__ float s_red[kSkinnyWaves][64][4];
+  __shared__ __attribute__((aligned(16))) float s_tile[kSkinnyWaves][1 + MT][16][kSkinnyCols];
+  __shared__ float s_red[MT][kSkinnyWaves][64][4];
   const int nt = blockIdx.x % n_tiles;
   const int mt = blockIdx.x / n_tiles;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int j = lane & 15;
   const int kk = lane >> 4;
-  const int n0 = nt * 16, m0 = mt * 16;
+  const int n0 = nt * 16, m0 = mt * 16 * MT;
   const int kw = k / kSkinnyWaves;  // a multiple of 2 * kSkinnyCols
   const int kb0 = wave * kw;
   const int n_steps = kw / kSkinnyCols;
   // staging: instruction i reads rows 4i + lane / 16, 16-byte column lane % 16,
-  // through a buffer resource over the 16 w rows and one over the tile's
-  // x rows (rows past m read zeros; their outputs are not stored): a fixed
-  // byte offset per instruction and the step's column offset as the scalar
-  // offset, so the loop issues no address arithmetic
+  // through a buffer resource over the 16 w rows and one over the
+  // workgroup's x rows (rows past m read zeros; their outputs are not
+  // stored): a fixed byte offset per instruction and the step's column
+  // offset as the scalar offset, so the loop issues no address arithmetic
   const int sc = lane & 15;
   const __amdgpu_buffer_rsrc_t rsw = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<float *>(w + static_cast<size_t>(n0) * k), 0, 16 * k * 4, ikv::kBufWord3);
   const __amdgpu_buffer_rsrc_t rsx = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<float *>(x + static_cast<size_t>(m0) * k), 0, min(16, m - m0) * k * 4,
+      const_cast<float *>(x + static_cast<size_t>(m0) * k), 0, min(16 * MT, m - m0) * k * 4,
       ikv::kBufWord3);
   unsigned voff[4];
 #pragma unroll
@@ -351,20 +355,25 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_kernel(const float *
     const int r = 4 * i + (lane >> 4);
     voff[i] = static_cast<unsigned>((r * k + kb0 + 4 * sc) * 4);
   }
+  const unsigned tile_bytes = static_cast<unsigned>(16 * k * 4);  // one token tile of x
   float(*tw)[kSkinnyCols] = s_tile[wave][0];
-  float(*tx)[kSkinnyCols] = s_tile[wave][1];
-  floatx4 rw0[4], rx0[4], rw1[4], rx1[4];  // two steps in flight
-  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-  auto load_step = [&](floatx4 (&rw)[4], floatx4 (&rx)[4], int step) __attribute__((always_inline)) {
+  floatx4 rw0[4], rx0[MT][4], rw1[4], rx1[MT][4];  // two steps in flight
+  floatx4 acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+  auto load_step = [&](floatx4 (&rw)[4], floatx4 (&rx)[MT][4], int step) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       rw[i] = __builtin_amdgcn_raw_buffer_load_b128(rsw, voff[i], kSkinnyCols * step * 4, 0);
-      rx[i] = __builtin_amdgcn_raw_buffer_load_b128(rsx, voff[i], kSkinnyCols * step * 4, 0);
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+        rx[t][i] = __builtin_amdgcn_raw_buffer_load_b128(rsx, voff[i] + t * tile_bytes,
+                                                         kSkinnyCols * step * 4, 0);
     }
   };
   // store a register set as the current step, refill it with step `next`
   // (if any), then multiply the step out of LDS
-  auto body = [&](floatx4 (&rw)[4], floatx4 (&rx)[4], int next) __attribute__((always_inline)) {
+  auto body = [&](floatx4 (&rw)[4], floatx4 (&rx)[MT][4], int next) __attribute__((always_inline)) {
     // each register set is refilled right after its LDS write, in the
     // order it was loaded
 #pragma unroll
@@ -373,20 +382,27 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_kernel(const float *
       *reinterpret_cast<floatx4 *>(&tw[r][4 * (sc ^ r)]) = rw[i];
       if (next >= 0)
         rw[i] = __builtin_amdgcn_raw_buffer_load_b128(rsw, voff[i], kSkinnyCols * next * 4, 0);
-      *reinterpret_cast<floatx4 *>(&tx[r][4 * (sc ^ r)]) = rx[i];
-      if (next >= 0)
-        rx[i] = __builtin_amdgcn_raw_buffer_load_b128(rsx, voff[i], kSkinnyCols * next * 4, 0);
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        *reinterpret_cast<floatx4 *>(&s_tile[wave][1 + t][r][4 * (sc ^ r)]) = rx[t][i];
+        if (next >= 0)
+          rx[t][i] = __builtin_amdgcn_raw_buffer_load_b128(rsx, voff[i] + t * tile_bytes,
+                                                           kSkinnyCols * next * 4, 0);
+      }
     }
     __builtin_amdgcn_sched_barrier(0);  // the refill stays ahead of this step's reads and MFMAs
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int slot = (4 * u + kk) ^ j;
       const floatx4 a = *reinterpret_cast<const floatx4 *>(&tw[j][4 * slot]);
-      const floatx4 c = *reinterpret_cast<const floatx4 *>(&tx[j][4 * slot]);
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[0], c[0], acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[1], c[1], acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[2], c[2], acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[3], c[3], acc, 0, 0, 0);
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        const floatx4 c = *reinterpret_cast<const floatx4 *>(&s_tile[wave][1 + t][j][4 * slot]);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[0], c[0], acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[1], c[1], acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[2], c[2], acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[3], c[3], acc[t], 0, 0, 0);
+      }
     }
   };
   load_step(rw0, rx0, 0);
@@ -397,22 +413,28 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_kernel(const float *
   }
   body(rw0, rx0, -1);
   body(rw1, rx1, -1);
-  // lane l, register r: w row n0 + 4 (l / 16) + r, token m0 + l % 16
+  // lane l, register r of acc[t]: w row n0 + 4 (l / 16) + r, token
+  // m0 + 16 t + l % 16
 #pragma unroll
-  for (int r = 0; r < 4; ++r) s_red[wave][lane][r] = acc[r];
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s_red[t][wave][lane][r] = acc[t][r];
   __syncthreads();
   if (threadIdx.x < 256) {
     const int l = threadIdx.x >> 2;
     const int r = threadIdx.x & 3;
-    const int t = m0 + (l & 15);
     const int n = n0 + 4 * (l >> 4) + r;
-    float v = s_red[0][l][r];
 #pragma unroll
-    for (int q = 1; q < kSkinnyWaves; ++q) v += s_red[q][l][r];
-    if (t < m) {
-      const size_t o = static_cast<size_t>(t) * n_out + n;
-      if (residual) v += residual[o];
-      out[o] = v;
+    for (int t = 0; t < MT; ++t) {
+      const int tok = m0 + 16 * t + (l & 15);
+      float v = s_red[t][0][l][r];
+#pragma unroll
+      for (int q = 1; q < kSkinnyWaves; ++q) v += s_red[t][q][l][r];
+      if (tok < m) {
+        const size_t o = static_cast<size_t>(tok) * n_out + n;
+        if (residual) v += residual[o];
+        out[o] = v;
+      }
     }
   }
 }
@@ -420,7 +442,7 @@ __global__ __launch_bounds__(kSkinnyWaves * 64) void skinny_kernel(const float *
 bool skinny_ok(int64_t n_out, int64_t k, int64_t m, std::initializer_list<const void *> ptrs) {
   if (m < 2 || m > kSkinnyMaxM || n_out % 16 != 0 || k % (2 * kSkinnyCols * kSkinnyWaves) != 0)
     return false;
-  if (k > INT_MAX / (16 * 4)) return false;  // 16 rows of k floats: one buffer range
+  if (k > INT_MAX / (32 * 4)) return false;  // 32 rows of k floats: one buffer range
 
   for (const void *p : ptrs)
     if (p && !ikv::aligned16(p)) return false;
@@ -458,9 +480,21 @@ extern "C" int ikv_mul_mat_f32(const float *w, const float *x, float *out, int64
   }
   if (skinny_ok(n_out, k, m, {w, x})) {
     const int n_tiles = static_cast<int>(n_out / 16);
-    const int m_tiles = static_cast<int>((m + 15) / 16);
-    skinny_kernel<<<n_tiles * m_tiles, kSkinnyWaves * 64, 0, s>>>(w, x, out, residual, int(n_out),
-                                                                  int(k), int(m), n_tiles);
+    // 17-64 tokens over 256+ weight tiles (one workgroup per CU even with
+    // two token tiles each): two token tiles per workgroup, each weight step
+    // staged once per 32 tokens (Qwen3-8B q and down at 32 tokens 21.2 ->
+    // 16.6 and 57.5 -> 37.1 us). Fewer weight tiles keep one token tile per
+    // workgroup, for the workgroup count (the 0.6B o projection at 32
+    // tokens: 5.7 us with one, 8.5 with two).
+    if (m > 16 && n_tiles >= 256) {
+      const int m_pairs = static_cast<int>((m + 31) / 32);
+      skinny_kernel<2><<<n_tiles * m_pairs, kSkinnyWaves * 64, 0, s>>>(
+          w, x, out, residual, int(n_out), int(k), int(m), n_tiles);
+    } else {
+      const int m_tiles = static_cast<int>((m + 15) / 16);
+      skinny_kernel<1><<<n_tiles * m_tiles, kSkinnyWaves * 64, 0, s>>>(
+          w, x, out, residual, int(n_out), int(k), int(m), n_tiles);
+    }
     return ikv::launch_status();
   }
   if (ikv::gemm_nt_supported(n_out, k, m) && ikv::aligned16(w) && ikv::aligned16(x))

@@ -51,6 +51,7 @@ def test_gemv_matches_oracle(dev, oracle_pool, n_out, k):
                                         (16, 256, 2), (4096, 4096, 17), (1024, 2048, 65),
                                         (2048, 1024, 300), (3072, 1024, 2048), (1024, 3072, 129),
                                         (4096, 4096, 100), (192, 64, 70), (300, 200, 100),
+                                        (4096, 1024, 64), (4096, 2048, 40),  # two token tiles per workgroup
                                         (96, 200, 2100), (1024, 1024, 1000), (4096, 1024, 512)])
 def test_mul_mat_multi_token_matches_oracle(dev, oracle_pool, n_out, k, m):
     w = synth.normal(300 + m, (n_out, k), 0.02)
