@@ -728,7 +728,8 @@ __device__ __forceinline__ void decode_body(
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const int t = base + r * (NWAVE * 2) + wave * 2 + half;
-        const float d = ikv::half_wave_sum(ikv::dot4(qv[h], kr[r]));
+        const float dq = ikv::dot4(qv[h], kr[r]);
+        const float d = G <= 2 ? ikv::half_wave_sum_valu(dq) : ikv::half_wave_sum(dq);
         sc[r] = (t < t_end) ? d * scale_log2 : -INFINITY;
       }
       float mx = m[h];

@@ -48,6 +48,20 @@ __device__ __forceinline__ float half_wave_sum(float v) {
   v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
   return v;
 }
+// The same sum (the same bits: the last step adds the same two values)
+// with the last step on the VALU (v_permlane16_swap) instead of the LDS
+// pipe: shorter latency, one more VALU op. Faster in the decode with 2 query
+// heads per KV head (ctx 1024 6.76 -> 6.66 us), slower with 4 (ctx 4096
+// 11.37 -> 11.46 us), whose scores already keep the VALU busy.
+__device__ __forceinline__ float half_wave_sum_valu(float v) {
+  v += dpp<kDppXor1>(v);
+  v += dpp<kDppXor2>(v);
+  v += dpp<kDppHalfMirror>(v);
+  v += dpp<kDppMirror>(v);
+  const auto b =
+      __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
 
 // The values of x in lanes i % 32 (.x) and 32 + i % 32 (.y), in every lane i:
 // one v_permlane32_swap (lanes 32..63 of a copy trade places with lanes
