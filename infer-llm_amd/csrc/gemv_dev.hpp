@@ -18,9 +18,16 @@ __device__ __forceinline__ float4 nt_load4(const float *p) {
   return make_float4(v.x, v.y, v.z, v.w);
 }
 
+// Sum over the 64 lanes, every lane getting it: the half-wave sums end on
+// v_permlane16_swap and the halves meet on v_permlane32_swap, all on the
+// VALU (an LDS-pipe swizzle and bpermute had two round trips of latency at
+// the end of every row); the same adds of the same values as the index-
+// order tree, so the same bits.
 __device__ __forceinline__ float wave_sum64(float v) {
-  v = ikv::half_wave_sum(v);
-  return v + __shfl_xor(v, 32, 64);
+  v = ikv::half_wave_sum_valu(v);
+  const auto a =
+      __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(a[0]) + __uint_as_float(a[1]);
 }
 
 // x[k] * scale * nw[k] for a float4 of x: the standalone RMSNorm's
