@@ -450,8 +450,7 @@ __device__ __forceinline__ void qk_prologue(const Prologue &pro, ProStage<G> &st
       part += static_cast<double>(b);
       part += static_cast<double>(e);
       part += static_cast<double>(f);
-#pragma unroll
-      for (int o = 16; o > 0; o >>= 1) part += __shfl_xor(part, o, 64);
+      part = ikv::half_wave_sum_f64(part);
       float sc = 0.f;
       const bool certain = ikv::certified_rms_scale(part, D, pro.eps, (D - 1) + 8, sc);
       if (c == 0) scl[r] = certain ? sc : ikv::ordered_rms_scale(&s[r][0], D, pro.eps);

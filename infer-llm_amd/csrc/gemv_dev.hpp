@@ -61,7 +61,7 @@ __device__ __forceinline__ float rms_scale_from_first(const float4 (&first)[kBat
     s += static_cast<double>(c);
     s += static_cast<double>(d);
   }
-  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+  s = ikv::wave_sum_f64(s);
   return ikv::certified_or_ordered_scale(s, reinterpret_cast<const float *>(row), dim, eps,
                                          (dim - 1) + dim / 64 + 5, lane);
 }

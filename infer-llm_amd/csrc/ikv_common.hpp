@@ -72,6 +72,38 @@ __device__ __forceinline__ float2 halves(float x) {
   return make_float2(__uint_as_float(a[0]), __uint_as_float(a[1]));
 }
 
+// Double sums over the lanes of a half-wave / wave on the DPP network and
+// the VALU lane swaps (no LDS round trip): the same tree as half_wave_sum
+// (pairs, quads, 8, 16, 32 and, for the wave, 64 lanes), each step adding
+// the same two values in both partner lanes, so every lane gets the same
+// bits.
+template <int CTRL>
+__device__ __forceinline__ double dpp64(double v) {
+  const int2 u = __builtin_bit_cast(int2, v);
+  const int lo = __builtin_amdgcn_mov_dpp(u.x, CTRL, 0xF, 0xF, false);
+  const int hi = __builtin_amdgcn_mov_dpp(u.y, CTRL, 0xF, 0xF, false);
+  return __builtin_bit_cast(double, make_int2(lo, hi));
+}
+__device__ __forceinline__ double half_wave_sum_f64(double v) {
+  v += dpp64<kDppXor1>(v);
+  v += dpp64<kDppXor2>(v);
+  v += dpp64<kDppHalfMirror>(v);
+  v += dpp64<kDppMirror>(v);
+  const uint2 u = __builtin_bit_cast(uint2, v);
+  const auto lo = __builtin_amdgcn_permlane16_swap(u.x, u.x, false, false);
+  const auto hi = __builtin_amdgcn_permlane16_swap(u.y, u.y, false, false);
+  return __builtin_bit_cast(double, make_uint2(lo[0], hi[0])) +
+         __builtin_bit_cast(double, make_uint2(lo[1], hi[1]));
+}
+__device__ __forceinline__ double wave_sum_f64(double v) {
+  v = half_wave_sum_f64(v);
+  const uint2 u = __builtin_bit_cast(uint2, v);
+  const auto lo = __builtin_amdgcn_permlane32_swap(u.x, u.x, false, false);
+  const auto hi = __builtin_amdgcn_permlane32_swap(u.y, u.y, false, false);
+  return __builtin_bit_cast(double, make_uint2(lo[0], hi[0])) +
+         __builtin_bit_cast(double, make_uint2(lo[1], hi[1]));
+}
+
 __device__ __forceinline__ float wave_max(float v) {
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
   return v;
@@ -160,7 +192,7 @@ __device__ __forceinline__ float certified_or_ordered_scale(double s_any, const 
 // (dim % 256 == 0, row 16-byte aligned) for one wavefront, equal to the
 // reference's bit for bit: lane l adds in double the float squares of
 // elements 256*j + 4*l + c (j ascending, c = 0..3), the 64 lane sums combine
-// in a xor butterfly (32, 16, ..., 1; every lane gets the same bits), and the
+// in wave_sum_f64's tree (every lane gets the same bits), and the
 // scale is certified against the index-order sum (certified_rms_scale); when
 // it is not certain, lane 0 sums the row in index order (about 9 us for 1024
 // floats; rare) and every lane takes that.
@@ -175,7 +207,7 @@ __device__ __forceinline__ float rms_scale_strided(const float4 *row, int dim, f
     s += static_cast<double>(c);
     s += static_cast<double>(d);
   }
-  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+  s = wave_sum_f64(s);
   return certified_or_ordered_scale(s, reinterpret_cast<const float *>(row), dim, eps,
                                     (dim - 1) + dim / 64 + 5, lane);
 }

@@ -184,8 +184,7 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(const float *__restric
         const float sq = xv * xv;
         part += static_cast<double>(sq);
       }
-#pragma unroll
-      for (int o = 16; o > 0; o >>= 1) part += __shfl_xor(part, o, 64);
+      part = ikv::half_wave_sum_f64(part);
       float sc = 0.f;
       const bool certain =
           ikv::certified_rms_scale(part, dim, eps, (dim - 1) + (dim + 31) / 32 + 4, sc);
